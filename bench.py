@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""I2_S ternary GEMV throughput on one MI355X.
+
+Workload (one "step"): the BitNet-2B FFN GEMVs at batch 1 over 32 distinct,
+independently seeded weight sets -- per set, gate and up (6912 x 2560) share
+one int8-quantised activation, down (2560 x 6912) has its own. 424.7 MB of
+packed ternary weights, rotated every step, so HBM (not the 256 MB Infinity
+Cache) feeds them. A step is three launches on the library stream: the two
+per-token quantisers (32 rows of 2560 and 32 rows of 6912 f32 each) and one
+grouped GEMV over all 96 matrices with the epilogue fused. Inputs are
+resident in HBM before the timed region.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Prints ONE JSON line. `value` is algorithmic bytes per step / wall time per
+step. `roofline` is the grouped GEMV kernel alone, timed with HIP events on
+the stream it runs on. `cpu_baseline` is the reference's own CPU path
+(oracle/_ref, built from its sources) or the oracle's restatement of it,
+timed on this host over a bounded sample of the same workload.
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "I2_S GEMV achieved HBM GB/s (% of peak) + 2B-shape decode tokens/s, batch 1"
+PEAK_HBM_GBS = 8000.0
+SETS = 32
+K_UP, N_FF = 2560, 6912
+SHAPES = [("gate", N_FF, K_UP), ("up", N_FF, K_UP), ("down", K_UP, N_FF)]
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location("saphira_llm_amd", os.path.join(ROOT, "saphira-llm_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["saphira_llm_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """Config: BitNet-2B FFN GEMVs, batch 1, 32 rotated weight sets."""
+
+    def __init__(self, amd, dev, sets=SETS):
+        self.amd, self.dev, self.sets = amd, dev, sets
+        t0 = time.perf_counter()
+        self.host_w = []          # per set: [gate, up, down] packed bytes (kept for the CPU leg)
+        self.bufs = []
+        jobs = []
+        x_up = np.stack([amd.synth_normal(amd.synth_seed(1, s, 0, 100), K_UP) for s in range(sets)])
+        x_dn = np.stack([amd.synth_normal(amd.synth_seed(1, s, 0, 101), N_FF) for s in range(sets)])
+        self.x_up, self.x_dn = x_up, x_dn
+        self.b_xup, self.b_xdn = dev.put(x_up), dev.put(x_dn)
+        self.b_qup, self.b_qdn = dev.alloc(sets * K_UP), dev.alloc(sets * N_FF)
+        self.b_aup, self.b_adn = dev.alloc(8 * sets), dev.alloc(8 * sets)
+        self.b_y = []
+        w_bytes = 0
+        out_elems = 0
+        for s in range(sets):
+            ws = []
+            for m, (name, n_rows, n) in enumerate(SHAPES):
+                w = amd.synth_i2s(amd.synth_seed(1, s, 0, m), n_rows, n)
+                ws.append(w)
+                bw = dev.put(w)
+                by = dev.alloc(4 * n_rows)
+                self.bufs += [bw, by]
+                self.b_y.append(by)
+                if n == K_UP:
+                    q, a = self.b_qup.at(s * K_UP), self.b_aup.at(8 * s)
+                else:
+                    q, a = self.b_qdn.at(s * N_FF), self.b_adn.at(8 * s)
+                jobs.append(amd.GemvJob(bw.ptr, n_rows, n, q.value, a.value, by.ptr, None))
+                w_bytes += n_rows * n // 4 + 4          # codes + the f32 scale
+                out_elems += n_rows
+            self.host_w.append(ws)
+        self.jobs = jobs
+        self.plan = dev.plan(jobs)
+        # algorithmic bytes
+        self.weight_bytes = w_bytes
+        act_in = sets * (K_UP + N_FF)                   # distinct activation vectors (gate/up share)
+        self.step_bytes = w_bytes + 4 * act_in + 4 * out_elems          # f32 in, f32 out
+        self.gemv_bytes = w_bytes + (act_in + 8 * 2 * sets) + 4 * out_elems  # int8 q + act in, f32 out
+        self.ops = sum(2 * n_rows * n for _, n_rows, n in SHAPES) * sets
+        log(f"workload ready in {time.perf_counter() - t0:.1f}s: {len(jobs)} GEMVs, "
+            f"{w_bytes / 1e6:.1f} MB weights")
+
+    def step(self, ev=None):
+        d = self.dev
+        d.quant_act(self.b_xup.vp, K_UP, self.sets, self.b_qup.vp, self.b_aup.vp)
+        d.quant_act(self.b_xdn.vp, N_FF, self.sets, self.b_qdn.vp, self.b_adn.vp)
+        if ev is not None:
+            d.record(ev)
+        d.plan_run(self.plan)
+        if ev is not None:
+            d.record(ev + 1)
+
+    def check_against_oracle(self, orc, set_idx=0):
+        """Spot-check one set's outputs (parity is the tests' job; this guards
+        the timed configuration itself)."""
+        s = set_idx
+        ws = self.host_w[s]
+        for m, (name, n_rows, n) in enumerate(SHAPES):
+            x = self.x_up[s] if n == K_UP else self.x_dn[s]
+            want = orc.linear(ws[m], n_rows, n, x, orc.DOT_VNNI)[0]
+            got = self.b_y[3 * s + m].download(np.float32, n_rows)
+            if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+                raise SystemExit(f"bench: output mismatch against the oracle in set {s} {name}")
+
+
+def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
+    """Plain device copy and read-only checksum of known size: the achievable
+    HBM figure beside the GEMV."""
+    src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
+    part = dev.alloc(4 * 2048)
+    dev.copy(dst.vp, src.vp, nbytes)
+    dev.checksum(src.vp, nbytes, part.vp, 2048)
+    dev.sync()
+    dev.timer_start()
+    for _ in range(reps):
+        dev.copy(dst.vp, src.vp, nbytes)
+    copy_ms = dev.timer_stop() / reps
+    dev.timer_start()
+    for _ in range(reps):
+        dev.checksum(src.vp, nbytes, part.vp, 2048)
+    read_ms = dev.timer_stop() / reps
+    for b in (src, dst, part):
+        b.free()
+    return {"copy_GBps": round(2 * nbytes / copy_ms / 1e6, 1),
+            "read_GBps": round(nbytes / read_ms / 1e6, 1), "bytes": nbytes}
+
+
+def cpu_baseline(wl, seconds=6.0):
+    """The reference's CPU path (or the oracle's restatement) over a bounded
+    sample of the same workload: repeated passes over the 32 sets, each pass
+    quantise -> GEMV -> epilogue for gate/up/down, row-parallel with the
+    reference's split policy (src/forward.c:145-205)."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    use_ref = orc.ref_available()
+    try:
+        threads = min(16, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        threads = min(16, os.cpu_count() or 1)
+    Act = orc.Act
+    q_up, q_dn = np.empty(K_UP, np.int8), np.empty(N_FF, np.int8)
+    dots = np.empty(N_FF, np.int32)
+    y = np.empty(N_FF, np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    results = {}
+    for nt in sorted({1, threads}):
+        if use_ref:
+            r = orc.ref()
+            r.sllm_i2s_select_auto()
+            pool = r.ref_pool_create(nt)
+            quant = r.sllm_i2s_quant_act
+            run = lambda w, n_rows, n, q, a: r.ref_gemv_epilogue(pool, P(w), n_rows, n, P(q), ctypes.byref(a), P(dots), P(y))
+        else:
+            o = orc.orc()
+            pool = o.orc_pool_create(nt)
+            path = orc.DOT_VNNI if o.orc_vnni_supported() else orc.DOT_V3
+            quant = o.orc_quant_act
+            run = lambda w, n_rows, n, q, a: o.orc_gemv_epilogue_parallel(pool, P(w), n_rows, n, P(q), ctypes.byref(a), P(dots), P(y), path)
+        a_up, a_dn = Act(), Act()
+        passes, sets_done = 0, 0
+        t0 = time.perf_counter()
+        while True:
+            for s in range(wl.sets):
+                ws = wl.host_w[s]
+                quant(P(wl.x_up[s]), K_UP, P(q_up), ctypes.byref(a_up))
+                run(ws[0], N_FF, K_UP, q_up, a_up)
+                run(ws[1], N_FF, K_UP, q_up, a_up)
+                quant(P(wl.x_dn[s]), N_FF, P(q_dn), ctypes.byref(a_dn))
+                run(ws[2], K_UP, N_FF, q_dn, a_dn)
+                sets_done += 1
+                if time.perf_counter() - t0 > seconds:
+                    break
+            else:
+                passes += 1
+                continue
+            break
+        dt = time.perf_counter() - t0
+        if use_ref:
+            r.sllm_pool_destroy(pool)
+            isa = {0: "v3", 1: "vnni"}.get(r.sllm_i2s_dot_isa(), "other")
+        else:
+            orc.orc().orc_pool_destroy(pool)
+            isa = "vnni" if orc.orc().orc_vnni_supported() else "v3"
+        per_set = wl.step_bytes / wl.sets
+        results[nt] = {"GBps": sets_done * per_set / dt / 1e9, "sets": sets_done, "seconds": dt, "dot": isa}
+    best = results[threads]
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(best["GBps"], 3), "unit": "GB/s", "cores": threads,
+        "kind": "reference" if use_ref else "port",
+        "sample": (f"{best['sets']} FFN sets (gate+up+down, quantise+GEMV+epilogue) cycling over the "
+                   f"same {wl.sets} weight sets in {best['seconds']:.1f}s, {threads} threads, "
+                   f"dot={best['dot']}"),
+        "one_thread_GBps": round(results[1]["GBps"], 3),
+        "host": {"cpu": cpu_model, "nproc": os.cpu_count()},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the I2_S GEMV path runs on a single MI355X and "
+              "this build has no multi-GPU path (--gpus must be 1).", file=sys.stderr)
+        sys.exit(2)
+
+    amd = load_package()
+    dev = amd.Device(0)
+    log(f"device {dev.name}, {dev.cu} CUs, {dev.hbm / 2**30:.0f} GiB")
+    wl = Workload(amd, dev)
+
+    for _ in range(args.warmup):
+        wl.step()
+    dev.sync()
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle import oracle as orc
+        wl.check_against_oracle(orc, 0)
+        wl.check_against_oracle(orc, wl.sets - 1)
+        log("outputs of sets 0 and 31 match the oracle bit for bit")
+
+    K = args.steps
+    dev.events(2 * K)
+    dev.sync()
+    t0 = time.perf_counter()
+    for i in range(K):
+        wl.step(ev=2 * i)
+    dev.sync()
+    t1 = time.perf_counter()
+    gemv_ms = [dev.elapsed(2 * i, 2 * i + 1) for i in range(K)]
+    ms_per_step = (t1 - t0) * 1e3 / K
+    value = wl.step_bytes / (ms_per_step * 1e-3) / 1e9
+    gemv_avg = float(np.mean(gemv_ms))
+    achieved = wl.gemv_bytes / (gemv_avg * 1e-3) / 1e9
+    log(f"step {ms_per_step * 1e3:.1f} us, grouped GEMV {gemv_avg * 1e3:.1f} us "
+        f"(min {min(gemv_ms) * 1e3:.1f}), {achieved:.0f} GB/s")
+
+    calib = measure_copy_bandwidth(dev)
+    log(f"calibration: copy {calib['copy_GBps']} GB/s, read {calib['read_GBps']} GB/s")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemv_config1_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {
+            "workload": "BitNet-2B FFN GEMVs batch 1: gate+up 6912x2560 (shared activation) and "
+                        "down 2560x6912, 32 independently seeded I2_S weight sets rotated per step "
+                        "(424.7 MB packed), f32 N(0,1) activations int8-absmax quantised per token, "
+                        "f32 outputs",
+            "sets": SETS, "weight_bytes": wl.weight_bytes, "step_bytes": wl.step_bytes,
+            "launches_per_step": 3, "hbm_frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+            "tops": round(wl.ops / (ms_per_step * 1e-3) / 1e12, 3),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "kernel": "sllm_k_gemv_group (96 GEMVs, one launch)",
+            "avg_launch_us": round(gemv_avg * 1e3, 2), "bytes_per_launch": wl.gemv_bytes,
+        },
+        "calibration": calib,
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,200 @@
+/*
+ * sllm_gfx950.h -- C ABI of the MI355X (gfx950) I2_S ternary kernel row.
+ *
+ * libsllm_gfx950.so is C11 host code that reaches HIP only through a thin
+ * shim (hipModuleLoadData / hipModuleLaunchKernel on an embedded gfx950 code
+ * object, plus device buffers). No torch, no C++ types cross this boundary:
+ * plain pointers, sizes and int status codes.
+ *
+ * Two layers:
+ *
+ *  1. The kernel-row functions sllm_gfx950_i2s_* keep the exact signatures
+ *     and semantics of the reference's kernel layer
+ *     (include/saphira_llm/i2s_gemm.h:57-95) on HOST pointers, so the row can
+ *     be installed behind the reference's kernel dispatch without touching its
+ *     callers (src/forward.c:190-205, :651-793). Weights are looked up in a
+ *     registry of tensors uploaded byte-for-byte at load time.
+ *
+ *  2. The device functions sllm_gfx950_* (no i2s_ infix) take DEVICE pointers,
+ *     enqueue on the library's stream and return a status. This is the path a
+ *     device-resident forward pass uses; the quantiser, GEMV and epilogue can
+ *     be fused and several independent GEMVs share one launch.
+ *
+ * Packed I2_S tensors are the on-disk bytes unchanged: N rows of K/4 bytes in
+ * the transposed 128-element tile layout, then a 32-byte tail whose first
+ * four bytes are the f32 per-tensor scale (src/quant.c:72-106,
+ * src/gguf.c:268-282). K must be a multiple of 128 (src/forward.c:306-316).
+ *
+ * Errors: functions returning int return SLLM_GFX950_OK (0) or a negative
+ * status; sllm_gfx950_last_error() has the message. The void/int32 kernel-row
+ * functions mirror reference signatures that cannot return a status; on any
+ * failure (no device opened, unregistered weights, a HIP error) they print the
+ * reason to stderr and abort(). They never fall back to a CPU computation.
+ */
+#ifndef SAPHIRA_AMD_SLLM_GFX950_H
+#define SAPHIRA_AMD_SLLM_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. Codes the reference also has keep its sllm_status numbers
+ * (include/saphira_llm/status.h:26-56); the device codes are new. */
+enum {
+    SLLM_GFX950_OK                 = 0,
+    SLLM_GFX950_ERR_ARG            = -1,   /* SLLM_ERR_ARG                          */
+    SLLM_GFX950_ERR_NOMEM          = -2,   /* SLLM_ERR_NOMEM (host or device)       */
+    SLLM_GFX950_ERR_UNSUPPORTED    = -4,   /* SLLM_ERR_UNSUPPORTED                  */
+    SLLM_GFX950_ERR_TENSOR_SHAPE   = -34,  /* SLLM_ERR_TENSOR_SHAPE: K % 128 != 0   */
+    SLLM_GFX950_ERR_TOO_LARGE      = -36,  /* SLLM_ERR_TOO_LARGE: K above the limit */
+    SLLM_GFX950_ERR_NO_DEVICE      = -60,  /* no gfx950 device, or library not open */
+    SLLM_GFX950_ERR_HIP            = -61,  /* a HIP runtime call failed             */
+    SLLM_GFX950_ERR_NOT_REGISTERED = -62   /* host weights not in any registered tensor */
+};
+
+/* Elements per I2_S block (include/saphira_llm/i2s_gemm.h:25). */
+#define SLLM_GFX950_QK    128
+/* Largest K the GEMV stages in LDS (one int8 activation row). */
+#define SLLM_GFX950_MAX_K 65536
+
+/* Per-row activation metadata. Same layout as sllm_i2s_act
+ * (include/saphira_llm/i2s_gemm.h:37-40): 8 bytes, scale then sum. */
+typedef struct sllm_gfx950_act {
+    float   scale;   /* 127 / amax, or 0 for an all-zero row */
+    int32_t sum;     /* sum of the quantised values          */
+} sllm_gfx950_act;
+
+/* ------------------------------------------------------------------ */
+/* lifecycle                                                           */
+/* ------------------------------------------------------------------ */
+
+/* Open HIP device `device`, check it is gfx950, load the code object and
+ * create the library stream. Called once at model load, as the reference
+ * selects its kernel in sllm_model_load (src/forward.c:334). Idempotent. */
+int         sllm_gfx950_open(int device);
+void        sllm_gfx950_close(void);
+int         sllm_gfx950_is_open(void);
+const char *sllm_gfx950_status_string(int status);
+const char *sllm_gfx950_last_error(void);
+/* name: device marketing/arch name; cu: compute units; hbm: bytes of HBM */
+int         sllm_gfx950_device_info(char *name, size_t name_len, int *cu, size_t *hbm);
+
+/* ------------------------------------------------------------------ */
+/* device memory and the library stream                                */
+/* ------------------------------------------------------------------ */
+
+int   sllm_gfx950_malloc(void **dptr, size_t bytes);
+int   sllm_gfx950_free(void *dptr);
+int   sllm_gfx950_h2d(void *dst_dev, const void *src_host, size_t bytes);   /* synchronous */
+int   sllm_gfx950_d2h(void *dst_host, const void *src_dev, size_t bytes);   /* synchronous */
+int   sllm_gfx950_sync(void);           /* wait for the library stream */
+void *sllm_gfx950_stream(void);         /* the hipStream_t everything is enqueued on */
+/* Events recorded on the library stream around enqueued work. */
+int   sllm_gfx950_timer_start(void);
+int   sllm_gfx950_timer_stop(float *ms);   /* waits for the stop event */
+/* A numbered set of events on the library stream, for timing individual
+ * launches inside a longer run: reserve n, record any of them between
+ * launches, read the elapsed time between two (waits for the later one). */
+int   sllm_gfx950_events_reserve(int n);
+int   sllm_gfx950_event_record(int i);
+int   sllm_gfx950_event_elapsed(int i, int j, float *ms);
+
+/* Calibration kernels (no counterpart in the reference). A plain device
+ * copy and a read-only XOR checksum (n_partials workgroup partials) of known
+ * size: they measure the achievable HBM bandwidth beside the GEMV and scale
+ * the HBM byte counters. bytes must be a multiple of 16, pointers 16-byte
+ * aligned. */
+int   sllm_gfx950_copy(void *dst, const void *src, size_t bytes);
+int   sllm_gfx950_checksum(const void *src, size_t bytes, uint32_t *partials, uint32_t n_partials);
+
+/* ------------------------------------------------------------------ */
+/* device-pointer kernels (asynchronous, library stream)               */
+/* ------------------------------------------------------------------ */
+
+/* Replaces sllm_i2s_quant_act (include/saphira_llm/i2s_gemm.h:57-58,
+ * src/i2s_gemm.c:45-83) for n_tok consecutive rows of n floats:
+ * q[t*n + i], act[t]. Bit-exact with the reference. */
+int sllm_gfx950_quant_act(const float *x, size_t n, size_t n_tok,
+                          int8_t *q, sllm_gfx950_act *act);
+
+/* Replaces sllm_i2s_gemv (include/saphira_llm/i2s_gemm.h:81-82,
+ * src/i2s_gemm.c:260-269): rows_out[r] = sum_k code(r,k) * q[k], int32, for
+ * r < n_rows, where w points at row 0 of a packed tensor (or at any row
+ * boundary inside one). */
+int sllm_gfx950_gemv(const uint8_t *w, size_t n_rows, size_t n,
+                     const int8_t *q, int32_t *rows_out);
+
+/* The GEMV with the epilogue fused: out[r] = (float)(dot_r - act->sum) *
+ * (w_scale / act->scale), the grouping of src/i2s_gemm.c:271-290 as inlined at
+ * src/forward.c:653-655. w must be the whole tensor: w_scale is read from its
+ * tail at w + n_rows*n/4. */
+int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n,
+                              const int8_t *q, const sllm_gfx950_act *act,
+                              float *out);
+
+/* One projection as src/forward.c:651-655 performs it: quantise x (n floats)
+ * into q / act (device scratch the caller owns, so QKV or gate/up can share
+ * it), then the fused GEMV + epilogue into out (n_rows floats). */
+int sllm_gfx950_linear(const uint8_t *w, size_t n_rows, size_t n, const float *x,
+                       int8_t *q, sllm_gfx950_act *act, float *out);
+
+/* One independent GEMV of a batch. out and/or rows_out may be NULL (not
+ * both); act is needed when out is set. */
+typedef struct sllm_gfx950_gemv_job {
+    const uint8_t         *w;         /* whole packed tensor (device)      */
+    size_t                 n_rows;    /* N                                  */
+    size_t                 n;         /* K, multiple of 128                 */
+    const int8_t          *q;         /* K int8 (device)                    */
+    const sllm_gfx950_act *act;       /* device                             */
+    float                 *out;       /* N f32 epilogue output, or NULL     */
+    int32_t               *rows_out;  /* N int32 raw dots, or NULL          */
+} sllm_gfx950_gemv_job;
+
+/* Run independent GEMVs (e.g. Q, K and V against one activation, or many
+ * layers' matrices) in ONE launch. The job table is copied to the device on
+ * each call; use a plan to upload it once. */
+int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs);
+
+typedef struct sllm_gfx950_plan sllm_gfx950_plan;
+int  sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
+                             sllm_gfx950_plan **plan);
+int  sllm_gfx950_plan_run(const sllm_gfx950_plan *plan);
+void sllm_gfx950_plan_destroy(sllm_gfx950_plan *plan);
+
+/* Launch-shape override for tuning sweeps: lanes per row (4, 8 or 16),
+ * waves per workgroup (1..16) and rows per workgroup (a multiple of
+ * 64/lanes). 0 restores the automatic choice. Affects later launches only. */
+int sllm_gfx950_set_gemv_shape(int lanes_per_row, int waves, int rows_per_wg);
+
+/* ------------------------------------------------------------------ */
+/* host-pointer kernel row (the reference's signatures)                */
+/* ------------------------------------------------------------------ */
+
+/* Upload a packed I2_S tensor (n_rows*n/4 code bytes + 32-byte tail)
+ * byte-for-byte and remember it under its host address, so the kernel-row
+ * functions below can be handed the same borrowed pointers the reference's
+ * model holds (include/saphira_llm/forward.h:27-31). */
+int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n);
+int sllm_gfx950_tensor_unregister(const void *packed);
+/* The device copy of a registered host address (inside any tensor), or NULL. */
+const void *sllm_gfx950_tensor_device(const void *host);
+
+/* src/i2s_gemm.c:45-83 on the GPU. */
+void    sllm_gfx950_i2s_quant_act(const float *x, size_t n, int8_t *q_out,
+                                  sllm_gfx950_act *out);
+/* src/i2s_gemm.c:246-258: one row; 0 when w or q is NULL or n < 128. */
+int32_t sllm_gfx950_i2s_dot(const uint8_t *w, const int8_t *q, size_t n);
+/* src/i2s_gemm.c:260-269: w may be any row boundary inside a registered
+ * tensor (src/forward.c:190-194 passes w + begin*row_bytes). Returns without
+ * writing when w, q or rows_out is NULL. */
+void    sllm_gfx950_i2s_gemv(const uint8_t *w, size_t n_rows, size_t n,
+                             const int8_t *q, int32_t *rows_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAPHIRA_AMD_SLLM_GFX950_H */

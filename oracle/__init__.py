@@ -1,0 +1,1 @@
+"""The oracle package: test infrastructure only (see oracle.py)."""

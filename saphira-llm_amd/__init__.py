@@ -1,0 +1,311 @@
+"""ctypes bindings for libsllm_gfx950.so and libsllm_synth.so.
+
+The product is the C ABI in include/saphira_amd/*.h; this module is the
+plumbing the tests and bench.py use to reach it from Python. It holds no
+compute of its own: every kernel call goes through the shared library, and
+loading fails loudly (ImportError / GFX950Error) when the library is missing
+or the device cannot be opened.
+
+The directory name carries a hyphen, so load it by path::
+
+    spec = importlib.util.spec_from_file_location("saphira_llm_amd", ".../__init__.py")
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_size_t, c_uint, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsllm_gfx950.so")
+SYNTH_PATH = os.path.join(HERE, "libsllm_synth.so")
+
+QK = 128
+MAX_K = 65536
+STATUS = {
+    0: "ok", -1: "invalid-argument", -2: "out-of-memory", -4: "unsupported",
+    -34: "wrong-tensor-shape", -36: "exceeds-limit", -60: "no-gfx950-device",
+    -61: "hip-error", -62: "tensor-not-registered",
+}
+
+
+class Act(ctypes.Structure):
+    """sllm_gfx950_act: layout of the reference's sllm_i2s_act."""
+    _fields_ = [("scale", c_float), ("sum", c_int32)]
+
+
+class GemvJob(ctypes.Structure):
+    """sllm_gfx950_gemv_job."""
+    _fields_ = [("w", c_void_p), ("n_rows", c_size_t), ("n", c_size_t), ("q", c_void_p),
+                ("act", c_void_p), ("out", c_void_p), ("rows_out", c_void_p)]
+
+
+class KernelRow(ctypes.Structure):
+    """sllm_kernel_row."""
+    _fields_ = [("name", c_char_p), ("priority", c_int),
+                ("open", ctypes.CFUNCTYPE(c_int)),
+                ("quant_act", ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_void_p, c_void_p)),
+                ("dot", ctypes.CFUNCTYPE(c_int32, c_void_p, c_void_p, c_size_t)),
+                ("gemv", ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p))]
+
+
+# Every function the C ABI exports: name -> (restype, argtypes).
+PROTOTYPES = {
+    "sllm_gfx950_open": (c_int, [c_int]),
+    "sllm_gfx950_close": (None, []),
+    "sllm_gfx950_is_open": (c_int, []),
+    "sllm_gfx950_status_string": (c_char_p, [c_int]),
+    "sllm_gfx950_last_error": (c_char_p, []),
+    "sllm_gfx950_device_info": (c_int, [c_char_p, c_size_t, POINTER(c_int), POINTER(c_size_t)]),
+    "sllm_gfx950_malloc": (c_int, [POINTER(c_void_p), c_size_t]),
+    "sllm_gfx950_free": (c_int, [c_void_p]),
+    "sllm_gfx950_h2d": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "sllm_gfx950_d2h": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "sllm_gfx950_sync": (c_int, []),
+    "sllm_gfx950_stream": (c_void_p, []),
+    "sllm_gfx950_timer_start": (c_int, []),
+    "sllm_gfx950_timer_stop": (c_int, [POINTER(c_float)]),
+    "sllm_gfx950_events_reserve": (c_int, [c_int]),
+    "sllm_gfx950_event_record": (c_int, [c_int]),
+    "sllm_gfx950_event_elapsed": (c_int, [c_int, c_int, POINTER(c_float)]),
+    "sllm_gfx950_copy": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "sllm_gfx950_checksum": (c_int, [c_void_p, c_size_t, c_void_p, c_uint]),
+    "sllm_gfx950_quant_act": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "sllm_gfx950_gemv": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "sllm_gfx950_gemv_epilogue": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p]),
+    "sllm_gfx950_linear": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "sllm_gfx950_gemv_batch": (c_int, [POINTER(GemvJob), c_size_t]),
+    "sllm_gfx950_plan_create": (c_int, [POINTER(GemvJob), c_size_t, POINTER(c_void_p)]),
+    "sllm_gfx950_plan_run": (c_int, [c_void_p]),
+    "sllm_gfx950_plan_destroy": (None, [c_void_p]),
+    "sllm_gfx950_set_gemv_shape": (c_int, [c_int, c_int, c_int]),
+    "sllm_gfx950_tensor_register": (c_int, [c_void_p, c_size_t, c_size_t]),
+    "sllm_gfx950_tensor_unregister": (c_int, [c_void_p]),
+    "sllm_gfx950_tensor_device": (c_void_p, [c_void_p]),
+    "sllm_gfx950_i2s_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
+    "sllm_gfx950_i2s_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),
+    "sllm_gfx950_i2s_gemv": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "sllm_kdispatch_register": (c_int, [POINTER(KernelRow)]),
+    "sllm_kdispatch_count": (c_size_t, []),
+    "sllm_kdispatch_row": (POINTER(KernelRow), [c_size_t]),
+    "sllm_kdispatch_select": (c_int, [c_char_p]),
+    "sllm_kdispatch_installed": (POINTER(KernelRow), []),
+    "sllm_kdispatch_reset": (None, []),
+    "sllm_kdispatch_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
+    "sllm_kdispatch_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),
+    "sllm_kdispatch_gemv": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+}
+
+SYNTH_PROTOTYPES = {
+    "sllm_synth_seed": (c_uint64, [c_uint, c_uint, c_uint, c_uint]),
+    "sllm_synth_scale": (c_float, [c_uint64]),
+    "sllm_synth_codes": (None, [c_uint64, c_size_t, c_size_t, c_void_p]),
+    "sllm_synth_i2s": (c_int, [c_uint64, c_size_t, c_size_t, c_void_p, c_int]),
+    "sllm_synth_normal": (None, [c_uint64, c_size_t, c_void_p]),
+}
+
+_lib = None
+_synth = None
+
+
+def _bind(path, protos):
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built: run `make -C {HERE}` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in protos.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def lib():
+    """The loaded libsllm_gfx950.so with every prototype set."""
+    global _lib
+    if _lib is None:
+        _lib = _bind(LIB_PATH, PROTOTYPES)
+    return _lib
+
+
+def synth_lib():
+    global _synth
+    if _synth is None:
+        _synth = _bind(SYNTH_PATH, SYNTH_PROTOTYPES)
+    return _synth
+
+
+class GFX950Error(RuntimeError):
+    def __init__(self, status, where=""):
+        msg = lib().sllm_gfx950_last_error().decode(errors="replace")
+        super().__init__(f"{where}: {STATUS.get(status, status)} ({status}): {msg}")
+        self.status = status
+
+
+def check(status, where=""):
+    if status != 0:
+        raise GFX950Error(status, where)
+    return status
+
+
+def ptr(a):
+    """Host address of a contiguous numpy array."""
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# device handle
+# ---------------------------------------------------------------------------
+
+class DevBuf:
+    """A device allocation owned by the library (freed by free() or the Device)."""
+
+    def __init__(self, dev, nbytes):
+        self.dev = dev
+        self.nbytes = int(nbytes)
+        p = c_void_p()
+        check(lib().sllm_gfx950_malloc(ctypes.byref(p), self.nbytes), "malloc")
+        self.ptr = p.value
+
+    def at(self, offset):
+        return c_void_p(self.ptr + int(offset))
+
+    @property
+    def vp(self):
+        return c_void_p(self.ptr)
+
+    def upload(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        check(lib().sllm_gfx950_h2d(self.at(offset), ptr(arr), arr.nbytes), "h2d")
+
+    def download(self, dtype, count, offset=0):
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib().sllm_gfx950_d2h(ptr(out), self.at(offset), out.nbytes), "d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            check(lib().sllm_gfx950_free(c_void_p(self.ptr)), "free")
+            self.ptr = 0
+
+
+class Device:
+    """sllm_gfx950_open on `device`; raises GFX950Error when there is no gfx950."""
+
+    def __init__(self, device=0):
+        self.lib = lib()
+        check(self.lib.sllm_gfx950_open(device), "open")
+        name = ctypes.create_string_buffer(520)
+        cu, hbm = c_int(), c_size_t()
+        check(self.lib.sllm_gfx950_device_info(name, 520, ctypes.byref(cu), ctypes.byref(hbm)), "info")
+        self.name, self.cu, self.hbm = name.value.decode(), cu.value, hbm.value
+
+    def alloc(self, nbytes):
+        return DevBuf(self, nbytes)
+
+    def put(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = DevBuf(self, max(arr.nbytes, 1))
+        b.upload(arr)
+        return b
+
+    def sync(self):
+        check(self.lib.sllm_gfx950_sync(), "sync")
+
+    def timer_start(self):
+        check(self.lib.sllm_gfx950_timer_start(), "timer_start")
+
+    def timer_stop(self):
+        ms = c_float()
+        check(self.lib.sllm_gfx950_timer_stop(ctypes.byref(ms)), "timer_stop")
+        return ms.value
+
+    def events(self, n):
+        check(self.lib.sllm_gfx950_events_reserve(n), "events_reserve")
+
+    def record(self, i):
+        check(self.lib.sllm_gfx950_event_record(i), "event_record")
+
+    def elapsed(self, i, j):
+        ms = c_float()
+        check(self.lib.sllm_gfx950_event_elapsed(i, j, ctypes.byref(ms)), "event_elapsed")
+        return ms.value
+
+    def copy(self, dst, src, nbytes):
+        check(self.lib.sllm_gfx950_copy(dst, src, nbytes), "copy")
+
+    def checksum(self, src, nbytes, partials, n_partials):
+        check(self.lib.sllm_gfx950_checksum(src, nbytes, partials, n_partials), "checksum")
+
+    # device-pointer kernels -------------------------------------------------
+    def quant_act(self, x, n, n_tok, q, act):
+        check(self.lib.sllm_gfx950_quant_act(x, n, n_tok, q, act), "quant_act")
+
+    def gemv(self, w, n_rows, n, q, rows_out):
+        check(self.lib.sllm_gfx950_gemv(w, n_rows, n, q, rows_out), "gemv")
+
+    def gemv_epilogue(self, w, n_rows, n, q, act, out):
+        check(self.lib.sllm_gfx950_gemv_epilogue(w, n_rows, n, q, act, out), "gemv_epilogue")
+
+    def linear(self, w, n_rows, n, x, q, act, out):
+        check(self.lib.sllm_gfx950_linear(w, n_rows, n, x, q, act, out), "linear")
+
+    def gemv_batch(self, jobs):
+        arr = (GemvJob * len(jobs))(*jobs)
+        check(self.lib.sllm_gfx950_gemv_batch(arr, len(jobs)), "gemv_batch")
+
+    def plan(self, jobs):
+        arr = (GemvJob * len(jobs))(*jobs)
+        p = c_void_p()
+        check(self.lib.sllm_gfx950_plan_create(arr, len(jobs), ctypes.byref(p)), "plan_create")
+        return p
+
+    def plan_run(self, p):
+        check(self.lib.sllm_gfx950_plan_run(p), "plan_run")
+
+    def plan_destroy(self, p):
+        self.lib.sllm_gfx950_plan_destroy(p)
+
+    def set_gemv_shape(self, lanes_per_row=0, waves=0, rows_per_wg=0):
+        check(self.lib.sllm_gfx950_set_gemv_shape(lanes_per_row, waves, rows_per_wg), "set_gemv_shape")
+
+
+# ---------------------------------------------------------------------------
+# synthetic workloads
+# ---------------------------------------------------------------------------
+
+def synth_seed(cfg, set_=0, layer=0, matrix=0):
+    return synth_lib().sllm_synth_seed(cfg, set_, layer, matrix)
+
+
+def synth_scale(seed):
+    return np.float32(synth_lib().sllm_synth_scale(seed))
+
+
+def synth_codes(seed, n_rows, n):
+    out = np.empty(n_rows * n, dtype=np.uint8)
+    synth_lib().sllm_synth_codes(seed, n_rows, n, ptr(out))
+    return out.reshape(n_rows, n)
+
+
+def synth_i2s(seed, n_rows, n, threads=None, out=None):
+    """Packed tensor bytes (n_rows*n/4 + 32, uint8) for tensor `seed`."""
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    nbytes = n_rows * (n // 4) + 32
+    if out is None:
+        out = np.empty(nbytes, dtype=np.uint8)
+    assert out.nbytes == nbytes and out.dtype == np.uint8
+    if synth_lib().sllm_synth_i2s(seed, n_rows, n, ptr(out), threads) != 0:
+        raise ValueError(f"synth_i2s: bad shape {n_rows}x{n}")
+    return out
+
+
+def synth_normal(seed, count):
+    out = np.empty(count, dtype=np.float32)
+    synth_lib().sllm_synth_normal(seed, count, ptr(out))
+    return out
