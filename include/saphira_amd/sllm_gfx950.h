@@ -135,39 +135,61 @@ int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n,
                               const int8_t *q, const sllm_gfx950_act *act,
                               float *out);
 
-/* One projection as src/forward.c:651-655 performs it: quantise x (n floats)
- * into q / act (device scratch the caller owns, so QKV or gate/up can share
- * it), then the fused GEMV + epilogue into out (n_rows floats). */
+/* One projection as src/forward.c:651-655 performs it: quantise x (n
+ * floats), GEMV, epilogue into out (n_rows floats). q / act, when not NULL,
+ * receive the quantised row and its scale/sum (give both or neither). By
+ * default this is a quantiser launch then the GEMV; with fuse_quant set (see
+ * sllm_gfx950_set_tuning) the row-group kernel quantises x in LDS itself --
+ * the same operations, so the same bits -- in a single launch. */
 int sllm_gfx950_linear(const uint8_t *w, size_t n_rows, size_t n, const float *x,
                        int8_t *q, sllm_gfx950_act *act, float *out);
 
-/* One independent GEMV of a batch. out and/or rows_out may be NULL (not
- * both); act is needed when out is set. */
+/* One independent GEMV of a batch.
+ *   x != NULL: x is quantised per token (as sllm_gfx950_linear); q / act
+ *              are optional outputs (both or neither). Jobs sharing one x
+ *              (Q/K/V, gate/up) share one quantisation.
+ *   x == NULL: q / act are inputs (act only needed for out).
+ * out and/or rows_out may be NULL, not both. Device pointers, 16-byte
+ * aligned. */
 typedef struct sllm_gfx950_gemv_job {
-    const uint8_t         *w;         /* whole packed tensor (device)      */
-    size_t                 n_rows;    /* N                                  */
-    size_t                 n;         /* K, multiple of 128                 */
-    const int8_t          *q;         /* K int8 (device)                    */
-    const sllm_gfx950_act *act;       /* device                             */
-    float                 *out;       /* N f32 epilogue output, or NULL     */
-    int32_t               *rows_out;  /* N int32 raw dots, or NULL          */
+    const uint8_t   *w;         /* whole packed tensor (codes + tail)    */
+    size_t           n_rows;    /* N                                     */
+    size_t           n;         /* K, multiple of 128                    */
+    const float     *x;         /* K f32, or NULL                        */
+    int8_t          *q;         /* K int8                                */
+    sllm_gfx950_act *act;       /* scale / sum                           */
+    float           *out;       /* N f32 epilogue output, or NULL        */
+    int32_t         *rows_out;  /* N int32 raw dots, or NULL             */
 } sllm_gfx950_gemv_job;
 
-/* Run independent GEMVs (e.g. Q, K and V against one activation, or many
- * layers' matrices) in ONE launch. The job table is copied to the device on
- * each call; use a plan to upload it once. */
+/* Run independent GEMVs (Q, K and V against one activation, gate and up,
+ * or many layers' matrices) in one launch (two when some K > 16384). The
+ * job tables are built and uploaded on each call, and the call waits for
+ * the stream before freeing them; a plan uploads them once. */
 int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs);
 
 typedef struct sllm_gfx950_plan sllm_gfx950_plan;
 int  sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
                              sllm_gfx950_plan **plan);
 int  sllm_gfx950_plan_run(const sllm_gfx950_plan *plan);
+/* plan_run that also records numbered event `event` (see
+ * sllm_gfx950_event_record) between the quantiser launch and the GEMV
+ * launches, so each can be timed on the stream it runs on. */
+int  sllm_gfx950_plan_run_marked(const sllm_gfx950_plan *plan, int event);
 void sllm_gfx950_plan_destroy(sllm_gfx950_plan *plan);
 
-/* Launch-shape override for tuning sweeps: lanes per row (4, 8 or 16),
- * waves per workgroup (1..16) and rows per workgroup (a multiple of
- * 64/lanes). 0 restores the automatic choice. Affects later launches only. */
-int sllm_gfx950_set_gemv_shape(int lanes_per_row, int waves, int rows_per_wg);
+/* Launch-geometry override for tuning sweeps and tests; affects launches
+ * and plans created afterwards. All zero (variant -1) is automatic.
+ *   path           0 auto (streaming), 1 streaming kernel,
+ *                  2 row-group kernel (K <= 16384; larger K always streams)
+ *   variant        row-group geometry 0..3 (used when it covers K), -1 auto
+ *   lanes_per_row  streaming kernel: 4, 8 or 16
+ *   waves          waves per workgroup: 1..4 row-group, 1..16 streaming
+ *   rows_per_wg    rows per workgroup
+ *   fuse_quant     1: jobs carrying x are quantised inside the row-group
+ *                  kernel (one launch); 0: by a quantiser launch first */
+int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, int rows_per_wg,
+                           int fuse_quant);
 
 /* ------------------------------------------------------------------ */
 /* host-pointer kernel row (the reference's signatures)                */

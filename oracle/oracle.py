@@ -69,8 +69,9 @@ _REF_PROTOS = {
     "sllm_pool_destroy": (None, [c_void_p]),
     "sllm_pool_threads": (c_int, [c_void_p]),
     "ref_gemv": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "ref_gemv_all": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
     "ref_gemv_epilogue": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, POINTER(Act),
-                                 c_void_p, c_void_p]),
+                                 c_void_p, c_void_p, c_int]),
 }
 
 # the reference's ISA levels as passed to sllm_i2s_select_level

@@ -47,11 +47,23 @@ void ref_gemv(sllm_pool *pool, const uint8_t *w, size_t n_rows, size_t n,
     sllm_parallel_rows(pool, ref_gemv_rows, &j, n_rows, REF_ROW_GRAIN);
 }
 
+/* The same row split without the distribution threshold: every GEMV goes
+ * to the pool in grain-64 chunks (the reference's policy keeps GEMVs below
+ * 512 rows per thread on the calling thread). */
+void ref_gemv_all(sllm_pool *pool, const uint8_t *w, size_t n_rows, size_t n,
+                  const int8_t *q, int32_t *out) {
+    ref_gemv_job j = { w, n / 4u, n, q, out };
+    sllm_parallel_rows(pool, ref_gemv_rows, &j, n_rows, REF_ROW_GRAIN);
+}
+
 /* One projection after quantisation, as src/forward.c:652-655 does it:
- * the GEMV, then the epilogue with the tensor's trailing scale. */
+ * the GEMV, then the epilogue with the tensor's trailing scale. With
+ * `distribute_all` the GEMV ignores the distribution threshold. */
 void ref_gemv_epilogue(sllm_pool *pool, const uint8_t *w, size_t n_rows, size_t n,
-                       const int8_t *q, const sllm_i2s_act *act, int32_t *dots, float *y) {
-    ref_gemv(pool, w, n_rows, n, q, dots);
+                       const int8_t *q, const sllm_i2s_act *act, int32_t *dots, float *y,
+                       int distribute_all) {
+    if (distribute_all) ref_gemv_all(pool, w, n_rows, n, q, dots);
+    else ref_gemv(pool, w, n_rows, n, q, dots);
     const float ws = sllm_i2s_scale(w, n_rows * n);
     for (size_t r = 0; r < n_rows; ++r) {
         y[r] = sllm_i2s_epilogue(dots[r], act->sum, act->scale, ws);

@@ -38,8 +38,8 @@ class Act(ctypes.Structure):
 
 class GemvJob(ctypes.Structure):
     """sllm_gfx950_gemv_job."""
-    _fields_ = [("w", c_void_p), ("n_rows", c_size_t), ("n", c_size_t), ("q", c_void_p),
-                ("act", c_void_p), ("out", c_void_p), ("rows_out", c_void_p)]
+    _fields_ = [("w", c_void_p), ("n_rows", c_size_t), ("n", c_size_t), ("x", c_void_p),
+                ("q", c_void_p), ("act", c_void_p), ("out", c_void_p), ("rows_out", c_void_p)]
 
 
 class KernelRow(ctypes.Structure):
@@ -79,8 +79,9 @@ PROTOTYPES = {
     "sllm_gfx950_gemv_batch": (c_int, [POINTER(GemvJob), c_size_t]),
     "sllm_gfx950_plan_create": (c_int, [POINTER(GemvJob), c_size_t, POINTER(c_void_p)]),
     "sllm_gfx950_plan_run": (c_int, [c_void_p]),
+    "sllm_gfx950_plan_run_marked": (c_int, [c_void_p, c_int]),
     "sllm_gfx950_plan_destroy": (None, [c_void_p]),
-    "sllm_gfx950_set_gemv_shape": (c_int, [c_int, c_int, c_int]),
+    "sllm_gfx950_set_tuning": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "sllm_gfx950_tensor_register": (c_int, [c_void_p, c_size_t, c_size_t]),
     "sllm_gfx950_tensor_unregister": (c_int, [c_void_p]),
     "sllm_gfx950_tensor_device": (c_void_p, [c_void_p]),
@@ -264,14 +265,18 @@ class Device:
         check(self.lib.sllm_gfx950_plan_create(arr, len(jobs), ctypes.byref(p)), "plan_create")
         return p
 
-    def plan_run(self, p):
-        check(self.lib.sllm_gfx950_plan_run(p), "plan_run")
+    def plan_run(self, p, event=None):
+        if event is None:
+            check(self.lib.sllm_gfx950_plan_run(p), "plan_run")
+        else:
+            check(self.lib.sllm_gfx950_plan_run_marked(p, event), "plan_run_marked")
 
     def plan_destroy(self, p):
         self.lib.sllm_gfx950_plan_destroy(p)
 
-    def set_gemv_shape(self, lanes_per_row=0, waves=0, rows_per_wg=0):
-        check(self.lib.sllm_gfx950_set_gemv_shape(lanes_per_row, waves, rows_per_wg), "set_gemv_shape")
+    def set_tuning(self, path=0, variant=-1, lanes_per_row=0, waves=0, rows_per_wg=0, fuse_quant=0):
+        check(self.lib.sllm_gfx950_set_tuning(path, variant, lanes_per_row, waves, rows_per_wg, fuse_quant),
+              "set_tuning")
 
 
 # ---------------------------------------------------------------------------

@@ -49,17 +49,20 @@ __asm__(".section .rodata.sllm_gfx950_code_object,\"a\",@progbits\n"
 
 typedef struct k_gemv_job {
     const uint8_t         *w;
-    const int8_t          *q;
-    const sllm_gfx950_act *act;
+    const float           *x;
+    int8_t                *q;
+    sllm_gfx950_act       *act;
     float                 *out_f;
     int32_t               *out_i;
     uint32_t               n_rows;
     uint32_t               k;
     uint32_t               wg_begin;
     uint32_t               rows_per_wg;
+    uint32_t               variant;
+    uint32_t               pad;
 } k_gemv_job;
 
-_Static_assert(sizeof(k_gemv_job) == 56, "k_gemv_job must match gemv_job in i2s_kernels.hip");
+_Static_assert(sizeof(k_gemv_job) == 72, "k_gemv_job must match gemv_job in i2s_kernels.hip");
 _Static_assert(sizeof(sllm_gfx950_act) == 8, "sllm_gfx950_act must match sllm_i2s_act");
 
 enum { LPR_4 = 0, LPR_8 = 1, LPR_16 = 2, N_LPR = 3 };
@@ -83,13 +86,29 @@ typedef struct reg_tensor {
     uint8_t       *dev;
 } reg_tensor;
 
+/* One row for the list quantiser (mirror of quant_job in i2s_kernels.hip). */
+typedef struct k_quant_job {
+    const float     *x;
+    int8_t          *q;
+    sllm_gfx950_act *act;
+    uint32_t         n;
+    uint32_t         pad;
+} k_quant_job;
+
+_Static_assert(sizeof(k_quant_job) == 32, "k_quant_job must match quant_job in i2s_kernels.hip");
+
+/*
+ * A batch of GEMVs as launches: one list-quantiser launch for every distinct
+ * activation the batch quantises, the row-group kernel classes, then the
+ * streaming kernel. Device tables: quant list, rg class 0, 1, 2, stream.
+ */
 struct sllm_gfx950_plan {
-    void    *jobs_dev;
-    uint32_t n_jobs;
-    uint32_t n_wg;
-    uint32_t lds;
-    int      lpr_idx;
-    int      threads;
+    void      *tables_dev;
+    void      *scratch_dev;    /* q / act of jobs that quantise without giving buffers */
+    uint32_t   n_quant;
+    uint32_t   n_rg[3], rg_wg[3], rg_lds[3], rg_threads;
+    uint32_t   n_st, st_wg, st_lds, st_threads;
+    int        st_lpr_idx;
 };
 
 static struct {
@@ -99,25 +118,26 @@ static struct {
     size_t         hbm;
     char           name[520];
     hipModule_t    mod;
-    hipFunction_t  k_quant;
+    hipFunction_t  k_quant, k_quant_list;
     hipFunction_t  k_gemv[N_LPR];
     hipFunction_t  k_group[N_LPR];
+    hipFunction_t  k_rg[3], k_rg_group[3];
     hipFunction_t  k_copy;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
     hipEvent_t     ev_start, ev_stop;
     hipEvent_t    *events;
     int            n_events;
-    /* tuning override (0 = automatic) */
-    int            force_lpr, force_waves, force_rows;
+    /* tuning overrides (0 / -1 = automatic) */
+    int            force_path, force_variant, force_lpr, force_waves, force_rows, fuse_quant;
+    /* q / act for sllm_gfx950_linear when the caller gives none */
+    void          *lin_scratch;
     /* registry for the host-pointer row */
     reg_tensor    *regs;
     size_t         n_regs, cap_regs;
-    /* scratch for the host-pointer row and for per-call job tables */
+    /* scratch for the host-pointer row */
     void          *scratch;
     size_t         scratch_bytes;
-    void          *jobs_dev;
-    size_t         jobs_cap;
 } g;
 
 static pthread_mutex_t g_mtx = PTHREAD_MUTEX_INITIALIZER;
@@ -164,12 +184,21 @@ const char *sllm_gfx950_status_string(int status) {
 
 static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_quant, g.mod, "sllm_k_quant_act"));
+    HIP_TRY(hipModuleGetFunction(&g.k_quant_list, g.mod, "sllm_k_quant_list"));
     HIP_TRY(hipModuleGetFunction(&g.k_copy, g.mod, "sllm_k_copy"));
     HIP_TRY(hipModuleGetFunction(&g.k_checksum, g.mod, "sllm_k_checksum"));
     for (int i = 0; i < N_LPR; ++i) {
         HIP_TRY(hipModuleGetFunction(&g.k_gemv[i], g.mod, k_gemv_names[i]));
         HIP_TRY(hipModuleGetFunction(&g.k_group[i], g.mod, k_group_names[i]));
     }
+    for (int c = 0; c < 3; ++c) {
+        char name[64];
+        snprintf(name, sizeof name, "sllm_k_gemv_rg_c%d", c);
+        HIP_TRY(hipModuleGetFunction(&g.k_rg[c], g.mod, name));
+        snprintf(name, sizeof name, "sllm_k_gemv_rg_group_c%d", c);
+        HIP_TRY(hipModuleGetFunction(&g.k_rg_group[c], g.mod, name));
+    }
+    g.force_variant = -1;
     return SLLM_GFX950_OK;
 }
 
@@ -223,6 +252,14 @@ int sllm_gfx950_open(int device) {
         st = hip_fail(e, "hipEventCreate");
         goto out;
     }
+    if ((e = hipMalloc(&g.lin_scratch, SLLM_GFX950_MAX_K + 256)) != hipSuccess) {
+        hipEventDestroy(g.ev_start);
+        hipEventDestroy(g.ev_stop);
+        hipStreamDestroy(g.stream);
+        hipModuleUnload(g.mod);
+        st = hip_fail(e, "hipMalloc(row scratch)");
+        goto out;
+    }
     g.device = device;
     g.cu = prop.multiProcessorCount;
     g.hbm = prop.totalGlobalMem;
@@ -240,7 +277,7 @@ void sllm_gfx950_close(void) {
         for (size_t i = 0; i < g.n_regs; ++i) hipFree(g.regs[i].dev);
         free(g.regs);
         if (g.scratch) hipFree(g.scratch);
-        if (g.jobs_dev) hipFree(g.jobs_dev);
+        if (g.lin_scratch) hipFree(g.lin_scratch);
         for (int i = 0; i < g.n_events; ++i) hipEventDestroy(g.events[i]);
         free(g.events);
         hipEventDestroy(g.ev_start);
@@ -409,181 +446,263 @@ int sllm_gfx950_quant_act(const float *x, size_t n, size_t n_tok, int8_t *q,
     return launch(g.k_quant, (uint32_t) n_tok, QUANT_THREADS, 0, args);
 }
 
-/* Shape of one GEMV launch. */
-typedef struct gemv_shape {
+/*
+ * Launch geometry.
+ *
+ * Streaming kernel (default, any K): LPR lanes per row, W waves looping over
+ * groups of 64/LPR rows inside a slab of rows_per_wg rows; the activation is
+ * a quantised row staged in LDS, so jobs that carry f32 x are quantised
+ * first by one list-quantiser launch per batch. Measured on the BitNet-2B
+ * FFN shapes, small short-lived workgroups (LPR 8, 2 waves, 32 rows) stream
+ * fastest.
+ *
+ * Row-group kernel (path 2, K <= RG_MAX_K): a job's variant fixes (LPR,
+ * CPL chunks per lane) by its K class, compiled into three kernel classes
+ * (0: variants 0-1, 1: variant 2, 2: variant 3); a block of W waves walks
+ * rows_per_wg rows double-buffered. With fuse_quant it quantises x itself
+ * (one launch, no quantiser), which pays off only when launches dominate.
+ */
+#define RG_MAX_K 16384
+#define RG_DEFAULT_WAVES 2
+#define RG_DEFAULT_ROWS 64
+
+typedef struct rg_geom { int lpr, cpl, cls; } rg_geom;
+static const rg_geom k_rg_geom[4] = { { 8, 5, 0 }, { 16, 7, 0 }, { 8, 14, 1 }, { 16, 16, 2 } };
+
+/* variants 0, 1, 3 cover every K <= RG_MAX_K; 2 is only used when forced */
+static int rg_variant_for(size_t k) {
+    const size_t chunks = k / 64;
+    if (g.force_variant >= 0) {
+        const rg_geom *v = &k_rg_geom[g.force_variant];
+        if ((size_t) v->lpr * (size_t) v->cpl >= chunks) return g.force_variant;
+    }
+    static const int order[3] = { 0, 1, 3 };
+    for (int i = 0; i < 3; ++i) {
+        const rg_geom *v = &k_rg_geom[order[i]];
+        if ((size_t) v->lpr * (size_t) v->cpl >= chunks) return order[i];
+    }
+    return -1;
+}
+
+/* the row-group kernels are compiled for blocks of at most 4 waves */
+static int rg_waves(void) {
+    const int w = g.force_waves ? g.force_waves : RG_DEFAULT_WAVES;
+    return w > 4 ? 4 : w;
+}
+
+static uint32_t rg_rows_per_wg(void) {
+    return g.force_rows ? (uint32_t) g.force_rows : RG_DEFAULT_ROWS;
+}
+
+/* path for a job of width k: 2 = row-group kernel, 1 = streaming kernel */
+static int path_for(size_t k) {
+    if (k > RG_MAX_K) return 1;
+    if (g.force_path == 2 || g.fuse_quant) return 2;
+    return 1;
+}
+
+/* does a job carrying x quantise inside the GEMV (else: list quantiser first) */
+static int fused_for(size_t k) { return g.fuse_quant && path_for(k) == 2; }
+
+typedef struct stream_shape {
     int      lpr_idx;
     int      waves;
     uint32_t rows_per_wg;
-} gemv_shape;
+} stream_shape;
 
 static int lpr_index(int lpr) {
     for (int i = 0; i < N_LPR; ++i) if (k_lpr_value[i] == lpr) return i;
     return -1;
 }
 
-/*
- * Automatic launch shape. A row is split over `lpr` lanes (each takes every
- * lpr-th 16-byte chunk); a wave therefore covers 64/lpr rows per pass. Prefer
- * the split that keeps every lane busy (chunks per row divisible by lpr), then
- * enough waves to cover the chip.
- */
-static gemv_shape choose_shape(size_t n_rows, size_t n) {
-    gemv_shape s;
-    const size_t chunks = n / 64;
-    int best = LPR_4;
-    if (g.force_lpr) {
-        best = lpr_index(g.force_lpr);
-    } else {
-        /* smallest lpr whose rows-per-wave still gives >= 2 waves per CU */
-        const size_t cu = g.cu > 0 ? (size_t) g.cu : 256;
-        best = LPR_16;
-        for (int i = 0; i < N_LPR; ++i) {
-            const size_t rpw = 64 / (size_t) k_lpr_value[i];
-            const size_t waves = (n_rows + rpw - 1) / rpw;
-            if (waves >= 2 * cu && chunks % (size_t) k_lpr_value[i] == 0) { best = i; break; }
-        }
-    }
-    s.lpr_idx = best;
-    s.waves = g.force_waves ? g.force_waves : 4;
-    const uint32_t rpw = (uint32_t) (64 / k_lpr_value[best]);
-    s.rows_per_wg = g.force_rows ? (uint32_t) g.force_rows : (uint32_t) s.waves * rpw;
+static stream_shape stream_shape_for(void) {
+    stream_shape s;
+    s.lpr_idx = g.force_lpr ? lpr_index(g.force_lpr) : LPR_8;
+    s.waves = g.force_waves ? g.force_waves : 2;
+    const uint32_t rpw = (uint32_t) (64 / k_lpr_value[s.lpr_idx]);
+    s.rows_per_wg = g.force_rows ? (uint32_t) g.force_rows : 2u * (uint32_t) s.waves * rpw;
     return s;
 }
 
-int sllm_gfx950_set_gemv_shape(int lanes_per_row, int waves, int rows_per_wg) {
+int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, int rows_per_wg,
+                           int fuse_quant) {
+    if (path < 0 || path > 2) return fail(SLLM_GFX950_ERR_ARG, "path must be 0 (auto), 1 (stream) or 2 (row-group)");
+    if (variant < -1 || variant > 3) return fail(SLLM_GFX950_ERR_ARG, "variant must be -1 (auto) or 0..3");
     if (lanes_per_row != 0 && lpr_index(lanes_per_row) < 0) {
         return fail(SLLM_GFX950_ERR_ARG, "lanes per row must be 4, 8 or 16");
     }
     if (waves < 0 || waves > 16) return fail(SLLM_GFX950_ERR_ARG, "waves must be 0..16");
+    if ((path == 2 || fuse_quant) && waves > 4) return fail(SLLM_GFX950_ERR_ARG, "the row-group kernel takes at most 4 waves");
     if (rows_per_wg < 0) return fail(SLLM_GFX950_ERR_ARG, "rows per workgroup must be >= 0");
-    if (rows_per_wg > 0) {
-        const int l = lanes_per_row ? lanes_per_row : 4;
-        if (rows_per_wg % (64 / l) != 0) {
-            return fail(SLLM_GFX950_ERR_ARG, "rows per workgroup must be a multiple of %d", 64 / l);
-        }
-    }
+    if (fuse_quant < 0 || fuse_quant > 1) return fail(SLLM_GFX950_ERR_ARG, "fuse_quant must be 0 or 1");
+    if (fuse_quant && path == 1) return fail(SLLM_GFX950_ERR_ARG, "only the row-group kernel quantises in-kernel");
+    g.force_path = path;
+    g.force_variant = variant;
     g.force_lpr = lanes_per_row;
     g.force_waves = waves;
     g.force_rows = rows_per_wg;
+    g.fuse_quant = fuse_quant;
     return SLLM_GFX950_OK;
 }
 
-static int check_gemv_args(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q) {
-    if (w == NULL || q == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv: NULL pointer");
-    if (n % SLLM_GFX950_QK != 0) return fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "gemv: K=%zu is not a multiple of 128", n);
+static int check_weights(const uint8_t *w, size_t n_rows, size_t n) {
+    if (w == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv: NULL weights");
+    if (n == 0 || n % SLLM_GFX950_QK != 0) return fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "gemv: K=%zu is not a positive multiple of 128", n);
     if (n > SLLM_GFX950_MAX_K) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemv: K=%zu above %d", n, SLLM_GFX950_MAX_K);
     if (n_rows > UINT32_MAX / 2) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemv: %zu rows", n_rows);
-    if (((uintptr_t) w & 15u) != 0 || ((uintptr_t) q & 15u) != 0) {
-        return fail(SLLM_GFX950_ERR_ARG, "gemv: weights and activations must be 16-byte aligned");
-    }
+    if (((uintptr_t) w & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemv: weights must be 16-byte aligned");
     return SLLM_GFX950_OK;
 }
 
-static int gemv_launch(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
-                       const sllm_gfx950_act *act, float *out, int32_t *rows_out) {
-    NEED_OPEN();
-    int st = check_gemv_args(w, n_rows, n, q);
+/* Validate one public job and translate it (geometry filled later). */
+static int job_to_kernel(const sllm_gfx950_gemv_job *j, size_t i, k_gemv_job *kj) {
+    int st = check_weights(j->w, j->n_rows, j->n);
     if (st != SLLM_GFX950_OK) return st;
-    if (out == NULL && rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv: no output");
-    if (out != NULL && act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv: epilogue needs act");
-    if (n_rows == 0 || n == 0) return SLLM_GFX950_OK;
-    const gemv_shape s = choose_shape(n_rows, n);
-    k_gemv_job job = { w, q, act, out, rows_out, (uint32_t) n_rows, (uint32_t) n, 0, s.rows_per_wg };
-    const uint32_t grid = (uint32_t) ((n_rows + s.rows_per_wg - 1) / s.rows_per_wg);
-    void *args[] = { &job };
-    return launch(g.k_gemv[s.lpr_idx], grid, (uint32_t) (64 * s.waves), (uint32_t) n, args);
+    if (j->out == NULL && j->rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "job %zu: no output", i);
+    if (j->x != NULL) {
+        if (((uintptr_t) j->x & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "job %zu: x must be 16-byte aligned", i);
+        if (j->q != NULL && ((uintptr_t) j->q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "job %zu: q must be 16-byte aligned", i);
+        if ((j->q == NULL) != (j->act == NULL)) return fail(SLLM_GFX950_ERR_ARG, "job %zu: give both q and act, or neither", i);
+    } else {
+        if (j->q == NULL || ((uintptr_t) j->q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "job %zu: q must be given and 16-byte aligned", i);
+        if (j->out != NULL && j->act == NULL) return fail(SLLM_GFX950_ERR_ARG, "job %zu: the epilogue needs act", i);
+    }
+    *kj = (k_gemv_job) { j->w, j->x, j->q, j->act, j->out, j->rows_out, (uint32_t) j->n_rows,
+                         (uint32_t) j->n, 0, 0, 0, 0 };
+    return SLLM_GFX950_OK;
 }
 
-int sllm_gfx950_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
-                     int32_t *rows_out) {
-    if (rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv: NULL rows_out");
-    return gemv_launch(w, n_rows, n, q, NULL, NULL, rows_out);
+static size_t align256(size_t v) { return (v + 255u) & ~(size_t) 255u; }
+
+/* jobs that quantise x into plan scratch (carry x, no q / act, not fused) */
+static int takes_scratch(const sllm_gfx950_gemv_job *j) {
+    return j->x != NULL && j->q == NULL && !fused_for(j->n);
 }
 
-int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
-                              const sllm_gfx950_act *act, float *out) {
-    if (out == NULL || act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv_epilogue: NULL out/act");
-    return gemv_launch(w, n_rows, n, q, act, out, NULL);
-}
+/* scratch bytes for one quantised row of width k: q, then act */
+static size_t row_scratch(size_t k) { return align256(k) + 256; }
 
-int sllm_gfx950_linear(const uint8_t *w, size_t n_rows, size_t n, const float *x,
-                       int8_t *q, sllm_gfx950_act *act, float *out) {
-    NEED_OPEN();
-    int st = check_gemv_args(w, n_rows, n, q);
-    if (st != SLLM_GFX950_OK) return st;
-    if ((st = sllm_gfx950_quant_act(x, n, 1, q, act)) != SLLM_GFX950_OK) return st;
-    return sllm_gfx950_gemv_epilogue(w, n_rows, n, q, act, out);
-}
-
-/* Build the device job table for a batch; all jobs share one launch shape. */
-static int build_jobs(const sllm_gfx950_gemv_job *jobs, size_t n_jobs, k_gemv_job *kj,
-                      gemv_shape *shape_out, uint32_t *n_wg_out, uint32_t *lds_out) {
-    size_t max_rows = 0, max_k = 0, total_rows = 0;
+/* Bytes of plan scratch: one quantised row per distinct (x, K) among the
+ * jobs that take scratch. */
+static size_t plan_scratch_bytes(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
+    size_t bytes = 0;
     for (size_t i = 0; i < n_jobs; ++i) {
-        const sllm_gfx950_gemv_job *j = &jobs[i];
-        int st = check_gemv_args(j->w, j->n_rows, j->n, j->q);
+        if (!takes_scratch(&jobs[i])) continue;
+        size_t e = 0;
+        while (e < i && !(takes_scratch(&jobs[e]) && jobs[e].x == jobs[i].x && jobs[e].n == jobs[i].n)) ++e;
+        if (e == i) bytes += row_scratch(jobs[i].n);
+    }
+    return bytes;
+}
+
+/*
+ * Lay a batch out as launches. `kq` (n_jobs entries) receives the quant list:
+ * one row per distinct (x, q) among jobs that carry x and are not fused --
+ * into the job's q / act, or into plan scratch (p->scratch_dev, sized by
+ * plan_scratch_bytes) shared by every scratch job with the same (x, K).
+ * `tab` receives the GEMV tables in launch order (rg class 0, 1, 2, stream;
+ * each launch's wg_begin counts from 0); `tmp` / `launch_of` are scratch.
+ */
+static int plan_layout(const sllm_gfx950_gemv_job *jobs, size_t n_jobs, sllm_gfx950_plan *p,
+                       k_quant_job *kq, k_gemv_job *tab, k_gemv_job *tmp, uint8_t *launch_of) {
+    const stream_shape ss = stream_shape_for();
+    uint64_t wg[4] = { 0, 0, 0, 0 };
+    size_t lds[4] = { 0, 0, 0, 0 };
+    uint32_t count[4] = { 0, 0, 0, 0 };
+    size_t scratch_at = 0;
+    p->n_quant = 0;
+    for (size_t i = 0; i < n_jobs; ++i) {
+        k_gemv_job kj;
+        int st = job_to_kernel(&jobs[i], i, &kj);
         if (st != SLLM_GFX950_OK) return st;
-        if (j->out == NULL && j->rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "batch job %zu: no output", i);
-        if (j->out != NULL && j->act == NULL) return fail(SLLM_GFX950_ERR_ARG, "batch job %zu: epilogue needs act", i);
-        if (j->n_rows > max_rows) max_rows = j->n_rows;
-        if (j->n > max_k) max_k = j->n;
-        total_rows += j->n_rows;
+        if (kj.x != NULL && !fused_for(kj.k)) {
+            const int scratch = kj.q == NULL;
+            uint32_t e = 0;
+            for (; e < p->n_quant; ++e) {
+                if (kq[e].x != kj.x || kq[e].n != kj.k || (int) kq[e].pad != scratch) continue;
+                if (scratch || kq[e].q == kj.q) break;
+            }
+            if (e == p->n_quant) {
+                if (scratch) {
+                    uint8_t *row = (uint8_t *) p->scratch_dev + scratch_at;
+                    scratch_at += row_scratch(kj.k);
+                    kq[e] = (k_quant_job) { kj.x, (int8_t *) row,
+                                            (sllm_gfx950_act *) (row + align256(kj.k)), kj.k, 1 };
+                } else {
+                    kq[e] = (k_quant_job) { kj.x, kj.q, kj.act, kj.k, 0 };
+                }
+                p->n_quant++;
+            }
+            kj.q = kq[e].q;             /* the GEMV reads the quantised row */
+            kj.act = kq[e].act;
+            kj.x = NULL;
+        }
+        int l;
+        if (path_for(kj.k) == 2) {
+            const int v = rg_variant_for(kj.k);
+            kj.variant = (uint32_t) v;
+            kj.rows_per_wg = rg_rows_per_wg();
+            l = k_rg_geom[v].cls;
+        } else {
+            kj.rows_per_wg = ss.rows_per_wg;
+            l = 3;
+        }
+        kj.wg_begin = (uint32_t) wg[l];
+        wg[l] += (kj.n_rows + kj.rows_per_wg - 1) / kj.rows_per_wg;
+        if (kj.k > lds[l]) lds[l] = kj.k;
+        count[l]++;
+        launch_of[i] = (uint8_t) l;
+        tmp[i] = kj;
     }
-    /* one shape for the whole launch, judged on the total row count and the
-     * largest K (any shape is correct for any K; the choice only moves lane
-     * utilisation) */
-    const gemv_shape s = choose_shape(total_rows, max_k);
-    uint64_t wg = 0;
-    for (size_t i = 0; i < n_jobs; ++i) {
-        const sllm_gfx950_gemv_job *j = &jobs[i];
-        kj[i] = (k_gemv_job) { j->w, j->q, j->act, j->out, j->rows_out, (uint32_t) j->n_rows,
-                               (uint32_t) j->n, (uint32_t) wg, s.rows_per_wg };
-        wg += (j->n_rows + s.rows_per_wg - 1) / s.rows_per_wg;
+    for (int l = 0; l < 4; ++l) {
+        if (wg[l] > UINT32_MAX) return fail(SLLM_GFX950_ERR_TOO_LARGE, "batch: too many workgroups");
     }
-    if (wg > UINT32_MAX) return fail(SLLM_GFX950_ERR_TOO_LARGE, "batch: too many workgroups");
-    *shape_out = s;
-    *n_wg_out = (uint32_t) wg;
-    *lds_out = (uint32_t) max_k;
-    (void) max_rows;
+    size_t at = 0;
+    for (int l = 0; l < 4; ++l) {
+        for (size_t i = 0; i < n_jobs; ++i) if (launch_of[i] == l) tab[at++] = tmp[i];
+    }
+    for (int c = 0; c < 3; ++c) {
+        p->n_rg[c] = count[c];
+        p->rg_wg[c] = (uint32_t) wg[c];
+        p->rg_lds[c] = (uint32_t) lds[c];
+    }
+    p->rg_threads = (uint32_t) (64 * rg_waves());
+    p->n_st = count[3];
+    p->st_wg = (uint32_t) wg[3];
+    p->st_lds = (uint32_t) lds[3];
+    p->st_threads = (uint32_t) (64 * ss.waves);
+    p->st_lpr_idx = ss.lpr_idx;
     return SLLM_GFX950_OK;
 }
 
-static int launch_group(const void *jobs_dev, uint32_t n_jobs, uint32_t n_wg, uint32_t lds,
-                        const gemv_shape *s) {
-    void *args[] = { (void *) &jobs_dev, &n_jobs };
-    return launch(g.k_group[s->lpr_idx], n_wg, (uint32_t) (64 * s->waves), lds, args);
+static int launch_quant(const float *x, uint32_t n, uint32_t n_tok, int8_t *q, sllm_gfx950_act *act) {
+    void *args[] = { (void *) &x, &n, &q, &act };
+    return launch(g.k_quant, n_tok, QUANT_THREADS, 0, args);
 }
 
-int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
-    NEED_OPEN();
-    if (n_jobs == 0) return SLLM_GFX950_OK;
-    if (jobs == NULL || n_jobs > UINT32_MAX) return fail(SLLM_GFX950_ERR_ARG, "batch: bad job list");
-    k_gemv_job *kj = malloc(n_jobs * sizeof *kj);
-    if (kj == NULL) return fail(SLLM_GFX950_ERR_NOMEM, "batch: host job table");
-    gemv_shape s;
-    uint32_t n_wg = 0, lds = 0;
-    int st = build_jobs(jobs, n_jobs, kj, &s, &n_wg, &lds);
-    const size_t bytes = n_jobs * sizeof *kj;
-    if (st == SLLM_GFX950_OK && bytes > g.jobs_cap) {
-        /* the previous table may still be read by an enqueued launch */
-        hipError_t e = hipStreamSynchronize(g.stream);
-        if (e == hipSuccess && g.jobs_dev) e = hipFree(g.jobs_dev);
-        g.jobs_dev = NULL;
-        g.jobs_cap = 0;
-        if (e == hipSuccess) e = hipMalloc(&g.jobs_dev, bytes);
-        if (e != hipSuccess) st = hip_fail(e, "batch: job table");
-        else g.jobs_cap = bytes;
+static int plan_launch(const sllm_gfx950_plan *p, int event) {
+    int st = SLLM_GFX950_OK;
+    const k_quant_job *kq = p->tables_dev;
+    if (p->n_quant) {
+        void *args[] = { (void *) &kq };
+        st = launch(g.k_quant_list, p->n_quant, QUANT_THREADS, 0, args);
     }
-    if (st == SLLM_GFX950_OK) {
-        /* synchronous upload: the host table is freed below, and a launch
-         * already enqueued may be reading the device table */
-        hipError_t e = hipStreamSynchronize(g.stream);
-        if (e == hipSuccess) e = hipMemcpy(g.jobs_dev, kj, bytes, hipMemcpyHostToDevice);
-        if (e != hipSuccess) st = hip_fail(e, "batch: job upload");
+    if (st == SLLM_GFX950_OK && event >= 0) st = sllm_gfx950_event_record(event);
+    const k_gemv_job *t = (const k_gemv_job *) (kq + p->n_quant);
+    for (int c = 0; c < 3 && st == SLLM_GFX950_OK; ++c) {
+        if (p->n_rg[c]) {
+            uint32_t n = p->n_rg[c];
+            void *args[] = { (void *) &t, &n };
+            st = launch(g.k_rg_group[c], p->rg_wg[c], p->rg_threads, p->rg_lds[c], args);
+            t += p->n_rg[c];
+        }
     }
-    free(kj);
-    if (st != SLLM_GFX950_OK) return st;
-    return launch_group(g.jobs_dev, (uint32_t) n_jobs, n_wg, lds, &s);
+    if (st == SLLM_GFX950_OK && p->n_st) {
+        uint32_t n = p->n_st;
+        void *args[] = { (void *) &t, &n };
+        st = launch(g.k_group[p->st_lpr_idx], p->st_wg, p->st_threads, p->st_lds, args);
+    }
+    return st;
 }
 
 int sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
@@ -592,29 +711,48 @@ int sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
     if (plan == NULL) return fail(SLLM_GFX950_ERR_ARG, "plan: NULL out pointer");
     *plan = NULL;
     if (jobs == NULL || n_jobs == 0 || n_jobs > UINT32_MAX) return fail(SLLM_GFX950_ERR_ARG, "plan: bad job list");
-    k_gemv_job *kj = malloc(n_jobs * sizeof *kj);
     sllm_gfx950_plan *p = calloc(1, sizeof *p);
-    if (kj == NULL || p == NULL) {
-        free(kj);
-        free(p);
-        return fail(SLLM_GFX950_ERR_NOMEM, "plan: host tables");
+    k_quant_job *kq = malloc(n_jobs * sizeof *kq);
+    k_gemv_job *tab = malloc(n_jobs * sizeof *tab);
+    k_gemv_job *tmp = malloc(n_jobs * sizeof *tmp);
+    uint8_t *launch_of = malloc(n_jobs);
+    int st = SLLM_GFX950_OK;
+    if (p == NULL || kq == NULL || tab == NULL || tmp == NULL || launch_of == NULL) {
+        st = fail(SLLM_GFX950_ERR_NOMEM, "plan: host tables");
     }
-    gemv_shape s;
-    int st = build_jobs(jobs, n_jobs, kj, &s, &p->n_wg, &p->lds);
     if (st == SLLM_GFX950_OK) {
-        hipError_t e = hipMalloc(&p->jobs_dev, n_jobs * sizeof *kj);
-        if (e == hipSuccess) e = hipMemcpy(p->jobs_dev, kj, n_jobs * sizeof *kj, hipMemcpyHostToDevice);
-        if (e != hipSuccess) st = hip_fail(e, "plan: job table");
+        const size_t scratch = plan_scratch_bytes(jobs, n_jobs);
+        if (scratch) {
+            hipError_t e = hipMalloc(&p->scratch_dev, scratch);
+            if (e != hipSuccess) st = hip_fail(e, "plan: activation scratch");
+        }
     }
-    free(kj);
+    if (st == SLLM_GFX950_OK) st = plan_layout(jobs, n_jobs, p, kq, tab, tmp, launch_of);
+    if (st == SLLM_GFX950_OK) {
+        const size_t qbytes = p->n_quant * sizeof *kq, bytes = qbytes + n_jobs * sizeof *tab;
+        uint8_t *host = malloc(bytes);
+        if (host == NULL) st = fail(SLLM_GFX950_ERR_NOMEM, "plan: table staging");
+        if (st == SLLM_GFX950_OK) {
+            memcpy(host, kq, qbytes);
+            memcpy(host + qbytes, tab, n_jobs * sizeof *tab);
+            hipError_t e = hipMalloc(&p->tables_dev, bytes);
+            if (e == hipSuccess) e = hipMemcpy(p->tables_dev, host, bytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) st = hip_fail(e, "plan: job tables");
+        }
+        free(host);
+    }
+    free(kq);
+    free(tab);
+    free(tmp);
+    free(launch_of);
     if (st != SLLM_GFX950_OK) {
-        if (p->jobs_dev) hipFree(p->jobs_dev);
-        free(p);
+        if (p) {
+            if (p->tables_dev) hipFree(p->tables_dev);
+            if (p->scratch_dev) hipFree(p->scratch_dev);
+            free(p);
+        }
         return st;
     }
-    p->n_jobs = (uint32_t) n_jobs;
-    p->lpr_idx = s.lpr_idx;
-    p->threads = 64 * s.waves;
     *plan = p;
     return SLLM_GFX950_OK;
 }
@@ -622,17 +760,92 @@ int sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
 int sllm_gfx950_plan_run(const sllm_gfx950_plan *p) {
     NEED_OPEN();
     if (p == NULL) return fail(SLLM_GFX950_ERR_ARG, "plan_run: NULL plan");
-    const gemv_shape s = { p->lpr_idx, p->threads / 64, 0 };
-    return launch_group(p->jobs_dev, p->n_jobs, p->n_wg, p->lds, &s);
+    return plan_launch(p, -1);
+}
+
+int sllm_gfx950_plan_run_marked(const sllm_gfx950_plan *p, int event) {
+    NEED_OPEN();
+    if (p == NULL) return fail(SLLM_GFX950_ERR_ARG, "plan_run: NULL plan");
+    if (event < 0 || event >= g.n_events) return fail(SLLM_GFX950_ERR_ARG, "plan_run_marked: event %d not reserved", event);
+    return plan_launch(p, event);
 }
 
 void sllm_gfx950_plan_destroy(sllm_gfx950_plan *p) {
     if (p == NULL) return;
     if (g.open) {
         hipStreamSynchronize(g.stream);
-        hipFree(p->jobs_dev);
+        hipFree(p->tables_dev);
+        if (p->scratch_dev) hipFree(p->scratch_dev);
     }
     free(p);
+}
+
+/* A batch is a plan used once; its tables are freed after the stream drains. */
+int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
+    NEED_OPEN();
+    if (n_jobs == 0) return SLLM_GFX950_OK;
+    sllm_gfx950_plan *p = NULL;
+    int st = sllm_gfx950_plan_create(jobs, n_jobs, &p);
+    if (st != SLLM_GFX950_OK) return st;
+    st = plan_launch(p, -1);
+    sllm_gfx950_plan_destroy(p);      /* synchronises before freeing the tables */
+    return st;
+}
+
+/* One job, passed by value to the single-job entry points. A job carrying
+ * x is quantised first (into its q / act, or the library's row scratch)
+ * unless the row-group kernel quantises in-kernel. */
+static int single_launch(const sllm_gfx950_gemv_job *j) {
+    k_gemv_job kj;
+    int st = job_to_kernel(j, 0, &kj);
+    if (st != SLLM_GFX950_OK) return st;
+    if (kj.n_rows == 0) return SLLM_GFX950_OK;
+    if (kj.x != NULL && !fused_for(kj.k)) {
+        if (kj.q == NULL) {
+            kj.q = (int8_t *) g.lin_scratch;
+            kj.act = (sllm_gfx950_act *) ((uint8_t *) g.lin_scratch + SLLM_GFX950_MAX_K);
+        }
+        st = launch_quant(kj.x, kj.k, 1, kj.q, kj.act);
+        if (st != SLLM_GFX950_OK) return st;
+        kj.x = NULL;
+    }
+    if (path_for(kj.k) == 2) {
+        const int v = rg_variant_for(kj.k);
+        kj.variant = (uint32_t) v;
+        kj.rows_per_wg = rg_rows_per_wg();
+        void *args[] = { &kj };
+        return launch(g.k_rg[k_rg_geom[v].cls], (kj.n_rows + kj.rows_per_wg - 1) / kj.rows_per_wg,
+                      (uint32_t) (64 * rg_waves()), kj.k, args);
+    }
+    const stream_shape ss = stream_shape_for();
+    kj.rows_per_wg = ss.rows_per_wg;
+    void *args[] = { &kj };
+    return launch(g.k_gemv[ss.lpr_idx], (kj.n_rows + kj.rows_per_wg - 1) / kj.rows_per_wg,
+                  (uint32_t) (64 * ss.waves), kj.k, args);
+}
+
+int sllm_gfx950_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
+                     int32_t *rows_out) {
+    NEED_OPEN();
+    if (rows_out == NULL || q == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv: NULL q or rows_out");
+    const sllm_gfx950_gemv_job j = { w, n_rows, n, NULL, (int8_t *) q, NULL, NULL, rows_out };
+    return single_launch(&j);
+}
+
+int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
+                              const sllm_gfx950_act *act, float *out) {
+    NEED_OPEN();
+    if (out == NULL || act == NULL || q == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv_epilogue: NULL q, act or out");
+    const sllm_gfx950_gemv_job j = { w, n_rows, n, NULL, (int8_t *) q, (sllm_gfx950_act *) act, out, NULL };
+    return single_launch(&j);
+}
+
+int sllm_gfx950_linear(const uint8_t *w, size_t n_rows, size_t n, const float *x,
+                       int8_t *q, sllm_gfx950_act *act, float *out) {
+    NEED_OPEN();
+    if (x == NULL || out == NULL) return fail(SLLM_GFX950_ERR_ARG, "linear: NULL x or out");
+    const sllm_gfx950_gemv_job j = { w, n_rows, n, x, q, act, out, NULL };
+    return single_launch(&j);
 }
 
 /* ------------------------------------------------------------------ */

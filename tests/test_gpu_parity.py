@@ -92,7 +92,15 @@ def test_quant_act_edge_rows(amd, orc, dev):
 # ---------------------------------------------------------------------------
 
 SHAPES = [(2560, 2560), (6912, 2560), (2560, 6912), (640, 2560), (1, 128), (3, 384),
-          (17, 1280), (1001, 6912), (129, 65536)]
+          (17, 1280), (1001, 6912), (77, 16384), (129, 65536)]
+
+# (path, variant, lanes_per_row, waves, rows_per_wg[, fuse_quant]): every kernel geometry
+GEOMETRIES = [(1, -1, 4, 1, 0), (1, -1, 8, 4, 0), (1, -1, 16, 2, 0), (1, -1, 8, 2, 48),
+              (2, 0, 0, 1, 0), (2, 0, 0, 2, 0), (2, 1, 0, 2, 0), (2, 1, 0, 4, 0),
+              (2, 2, 0, 2, 0), (2, 3, 0, 1, 0), (2, 3, 0, 4, 0),
+              (2, 0, 0, 2, 8), (2, 1, 0, 4, 24), (2, 3, 0, 2, 40), (2, 0, 0, 4, 1000),
+              (0, -1, 0, 0, 0)]
+FUSED = [(2, -1, 0, 2, 0, 1), (2, 3, 0, 4, 0, 1), (2, 0, 0, 1, 24, 1)]
 
 
 @pytest.mark.parametrize("n_rows,n", SHAPES)
@@ -104,20 +112,15 @@ def test_gemv_int32_matches_oracle(amd, orc, dev, n_rows, n):
     q = rng.integers(-128, 128, n, dtype=np.int8)
     want = orc.gemv(w, n_rows, n, q, orc.DOT_VNNI)
     bw, bq, bo = dev.put(w), dev.put(q), dev.alloc(4 * n_rows)
-    for lpr in (4, 8, 16):
-        for waves in (1, 4):
-            dev.set_gemv_shape(lpr, waves, 0)
+    try:
+        for geom in GEOMETRIES:
+            dev.set_tuning(*geom)
+            bo.upload(np.full(n_rows, -7, np.int32))
             dev.gemv(bw.vp, n_rows, n, bq.vp, bo.vp)
             dev.sync()
-            np.testing.assert_array_equal(bo.download(np.int32, n_rows), want, err_msg=f"lpr={lpr} waves={waves}")
-    dev.set_gemv_shape(8, 2, 48)        # rows per workgroup not a multiple of the wave's rows
-    dev.gemv(bw.vp, n_rows, n, bq.vp, bo.vp)
-    dev.sync()
-    np.testing.assert_array_equal(bo.download(np.int32, n_rows), want)
-    dev.set_gemv_shape(0, 0, 0)
-    dev.gemv(bw.vp, n_rows, n, bq.vp, bo.vp)
-    dev.sync()
-    np.testing.assert_array_equal(bo.download(np.int32, n_rows), want)
+            np.testing.assert_array_equal(bo.download(np.int32, n_rows), want, err_msg=f"geometry {geom}")
+    finally:
+        dev.set_tuning()
     for b in (bw, bq, bo):
         b.free()
 
@@ -150,14 +153,29 @@ def test_linear_matches_oracle(amd, orc, dev, n_rows, n):
     y_o, q_o, d_o, s_o, t_o = orc.linear(w, n_rows, n, x, orc.DOT_VNNI)
     bw, bx = dev.put(w), dev.put(x)
     bq, ba, by, bi = dev.alloc(n), dev.alloc(8), dev.alloc(4 * n_rows), dev.alloc(4 * n_rows)
-    dev.linear(bw.vp, n_rows, n, bx.vp, bq.vp, ba.vp, by.vp)
-    dev.gemv(bw.vp, n_rows, n, bq.vp, bi.vp)
-    dev.sync()
-    np.testing.assert_array_equal(bq.download(np.int8, n), q_o)
-    a = ba.download(np.uint8, 8)
-    assert a[:4].view(np.float32)[0] == s_o and a[4:].view(np.int32)[0] == t_o
-    np.testing.assert_array_equal(bi.download(np.int32, n_rows), d_o)
-    assert f32_bits_equal(by.download(np.float32, n_rows), y_o)
+    try:
+        for geom in [(0, -1, 0, 0, 0), (2, -1, 0, 1, 0), (2, 3, 0, 4, 0), (1, -1, 8, 2, 0)] + FUSED:
+            dev.set_tuning(*geom)
+            for b, fill in ((bq, np.zeros(n, np.int8)), (ba, np.zeros(2, np.int32)),
+                            (by, np.zeros(n_rows, np.float32)), (bi, np.zeros(n_rows, np.int32))):
+                b.upload(fill)
+            dev.linear(bw.vp, n_rows, n, bx.vp, bq.vp, ba.vp, by.vp)
+            dev.gemv(bw.vp, n_rows, n, bq.vp, bi.vp)
+            dev.sync()
+            np.testing.assert_array_equal(bq.download(np.int8, n), q_o, err_msg=str(geom))
+            a = ba.download(np.uint8, 8)
+            assert a[:4].view(np.float32)[0] == s_o and a[4:].view(np.int32)[0] == t_o, geom
+            np.testing.assert_array_equal(bi.download(np.int32, n_rows), d_o, err_msg=str(geom))
+            assert f32_bits_equal(by.download(np.float32, n_rows), y_o), geom
+        # without q / act outputs: library row scratch, or in-kernel
+        for geom in [(0, -1, 0, 0, 0)] + FUSED:
+            dev.set_tuning(*geom)
+            by.upload(np.zeros(n_rows, np.float32))
+            dev.linear(bw.vp, n_rows, n, bx.vp, None, None, by.vp)
+            dev.sync()
+            assert f32_bits_equal(by.download(np.float32, n_rows), y_o), geom
+    finally:
+        dev.set_tuning()
     for b in (bw, bx, bq, ba, by, bi):
         b.free()
 
@@ -196,18 +214,22 @@ def test_batch_and_plan_over_a_block_match_oracle(amd, orc, dev):
         q_o, s_o, t_o = orc.quant_act(x)
         bx, bq, ba = dev.put(x), dev.alloc(n), dev.alloc(8)
         dev.quant_act(bx.vp, n, 1, bq.vp, ba.vp)
-        acts[a] = (bq, ba, q_o, s_o, t_o)
+        acts[a] = (bq, ba, q_o, s_o, t_o, bx)
         bufs += [bx, bq, ba]
     jobs, wants, outs = [], [], []
     for i, (name, n_rows, n, a) in enumerate(BLOCK):
         w = tensor(amd, amd.synth_seed(2, 0, 0, i), n_rows, n)
-        bq, ba, q_o, s_o, t_o = acts[a]
+        bq, ba, q_o, s_o, t_o, _ = acts[a]
         d = orc.gemv(w, n_rows, n, q_o, orc.DOT_VNNI)
         wants.append((d, orc.epilogue_np(d, t_o, s_o, orc.scale(w, n_rows * n))))
         bw, by, bi = dev.put(w), dev.alloc(4 * n_rows), dev.alloc(4 * n_rows)
         outs.append((by, bi, n_rows))
         bufs += [bw, by, bi]
-        jobs.append(amd.GemvJob(bw.ptr, n_rows, n, bq.ptr, ba.ptr, by.ptr, bi.ptr))
+        # odd jobs quantise in-kernel from x, even jobs read the quantised row
+        if i % 2:
+            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, acts[a][5].ptr, None, None, by.ptr, bi.ptr))
+        else:
+            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, None, bq.ptr, ba.ptr, by.ptr, bi.ptr))
     # the numpy epilogue is checked against the C oracle here too
     d0 = wants[0][0]
     assert f32_bits_equal(wants[0][1][:64], orc.epilogue_rows(d0[:64], acts[0][4], acts[0][3],
@@ -231,6 +253,65 @@ def test_batch_and_plan_over_a_block_match_oracle(amd, orc, dev):
         check(f"plan replay {rep}")
     dev.plan_destroy(plan)
     for b in bufs:
+        b.free()
+
+
+def test_mixed_plan_runs_every_launch_kind(amd, orc, dev):
+    """One plan holding row-group jobs (fused and pre-quantised) and K > 16384
+    jobs that take the streaming kernel after a quantiser launch."""
+    specs = [(300, 2560, True), (64, 65536, True), (50, 16384, False), (129, 6912, True), (33, 20480, False)]
+    jobs, checks, bufs = [], [], []
+    for i, (n_rows, n, fused) in enumerate(specs):
+        w = tensor(amd, amd.synth_seed(3, i, 0, 0), n_rows, n)
+        x = amd.synth_normal(700 + i, n)
+        y_o, q_o, d_o, s_o, t_o = orc.linear(w, n_rows, n, x, orc.DOT_VNNI)
+        bw, bx, bq, ba = dev.put(w), dev.put(x), dev.alloc(n), dev.alloc(8)
+        by, bi = dev.alloc(4 * n_rows), dev.alloc(4 * n_rows)
+        bufs += [bw, bx, bq, ba, by, bi]
+        if fused:
+            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, bx.ptr, bq.ptr, ba.ptr, by.ptr, bi.ptr))
+        else:
+            dev.quant_act(bx.vp, n, 1, bq.vp, ba.vp)
+            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, None, bq.ptr, ba.ptr, by.ptr, bi.ptr))
+        checks.append((by, bi, bq, n_rows, n, y_o, d_o, q_o))
+    try:
+        for geom in [(0, -1, 0, 0, 0)] + FUSED:
+            say("mixed plan", geom)
+            dev.set_tuning(*geom)
+            plan = dev.plan(jobs)
+            for rep in range(2):
+                for by, bi, bq, n_rows, n, y_o, d_o, q_o in checks:
+                    by.upload(np.zeros(n_rows, np.float32))
+                    bi.upload(np.zeros(n_rows, np.int32))
+                dev.plan_run(plan)
+                dev.sync()
+                for by, bi, bq, n_rows, n, y_o, d_o, q_o in checks:
+                    np.testing.assert_array_equal(bi.download(np.int32, n_rows), d_o, err_msg=f"{n_rows}x{n} {geom}")
+                    assert f32_bits_equal(by.download(np.float32, n_rows), y_o), (n_rows, n, geom)
+                    np.testing.assert_array_equal(bq.download(np.int8, n), q_o)
+            dev.plan_destroy(plan)
+    finally:
+        dev.set_tuning()
+    say("mixed batch")
+    dev.gemv_batch(jobs)
+    dev.sync()
+    for by, bi, bq, n_rows, n, y_o, d_o, q_o in checks:
+        np.testing.assert_array_equal(bi.download(np.int32, n_rows), d_o)
+    for b in bufs:
+        b.free()
+
+
+def test_checksum_and_copy_kernels(amd, dev):
+    rng = np.random.default_rng(5)
+    a = rng.integers(0, 2**32, 1 << 20, dtype=np.uint32)
+    src, dst, part = dev.put(a), dev.alloc(a.nbytes), dev.alloc(4 * 64)
+    say("copy / checksum")
+    dev.copy(dst.vp, src.vp, a.nbytes)
+    dev.checksum(src.vp, a.nbytes, part.vp, 64)
+    dev.sync()
+    np.testing.assert_array_equal(dst.download(np.uint32, a.size), a)
+    assert int(np.bitwise_xor.reduce(part.download(np.uint32, 64))) == int(np.bitwise_xor.reduce(a))
+    for b in (src, dst, part):
         b.free()
 
 
@@ -285,7 +366,13 @@ def test_argument_errors_are_reported_not_launched(amd, dev):
     assert lib.sllm_gfx950_gemv(b.vp, 4, 65536 + 128, b.vp, b.vp) == -36  # K above the LDS limit
     assert lib.sllm_gfx950_gemv(b.at(4), 4, 128, b.vp, b.vp) == -1       # misaligned weights
     assert lib.sllm_gfx950_gemv_epilogue(b.vp, 4, 128, b.vp, None, b.vp) == -1
-    assert lib.sllm_gfx950_set_gemv_shape(5, 0, 0) == -1
+    assert lib.sllm_gfx950_set_tuning(0, -1, 5, 0, 0, 0) == -1
+    assert lib.sllm_gfx950_set_tuning(2, -1, 0, 8, 0, 0) == -1         # row-group: <= 4 waves
+    assert lib.sllm_gfx950_set_tuning(1, -1, 0, 0, 0, 1) == -1         # only the row-group kernel fuses
+    x = dev.alloc(4 * 128)
+    job = amd.GemvJob(b.ptr, 4, 128, x.ptr, b.ptr, None, b.ptr, None)  # q without act
+    assert lib.sllm_gfx950_gemv_batch(ctypes.byref(job), 1) == -1
+    x.free()
     assert lib.sllm_gfx950_tensor_register(None, 4, 128) == -1
     b.free()
 
@@ -319,7 +406,7 @@ def test_config1_rotated_sets_match_oracle(amd, orc, dev):
             checks.append((d, orc.epilogue_np(d, t_o, s_o, orc.scale(w, n_rows * n))))
             bw, by, bi = dev.put(w), dev.alloc(4 * n_rows), dev.alloc(4 * n_rows)
             bufs += [bw, by, bi]
-            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, bq.ptr, ba.ptr, by.ptr, bi.ptr))
+            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, None, bq.ptr, ba.ptr, by.ptr, bi.ptr))
     pool.close()
     say("config1 plan", len(jobs))
     plan = dev.plan(jobs)
