@@ -137,17 +137,19 @@ int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n,
 
 /* One projection as src/forward.c:651-655 performs it: quantise x (n
  * floats), GEMV, epilogue into out (n_rows floats). q / act, when not NULL,
- * receive the quantised row and its scale/sum (give both or neither). By
- * default this is a quantiser launch then the GEMV; with fuse_quant set (see
- * sllm_gfx950_set_tuning) the row-group kernel quantises x in LDS itself --
- * the same operations, so the same bits -- in a single launch. */
+ * receive the quantised row and its scale/sum (give both or neither). For
+ * K <= 7168 this is one launch: the slab kernel quantises x in LDS itself
+ * (the quantiser's operations, so the same bits); larger K (or the
+ * streaming path forced with sllm_gfx950_set_tuning) runs a quantiser
+ * launch first. */
 int sllm_gfx950_linear(const uint8_t *w, size_t n_rows, size_t n, const float *x,
                        int8_t *q, sllm_gfx950_act *act, float *out);
 
 /* One independent GEMV of a batch.
  *   x != NULL: x is quantised per token (as sllm_gfx950_linear); q / act
- *              are optional outputs (both or neither). Jobs sharing one x
- *              (Q/K/V, gate/up) share one quantisation.
+ *              are optional outputs (both or neither), written once per
+ *              job. Every job quantises its own x, with identical bits for
+ *              jobs sharing one x (Q/K/V, gate/up).
  *   x == NULL: q / act are inputs (act only needed for out).
  * out and/or rows_out may be NULL, not both. Device pointers, 16-byte
  * aligned. */
@@ -163,9 +165,10 @@ typedef struct sllm_gfx950_gemv_job {
 } sllm_gfx950_gemv_job;
 
 /* Run independent GEMVs (Q, K and V against one activation, gate and up,
- * or many layers' matrices) in one launch (two when some K > 16384). The
- * job tables are built and uploaded on each call, and the call waits for
- * the stream before freeing them; a plan uploads them once. */
+ * or many layers' matrices) in one launch when every K <= 7168 (else also a
+ * quantiser and a streaming launch). The job tables are built and uploaded
+ * on each call, and the call waits for the stream before freeing them; a
+ * plan uploads them once. */
 int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs);
 
 typedef struct sllm_gfx950_plan sllm_gfx950_plan;
@@ -173,23 +176,24 @@ int  sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
                              sllm_gfx950_plan **plan);
 int  sllm_gfx950_plan_run(const sllm_gfx950_plan *plan);
 /* plan_run that also records numbered event `event` (see
- * sllm_gfx950_event_record) between the quantiser launch and the GEMV
- * launches, so each can be timed on the stream it runs on. */
+ * sllm_gfx950_event_record) between the quantiser launch (present only for
+ * streaming jobs carrying x) and the GEMV launches, so each can be timed on
+ * the stream it runs on. */
 int  sllm_gfx950_plan_run_marked(const sllm_gfx950_plan *plan, int event);
 void sllm_gfx950_plan_destroy(sllm_gfx950_plan *plan);
 
 /* Launch-geometry override for tuning sweeps and tests; affects launches
  * and plans created afterwards. All zero (variant -1) is automatic.
- *   path           0 auto (streaming), 1 streaming kernel,
- *                  2 row-group kernel (K <= 16384; larger K always streams)
- *   variant        row-group geometry 0..3 (used when it covers K), -1 auto
+ *   path           0 auto and 2: slab kernel for K <= 7168, streaming kernel
+ *                  above; 1: streaming kernel for every K
+ *   variant        slab geometry: 0 (8 lanes x 5 chunks per row) or 1
+ *                  (16 x 7), used when it covers K; -1 auto
  *   lanes_per_row  streaming kernel: 4, 8 or 16
- *   waves          waves per workgroup: 1..4 row-group, 1..16 streaming
- *   rows_per_wg    rows per workgroup
- *   fuse_quant     1: jobs carrying x are quantised inside the row-group
- *                  kernel (one launch); 0: by a quantiser launch first */
+ *   waves          streaming kernel: waves per workgroup, 1..16
+ *   rows_per_wg    streaming kernel: rows per workgroup
+ *   slab_kib       slab kernel: KiB of packed weights per workgroup */
 int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, int rows_per_wg,
-                           int fuse_quant);
+                           int slab_kib);
 
 /* ------------------------------------------------------------------ */
 /* host-pointer kernel row (the reference's signatures)                */

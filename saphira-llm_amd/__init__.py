@@ -274,8 +274,8 @@ class Device:
     def plan_destroy(self, p):
         self.lib.sllm_gfx950_plan_destroy(p)
 
-    def set_tuning(self, path=0, variant=-1, lanes_per_row=0, waves=0, rows_per_wg=0, fuse_quant=0):
-        check(self.lib.sllm_gfx950_set_tuning(path, variant, lanes_per_row, waves, rows_per_wg, fuse_quant),
+    def set_tuning(self, path=0, variant=-1, lanes_per_row=0, waves=0, rows_per_wg=0, slab_kib=0):
+        check(self.lib.sllm_gfx950_set_tuning(path, variant, lanes_per_row, waves, rows_per_wg, slab_kib),
               "set_tuning")
 
 

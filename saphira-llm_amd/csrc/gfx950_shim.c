@@ -56,22 +56,29 @@ typedef struct k_gemv_job {
     int32_t               *out_i;
     uint32_t               n_rows;
     uint32_t               k;
-    uint32_t               wg_begin;
-    uint32_t               rows_per_wg;
     uint32_t               variant;
     uint32_t               pad;
 } k_gemv_job;
 
-_Static_assert(sizeof(k_gemv_job) == 72, "k_gemv_job must match gemv_job in i2s_kernels.hip");
+/* One workgroup's share of a job (mirror of wg_desc): slab a of b slabs for
+ * the slab kernel, rows [a, b) for the streaming kernel. */
+typedef struct k_wg_desc {
+    uint32_t job;
+    uint32_t a;
+    uint32_t b;
+    uint32_t flags;
+} k_wg_desc;
+
+enum { WG_PUBLISH = 1 };
+
+_Static_assert(sizeof(k_gemv_job) == 64, "k_gemv_job must match gemv_job in i2s_kernels.hip");
+_Static_assert(sizeof(k_wg_desc) == 16, "k_wg_desc must match wg_desc in i2s_kernels.hip");
 _Static_assert(sizeof(sllm_gfx950_act) == 8, "sllm_gfx950_act must match sllm_i2s_act");
 
 enum { LPR_4 = 0, LPR_8 = 1, LPR_16 = 2, N_LPR = 3 };
 static const int k_lpr_value[N_LPR] = { 4, 8, 16 };
-static const char *const k_gemv_names[N_LPR] = {
-    "sllm_k_gemv_l4", "sllm_k_gemv_l8", "sllm_k_gemv_l16"
-};
-static const char *const k_group_names[N_LPR] = {
-    "sllm_k_gemv_group_l4", "sllm_k_gemv_group_l8", "sllm_k_gemv_group_l16"
+static const char *const k_stream_names[N_LPR] = {
+    "sllm_k_gemv_stream_l4", "sllm_k_gemv_stream_l8", "sllm_k_gemv_stream_l16"
 };
 
 #define QUANT_THREADS 256
@@ -98,16 +105,18 @@ typedef struct k_quant_job {
 _Static_assert(sizeof(k_quant_job) == 32, "k_quant_job must match quant_job in i2s_kernels.hip");
 
 /*
- * A batch of GEMVs as launches: one list-quantiser launch for every distinct
- * activation the batch quantises, the row-group kernel classes, then the
- * streaming kernel. Device tables: quant list, rg class 0, 1, 2, stream.
+ * A batch of GEMVs as launches: one list-quantiser launch for the distinct
+ * activations of streaming jobs that carry f32 x, one slab launch, one
+ * streaming launch. Device tables, in this order: quant list, jobs, slab
+ * workgroup descriptors, streaming workgroup descriptors.
  */
 struct sllm_gfx950_plan {
     void      *tables_dev;
-    void      *scratch_dev;    /* q / act of jobs that quantise without giving buffers */
+    void      *scratch_dev;    /* q / act of streaming jobs that quantise without giving buffers */
     uint32_t   n_quant;
-    uint32_t   n_rg[3], rg_wg[3], rg_lds[3], rg_threads;
-    uint32_t   n_st, st_wg, st_lds, st_threads;
+    uint32_t   n_jobs;
+    uint32_t   slab_wg;        /* multiple of 8 (empty descriptors pad it) */
+    uint32_t   st_wg, st_lds, st_threads;
     int        st_lpr_idx;
 };
 
@@ -119,9 +128,8 @@ static struct {
     char           name[520];
     hipModule_t    mod;
     hipFunction_t  k_quant, k_quant_list;
-    hipFunction_t  k_gemv[N_LPR];
-    hipFunction_t  k_group[N_LPR];
-    hipFunction_t  k_rg[3], k_rg_group[3];
+    hipFunction_t  k_slab;
+    hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -129,7 +137,7 @@ static struct {
     hipEvent_t    *events;
     int            n_events;
     /* tuning overrides (0 / -1 = automatic) */
-    int            force_path, force_variant, force_lpr, force_waves, force_rows, fuse_quant;
+    int            force_path, force_variant, force_lpr, force_waves, force_rows, slab_kib;
     /* q / act for sllm_gfx950_linear when the caller gives none */
     void          *lin_scratch;
     /* registry for the host-pointer row */
@@ -187,17 +195,8 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_quant_list, g.mod, "sllm_k_quant_list"));
     HIP_TRY(hipModuleGetFunction(&g.k_copy, g.mod, "sllm_k_copy"));
     HIP_TRY(hipModuleGetFunction(&g.k_checksum, g.mod, "sllm_k_checksum"));
-    for (int i = 0; i < N_LPR; ++i) {
-        HIP_TRY(hipModuleGetFunction(&g.k_gemv[i], g.mod, k_gemv_names[i]));
-        HIP_TRY(hipModuleGetFunction(&g.k_group[i], g.mod, k_group_names[i]));
-    }
-    for (int c = 0; c < 3; ++c) {
-        char name[64];
-        snprintf(name, sizeof name, "sllm_k_gemv_rg_c%d", c);
-        HIP_TRY(hipModuleGetFunction(&g.k_rg[c], g.mod, name));
-        snprintf(name, sizeof name, "sllm_k_gemv_rg_group_c%d", c);
-        HIP_TRY(hipModuleGetFunction(&g.k_rg_group[c], g.mod, name));
-    }
+    HIP_TRY(hipModuleGetFunction(&g.k_slab, g.mod, "sllm_k_gemv_slab"));
+    for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
 }
@@ -449,60 +448,64 @@ int sllm_gfx950_quant_act(const float *x, size_t n, size_t n_tok, int8_t *q,
 /*
  * Launch geometry.
  *
- * Streaming kernel (default, any K): LPR lanes per row, W waves looping over
- * groups of 64/LPR rows inside a slab of rows_per_wg rows; the activation is
- * a quantised row staged in LDS, so jobs that carry f32 x are quantised
- * first by one list-quantiser launch per batch. Measured on the BitNet-2B
- * FFN shapes, small short-lived workgroups (LPR 8, 2 waves, 32 rows) stream
- * fastest.
+ * Slab kernel (K <= SLAB_MAX_K: every BitNet-2B projection; the default):
+ * blocks of four waves, each owning a slab of consecutive rows of one job
+ * (whole groups of 4 * 64/LPR rows), sized to about slab_kib KiB of packed
+ * weights so that every workgroup streams the same bytes. The geometry
+ * follows K: variant 0 runs 8 lanes x 5 chunks per row
+ * (K <= 2560), variant 1 16 lanes x 7 chunks (K <= 7168). A job carrying
+ * f32 x is quantised inside the kernel: no quantiser launch.
  *
- * Row-group kernel (path 2, K <= RG_MAX_K): a job's variant fixes (LPR,
- * CPL chunks per lane) by its K class, compiled into three kernel classes
- * (0: variants 0-1, 1: variant 2, 2: variant 3); a block of W waves walks
- * rows_per_wg rows double-buffered. With fuse_quant it quantises x itself
- * (one launch, no quantiser), which pays off only when launches dominate.
+ * Streaming kernel (larger K, or forced with path 1): LPR lanes per row, W
+ * waves looping over groups of 64/LPR rows inside a slab of rows_per_wg rows,
+ * reading a quantised row staged in LDS; jobs carrying f32 x are quantised
+ * first, by one list-quantiser launch per batch.
+ *
+ * Batches describe every workgroup with a (job, rows) descriptor, padded
+ * with empty ones to a multiple of 8 so that the kernel can hand each XCD a
+ * contiguous eighth of the table.
  */
-#define RG_MAX_K 16384
-#define RG_DEFAULT_WAVES 2
-#define RG_DEFAULT_ROWS 64
+#define SLAB_THREADS     256
+#define SLAB_MAX_K       7168
+#define SLAB_MAX_ROWS    1024
+#define SLAB_DEFAULT_KIB 128
 
-typedef struct rg_geom { int lpr, cpl, cls; } rg_geom;
-static const rg_geom k_rg_geom[4] = { { 8, 5, 0 }, { 16, 7, 0 }, { 8, 14, 1 }, { 16, 16, 2 } };
+typedef struct slab_geom { int lpr, cpl; } slab_geom;
+static const slab_geom k_slab_geom[2] = { { 8, 5 }, { 16, 7 } };
 
-/* variants 0, 1, 3 cover every K <= RG_MAX_K; 2 is only used when forced */
-static int rg_variant_for(size_t k) {
+static int slab_variant_for(size_t k) {
     const size_t chunks = k / 64;
     if (g.force_variant >= 0) {
-        const rg_geom *v = &k_rg_geom[g.force_variant];
+        const slab_geom *v = &k_slab_geom[g.force_variant];
         if ((size_t) v->lpr * (size_t) v->cpl >= chunks) return g.force_variant;
     }
-    static const int order[3] = { 0, 1, 3 };
-    for (int i = 0; i < 3; ++i) {
-        const rg_geom *v = &k_rg_geom[order[i]];
-        if ((size_t) v->lpr * (size_t) v->cpl >= chunks) return order[i];
+    for (int i = 0; i < 2; ++i) {
+        if ((size_t) k_slab_geom[i].lpr * (size_t) k_slab_geom[i].cpl >= chunks) return i;
     }
     return -1;
 }
 
-/* the row-group kernels are compiled for blocks of at most 4 waves */
-static int rg_waves(void) {
-    const int w = g.force_waves ? g.force_waves : RG_DEFAULT_WAVES;
-    return w > 4 ? 4 : w;
+/* does a job of this shape take the slab kernel (else the streaming one) */
+static int slab_path(size_t n_rows, size_t k) {
+    if (g.force_path == 1 || k > SLAB_MAX_K) return 0;
+    /* the slab kernel addresses a tensor with 32-bit offsets */
+    return (uint64_t) n_rows * (k / 4) + 32 <= UINT32_MAX;
 }
 
-static uint32_t rg_rows_per_wg(void) {
-    return g.force_rows ? (uint32_t) g.force_rows : RG_DEFAULT_ROWS;
+/* Slabs of a job: about slab_kib KiB of weights each, at least one group
+ * each, and few enough groups per slab for its dots to fit in LDS. */
+static uint32_t slab_count(size_t n_rows, size_t k, int variant) {
+    const uint64_t target = (uint64_t) (g.slab_kib ? g.slab_kib : SLAB_DEFAULT_KIB) * 1024u;
+    const uint64_t group = 4u * (uint64_t) (64 / k_slab_geom[variant].lpr);
+    const uint64_t n_groups = (n_rows + group - 1) / group;
+    const uint64_t max_groups = SLAB_MAX_ROWS / group;
+    uint64_t slabs = ((uint64_t) n_rows * (k / 4) + target / 2) / target;
+    if (slabs < (n_groups + max_groups - 1) / max_groups) slabs = (n_groups + max_groups - 1) / max_groups;
+    if (slabs > n_groups) slabs = n_groups;
+    if (slabs == 0) slabs = 1;
+    return (uint32_t) slabs;
 }
 
-/* path for a job of width k: 2 = row-group kernel, 1 = streaming kernel */
-static int path_for(size_t k) {
-    if (k > RG_MAX_K) return 1;
-    if (g.force_path == 2 || g.fuse_quant) return 2;
-    return 1;
-}
-
-/* does a job carrying x quantise inside the GEMV (else: list quantiser first) */
-static int fused_for(size_t k) { return g.fuse_quant && path_for(k) == 2; }
 
 typedef struct stream_shape {
     int      lpr_idx;
@@ -525,23 +528,21 @@ static stream_shape stream_shape_for(void) {
 }
 
 int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, int rows_per_wg,
-                           int fuse_quant) {
-    if (path < 0 || path > 2) return fail(SLLM_GFX950_ERR_ARG, "path must be 0 (auto), 1 (stream) or 2 (row-group)");
-    if (variant < -1 || variant > 3) return fail(SLLM_GFX950_ERR_ARG, "variant must be -1 (auto) or 0..3");
+                           int slab_kib) {
+    if (path < 0 || path > 2) return fail(SLLM_GFX950_ERR_ARG, "path must be 0 (auto), 1 (streaming) or 2 (slab)");
+    if (variant < -1 || variant > 1) return fail(SLLM_GFX950_ERR_ARG, "slab variant must be -1 (auto), 0 or 1");
     if (lanes_per_row != 0 && lpr_index(lanes_per_row) < 0) {
         return fail(SLLM_GFX950_ERR_ARG, "lanes per row must be 4, 8 or 16");
     }
     if (waves < 0 || waves > 16) return fail(SLLM_GFX950_ERR_ARG, "waves must be 0..16");
-    if ((path == 2 || fuse_quant) && waves > 4) return fail(SLLM_GFX950_ERR_ARG, "the row-group kernel takes at most 4 waves");
     if (rows_per_wg < 0) return fail(SLLM_GFX950_ERR_ARG, "rows per workgroup must be >= 0");
-    if (fuse_quant < 0 || fuse_quant > 1) return fail(SLLM_GFX950_ERR_ARG, "fuse_quant must be 0 or 1");
-    if (fuse_quant && path == 1) return fail(SLLM_GFX950_ERR_ARG, "only the row-group kernel quantises in-kernel");
+    if (slab_kib < 0 || slab_kib > 65536) return fail(SLLM_GFX950_ERR_ARG, "slab KiB must be 0..65536");
     g.force_path = path;
     g.force_variant = variant;
     g.force_lpr = lanes_per_row;
     g.force_waves = waves;
     g.force_rows = rows_per_wg;
-    g.fuse_quant = fuse_quant;
+    g.slab_kib = slab_kib;
     return SLLM_GFX950_OK;
 }
 
@@ -554,7 +555,7 @@ static int check_weights(const uint8_t *w, size_t n_rows, size_t n) {
     return SLLM_GFX950_OK;
 }
 
-/* Validate one public job and translate it (geometry filled later). */
+/* Validate one public job and translate it (variant filled in later). */
 static int job_to_kernel(const sllm_gfx950_gemv_job *j, size_t i, k_gemv_job *kj) {
     int st = check_weights(j->w, j->n_rows, j->n);
     if (st != SLLM_GFX950_OK) return st;
@@ -568,15 +569,15 @@ static int job_to_kernel(const sllm_gfx950_gemv_job *j, size_t i, k_gemv_job *kj
         if (j->out != NULL && j->act == NULL) return fail(SLLM_GFX950_ERR_ARG, "job %zu: the epilogue needs act", i);
     }
     *kj = (k_gemv_job) { j->w, j->x, j->q, j->act, j->out, j->rows_out, (uint32_t) j->n_rows,
-                         (uint32_t) j->n, 0, 0, 0, 0 };
+                         (uint32_t) j->n, 0, 0 };
     return SLLM_GFX950_OK;
 }
 
 static size_t align256(size_t v) { return (v + 255u) & ~(size_t) 255u; }
 
-/* jobs that quantise x into plan scratch (carry x, no q / act, not fused) */
+/* streaming jobs that quantise x into plan scratch (carry x, no q / act) */
 static int takes_scratch(const sllm_gfx950_gemv_job *j) {
-    return j->x != NULL && j->q == NULL && !fused_for(j->n);
+    return j->x != NULL && j->q == NULL && !slab_path(j->n_rows, j->n);
 }
 
 /* scratch bytes for one quantised row of width k: q, then act */
@@ -595,84 +596,102 @@ static size_t plan_scratch_bytes(const sllm_gfx950_gemv_job *jobs, size_t n_jobs
     return bytes;
 }
 
+/* workgroups a job takes (streaming: and the rows each one owns) */
+static uint32_t job_workgroups(const k_gemv_job *kj, int slab, uint32_t *rows) {
+    if (slab) {
+        *rows = 0;
+        return slab_count(kj->n_rows, kj->k, (int) kj->variant);
+    }
+    *rows = stream_shape_for().rows_per_wg;
+    return (kj->n_rows + *rows - 1) / *rows;
+}
+
+static uint64_t pad8(uint64_t v) { return (v + 7u) & ~(uint64_t) 7u; }
+
 /*
- * Lay a batch out as launches. `kq` (n_jobs entries) receives the quant list:
- * one row per distinct (x, q) among jobs that carry x and are not fused --
- * into the job's q / act, or into plan scratch (p->scratch_dev, sized by
- * plan_scratch_bytes) shared by every scratch job with the same (x, K).
- * `tab` receives the GEMV tables in launch order (rg class 0, 1, 2, stream;
- * each launch's wg_begin counts from 0); `tmp` / `launch_of` are scratch.
+ * Lay a batch out. `kj` (n_jobs entries) receives the jobs in submission
+ * order -- streaming jobs that carried x now read their quantised row -- and
+ * `kq` (n_jobs entries) the quant list: one row per distinct (x, q) among
+ * streaming jobs that carry x, into the job's q / act or into plan scratch
+ * (p->scratch_dev, sized by plan_scratch_bytes) shared by every scratch job
+ * with the same (x, K). Sets the plan's counts; the descriptors are written
+ * by plan_descriptors.
  */
 static int plan_layout(const sllm_gfx950_gemv_job *jobs, size_t n_jobs, sllm_gfx950_plan *p,
-                       k_quant_job *kq, k_gemv_job *tab, k_gemv_job *tmp, uint8_t *launch_of) {
+                       k_quant_job *kq, k_gemv_job *kj, uint8_t *is_slab) {
     const stream_shape ss = stream_shape_for();
-    uint64_t wg[4] = { 0, 0, 0, 0 };
-    size_t lds[4] = { 0, 0, 0, 0 };
-    uint32_t count[4] = { 0, 0, 0, 0 };
-    size_t scratch_at = 0;
+    uint64_t slab_wg = 0, st_wg = 0;
+    size_t st_lds = 0, scratch_at = 0;
     p->n_quant = 0;
     for (size_t i = 0; i < n_jobs; ++i) {
-        k_gemv_job kj;
-        int st = job_to_kernel(&jobs[i], i, &kj);
+        k_gemv_job *j = &kj[i];
+        int st = job_to_kernel(&jobs[i], i, j);
         if (st != SLLM_GFX950_OK) return st;
-        if (kj.x != NULL && !fused_for(kj.k)) {
-            const int scratch = kj.q == NULL;
+        is_slab[i] = (uint8_t) slab_path(j->n_rows, j->k);
+        if (is_slab[i]) {
+            j->variant = (uint32_t) slab_variant_for(j->k);
+        } else if (j->x != NULL) {
+            const int scratch = j->q == NULL;
             uint32_t e = 0;
             for (; e < p->n_quant; ++e) {
-                if (kq[e].x != kj.x || kq[e].n != kj.k || (int) kq[e].pad != scratch) continue;
-                if (scratch || kq[e].q == kj.q) break;
+                if (kq[e].x != j->x || kq[e].n != j->k || (int) kq[e].pad != scratch) continue;
+                if (scratch || kq[e].q == j->q) break;
             }
             if (e == p->n_quant) {
                 if (scratch) {
                     uint8_t *row = (uint8_t *) p->scratch_dev + scratch_at;
-                    scratch_at += row_scratch(kj.k);
-                    kq[e] = (k_quant_job) { kj.x, (int8_t *) row,
-                                            (sllm_gfx950_act *) (row + align256(kj.k)), kj.k, 1 };
+                    scratch_at += row_scratch(j->k);
+                    kq[e] = (k_quant_job) { j->x, (int8_t *) row,
+                                            (sllm_gfx950_act *) (row + align256(j->k)), j->k, 1 };
                 } else {
-                    kq[e] = (k_quant_job) { kj.x, kj.q, kj.act, kj.k, 0 };
+                    kq[e] = (k_quant_job) { j->x, j->q, j->act, j->k, 0 };
                 }
                 p->n_quant++;
             }
-            kj.q = kq[e].q;             /* the GEMV reads the quantised row */
-            kj.act = kq[e].act;
-            kj.x = NULL;
+            j->q = kq[e].q;             /* the GEMV reads the quantised row */
+            j->act = kq[e].act;
+            j->x = NULL;
         }
-        int l;
-        if (path_for(kj.k) == 2) {
-            const int v = rg_variant_for(kj.k);
-            kj.variant = (uint32_t) v;
-            kj.rows_per_wg = rg_rows_per_wg();
-            l = k_rg_geom[v].cls;
+        uint32_t rows;
+        const uint64_t wg = job_workgroups(j, is_slab[i], &rows);
+        if (is_slab[i]) {
+            slab_wg += wg;
         } else {
-            kj.rows_per_wg = ss.rows_per_wg;
-            l = 3;
+            st_wg += wg;
+            if (j->k > st_lds) st_lds = j->k;
         }
-        kj.wg_begin = (uint32_t) wg[l];
-        wg[l] += (kj.n_rows + kj.rows_per_wg - 1) / kj.rows_per_wg;
-        if (kj.k > lds[l]) lds[l] = kj.k;
-        count[l]++;
-        launch_of[i] = (uint8_t) l;
-        tmp[i] = kj;
     }
-    for (int l = 0; l < 4; ++l) {
-        if (wg[l] > UINT32_MAX) return fail(SLLM_GFX950_ERR_TOO_LARGE, "batch: too many workgroups");
-    }
-    size_t at = 0;
-    for (int l = 0; l < 4; ++l) {
-        for (size_t i = 0; i < n_jobs; ++i) if (launch_of[i] == l) tab[at++] = tmp[i];
-    }
-    for (int c = 0; c < 3; ++c) {
-        p->n_rg[c] = count[c];
-        p->rg_wg[c] = (uint32_t) wg[c];
-        p->rg_lds[c] = (uint32_t) lds[c];
-    }
-    p->rg_threads = (uint32_t) (64 * rg_waves());
-    p->n_st = count[3];
-    p->st_wg = (uint32_t) wg[3];
-    p->st_lds = (uint32_t) lds[3];
+    slab_wg = pad8(slab_wg);
+    st_wg = pad8(st_wg);
+    if (slab_wg > INT32_MAX || st_wg > INT32_MAX) return fail(SLLM_GFX950_ERR_TOO_LARGE, "batch: too many workgroups");
+    p->n_jobs = (uint32_t) n_jobs;
+    p->slab_wg = (uint32_t) slab_wg;
+    p->st_wg = (uint32_t) st_wg;
+    p->st_lds = (uint32_t) st_lds;
     p->st_threads = (uint32_t) (64 * ss.waves);
     p->st_lpr_idx = ss.lpr_idx;
     return SLLM_GFX950_OK;
+}
+
+/* One descriptor per workgroup: slab jobs into sd, streaming jobs into td,
+ * each in job order and padded with empty descriptors. */
+static void plan_descriptors(const sllm_gfx950_plan *p, const k_gemv_job *kj, const uint8_t *is_slab,
+                             k_wg_desc *sd, k_wg_desc *td) {
+    uint32_t ns = 0, nt = 0;
+    for (uint32_t i = 0; i < p->n_jobs; ++i) {
+        uint32_t rows;
+        const uint32_t wg = job_workgroups(&kj[i], is_slab[i], &rows);
+        for (uint32_t w = 0; w < wg; ++w) {
+            if (is_slab[i]) {
+                sd[ns++] = (k_wg_desc) { i, w, wg, w == 0 ? WG_PUBLISH : 0 };
+            } else {
+                const uint32_t b = w * rows, e = b + rows < kj[i].n_rows ? b + rows : kj[i].n_rows;
+                td[nt++] = (k_wg_desc) { i, b, e, 0 };
+            }
+        }
+    }
+    while (ns < p->slab_wg) sd[ns++] = (k_wg_desc) { 0, 0, 0, 0 };
+    while (nt < p->st_wg) td[nt++] = (k_wg_desc) { 0, 0, 0, 0 };
 }
 
 static int launch_quant(const float *x, uint32_t n, uint32_t n_tok, int8_t *q, sllm_gfx950_act *act) {
@@ -682,25 +701,28 @@ static int launch_quant(const float *x, uint32_t n, uint32_t n_tok, int8_t *q, s
 
 static int plan_launch(const sllm_gfx950_plan *p, int event) {
     int st = SLLM_GFX950_OK;
-    const k_quant_job *kq = p->tables_dev;
+    const uint8_t *base = p->tables_dev;
+    const k_quant_job *kq = (const k_quant_job *) base;
+    const k_gemv_job *jobs = (const k_gemv_job *) (base + p->n_quant * sizeof(k_quant_job));
+    const k_wg_desc *sd = (const k_wg_desc *) (jobs + p->n_jobs);
+    const k_wg_desc *td = sd + p->slab_wg;
+    k_gemv_job none;
+    memset(&none, 0, sizeof none);
+    uint32_t zero = 0;
     if (p->n_quant) {
         void *args[] = { (void *) &kq };
         st = launch(g.k_quant_list, p->n_quant, QUANT_THREADS, 0, args);
     }
     if (st == SLLM_GFX950_OK && event >= 0) st = sllm_gfx950_event_record(event);
-    const k_gemv_job *t = (const k_gemv_job *) (kq + p->n_quant);
-    for (int c = 0; c < 3 && st == SLLM_GFX950_OK; ++c) {
-        if (p->n_rg[c]) {
-            uint32_t n = p->n_rg[c];
-            void *args[] = { (void *) &t, &n };
-            st = launch(g.k_rg_group[c], p->rg_wg[c], p->rg_threads, p->rg_lds[c], args);
-            t += p->n_rg[c];
-        }
+    if (st == SLLM_GFX950_OK && p->slab_wg) {
+        uint32_t n = p->slab_wg;
+        void *args[] = { (void *) &jobs, (void *) &sd, &n, &none, &zero };
+        st = launch(g.k_slab, p->slab_wg, SLAB_THREADS, 0, args);
     }
-    if (st == SLLM_GFX950_OK && p->n_st) {
-        uint32_t n = p->n_st;
-        void *args[] = { (void *) &t, &n };
-        st = launch(g.k_group[p->st_lpr_idx], p->st_wg, p->st_threads, p->st_lds, args);
+    if (st == SLLM_GFX950_OK && p->st_wg) {
+        uint32_t n = p->st_wg;
+        void *args[] = { (void *) &jobs, (void *) &td, &n, &none, &zero };
+        st = launch(g.k_stream[p->st_lpr_idx], p->st_wg, p->st_threads, p->st_lds, args);
     }
     return st;
 }
@@ -710,14 +732,14 @@ int sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
     NEED_OPEN();
     if (plan == NULL) return fail(SLLM_GFX950_ERR_ARG, "plan: NULL out pointer");
     *plan = NULL;
-    if (jobs == NULL || n_jobs == 0 || n_jobs > UINT32_MAX) return fail(SLLM_GFX950_ERR_ARG, "plan: bad job list");
+    if (jobs == NULL || n_jobs == 0 || n_jobs > UINT32_MAX / 2) return fail(SLLM_GFX950_ERR_ARG, "plan: bad job list");
     sllm_gfx950_plan *p = calloc(1, sizeof *p);
     k_quant_job *kq = malloc(n_jobs * sizeof *kq);
-    k_gemv_job *tab = malloc(n_jobs * sizeof *tab);
-    k_gemv_job *tmp = malloc(n_jobs * sizeof *tmp);
-    uint8_t *launch_of = malloc(n_jobs);
+    k_gemv_job *kj = malloc(n_jobs * sizeof *kj);
+    uint8_t *is_slab = malloc(n_jobs);
+    uint8_t *host = NULL;
     int st = SLLM_GFX950_OK;
-    if (p == NULL || kq == NULL || tab == NULL || tmp == NULL || launch_of == NULL) {
+    if (p == NULL || kq == NULL || kj == NULL || is_slab == NULL) {
         st = fail(SLLM_GFX950_ERR_NOMEM, "plan: host tables");
     }
     if (st == SLLM_GFX950_OK) {
@@ -727,24 +749,27 @@ int sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
             if (e != hipSuccess) st = hip_fail(e, "plan: activation scratch");
         }
     }
-    if (st == SLLM_GFX950_OK) st = plan_layout(jobs, n_jobs, p, kq, tab, tmp, launch_of);
+    if (st == SLLM_GFX950_OK) st = plan_layout(jobs, n_jobs, p, kq, kj, is_slab);
     if (st == SLLM_GFX950_OK) {
-        const size_t qbytes = p->n_quant * sizeof *kq, bytes = qbytes + n_jobs * sizeof *tab;
-        uint8_t *host = malloc(bytes);
+        const size_t qbytes = p->n_quant * sizeof *kq, jbytes = n_jobs * sizeof *kj;
+        const size_t dbytes = ((size_t) p->slab_wg + p->st_wg) * sizeof(k_wg_desc);
+        const size_t bytes = qbytes + jbytes + dbytes;
+        host = malloc(bytes);
         if (host == NULL) st = fail(SLLM_GFX950_ERR_NOMEM, "plan: table staging");
         if (st == SLLM_GFX950_OK) {
             memcpy(host, kq, qbytes);
-            memcpy(host + qbytes, tab, n_jobs * sizeof *tab);
+            memcpy(host + qbytes, kj, jbytes);
+            k_wg_desc *sd = (k_wg_desc *) (host + qbytes + jbytes);
+            plan_descriptors(p, kj, is_slab, sd, sd + p->slab_wg);
             hipError_t e = hipMalloc(&p->tables_dev, bytes);
             if (e == hipSuccess) e = hipMemcpy(p->tables_dev, host, bytes, hipMemcpyHostToDevice);
             if (e != hipSuccess) st = hip_fail(e, "plan: job tables");
         }
-        free(host);
     }
+    free(host);
     free(kq);
-    free(tab);
-    free(tmp);
-    free(launch_of);
+    free(kj);
+    free(is_slab);
     if (st != SLLM_GFX950_OK) {
         if (p) {
             if (p->tables_dev) hipFree(p->tables_dev);
@@ -792,15 +817,25 @@ int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
     return st;
 }
 
-/* One job, passed by value to the single-job entry points. A job carrying
- * x is quantised first (into its q / act, or the library's row scratch)
- * unless the row-group kernel quantises in-kernel. */
+/* One job, passed to the kernel by value (no descriptor table). A
+ * streaming job carrying x is quantised first (into its q / act, or the
+ * library's row scratch); the slab kernel quantises in-kernel. */
 static int single_launch(const sllm_gfx950_gemv_job *j) {
     k_gemv_job kj;
     int st = job_to_kernel(j, 0, &kj);
     if (st != SLLM_GFX950_OK) return st;
     if (kj.n_rows == 0) return SLLM_GFX950_OK;
-    if (kj.x != NULL && !fused_for(kj.k)) {
+    const k_gemv_job *no_jobs = NULL;
+    const k_wg_desc *no_descs = NULL;
+    uint32_t zero = 0;
+    if (slab_path(kj.n_rows, kj.k)) {
+        kj.variant = (uint32_t) slab_variant_for(kj.k);
+        uint32_t rows, flags = 0;
+        const uint32_t wg = job_workgroups(&kj, 1, &rows);
+        void *args[] = { (void *) &no_jobs, (void *) &no_descs, &zero, &kj, &flags };
+        return launch(g.k_slab, wg, SLAB_THREADS, 0, args);
+    }
+    if (kj.x != NULL) {
         if (kj.q == NULL) {
             kj.q = (int8_t *) g.lin_scratch;
             kj.act = (sllm_gfx950_act *) ((uint8_t *) g.lin_scratch + SLLM_GFX950_MAX_K);
@@ -809,19 +844,11 @@ static int single_launch(const sllm_gfx950_gemv_job *j) {
         if (st != SLLM_GFX950_OK) return st;
         kj.x = NULL;
     }
-    if (path_for(kj.k) == 2) {
-        const int v = rg_variant_for(kj.k);
-        kj.variant = (uint32_t) v;
-        kj.rows_per_wg = rg_rows_per_wg();
-        void *args[] = { &kj };
-        return launch(g.k_rg[k_rg_geom[v].cls], (kj.n_rows + kj.rows_per_wg - 1) / kj.rows_per_wg,
-                      (uint32_t) (64 * rg_waves()), kj.k, args);
-    }
     const stream_shape ss = stream_shape_for();
-    kj.rows_per_wg = ss.rows_per_wg;
-    void *args[] = { &kj };
-    return launch(g.k_gemv[ss.lpr_idx], (kj.n_rows + kj.rows_per_wg - 1) / kj.rows_per_wg,
-                  (uint32_t) (64 * ss.waves), kj.k, args);
+    uint32_t rows;
+    const uint32_t wg = job_workgroups(&kj, 0, &rows);
+    void *args[] = { (void *) &no_jobs, (void *) &no_descs, &zero, &kj, &rows };
+    return launch(g.k_stream[ss.lpr_idx], wg, (uint32_t) (64 * ss.waves), kj.k, args);
 }
 
 int sllm_gfx950_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,

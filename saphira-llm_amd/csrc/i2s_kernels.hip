@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -187,7 +188,7 @@ __device__ __forceinline__ int finish(const dot4acc &acc) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMV jobs
+// GEMV jobs and workgroup descriptors
 // ---------------------------------------------------------------------------
 
 struct gemv_job {
@@ -199,100 +200,290 @@ struct gemv_job {
     int32_t       *out_i;      // raw int32 dots, or null
     uint32_t       n_rows;     // N
     uint32_t       k;          // K, a multiple of 128
-    uint32_t       wg_begin;   // first workgroup of this job (group launches)
-    uint32_t       rows_per_wg;
-    uint32_t       variant;    // row-group geometry (row-group kernel only)
+    uint32_t       variant;    // slab kernel geometry: 0 = (8 lanes, 5 chunks), 1 = (16, 7)
     uint32_t       pad;
 };
 
-// w_scale / act_scale, the epilogue's once-per-column factor (i2s_gemm.c:288)
-__device__ __forceinline__ float epilogue_post(const gemv_job &job, float act_scale) {
-    const float ws = *G_CAST(const float, job.w + (size_t) job.n_rows * (job.k >> 2));
-    return ws / act_scale;
+// One workgroup's share of a batch, in job `job`:
+//   slab kernel      slab a of b slabs of the job (b == 0: padding); flags
+//                    WG_PUBLISH
+//   streaming kernel rows [a, b) (a >= b: padding)
+// Empty descriptors pad the table to a multiple of 8 workgroups.
+struct wg_desc {
+    uint32_t job;
+    uint32_t a;
+    uint32_t b;
+    uint32_t flags;
+};
+
+constexpr uint32_t WG_PUBLISH = 1;      // this workgroup writes the job's quantised row (q / act)
+
+// Workgroups are dealt to the 8 XCDs round-robin by block index. Read the
+// descriptor table so that XCD x runs the x-th eighth of it in order: the
+// slabs of one job then share an XCD, and its L2 fetches the job's activation
+// once instead of every XCD fetching it. n_wg is a multiple of 8.
+__device__ __forceinline__ uint32_t xcd_slot(uint32_t n_wg) {
+    return (blockIdx.x & 7u) * (n_wg >> 3) + (blockIdx.x >> 3);
 }
 
-__device__ __forceinline__ void store_row(const gemv_job &job, uint32_t row, int dot, int32_t asum,
-                                          float post) {
-    if (job.out_i != nullptr) G_CAST(int32_t, job.out_i)[row] = dot;
-    if (job.out_f != nullptr) G_CAST(float, job.out_f)[row] = (float) (dot - asum) * post;
+// w_scale, the f32 after the packed codes (src/quant.c:102-106)
+__device__ __forceinline__ float tensor_scale(const gemv_job &job) {
+    return *G_CAST(const float, job.w + (size_t) job.n_rows * (job.k >> 2));
 }
 
-// Copy the K-byte activation into LDS (the caller synchronises).
-__device__ __forceinline__ void stage_q(const int8_t *__restrict__ q, uint32_t k, int8_t *q_lds) {
-    for (uint32_t i = 16u * threadIdx.x; i < k; i += 16u * blockDim.x) {
-        *reinterpret_cast<u32x4 *>(q_lds + i) = *G_CAST(const u32x4, q + i);
+// ---------------------------------------------------------------------------
+// slab GEMV (K <= 7168: every BitNet-2B projection). A workgroup of four
+// waves owns a slab of consecutive rows of one job, sized by bytes so that
+// every workgroup streams about the same amount of weights. Each wave walks
+// groups of 64/LPR rows (LPR lanes per row, CPL 16-byte chunks per lane),
+// double-buffered: the next group's loads are in flight while the current
+// one is reduced, and the dots go to LDS, so no store sits between the loads
+// and nothing forces the wave to drain its loads. In the prologue the
+// activation loads are issued before the first weight group, so the wave
+// waits only for the activation while the weights keep streaming; when the
+// job carries f32 x the workgroup quantises it here (the operations of
+// quant_row, so the same bits) and no quantiser launch is needed. Outputs
+// and the epilogue are written at the end, coalesced.
+// ---------------------------------------------------------------------------
+
+constexpr int SLAB_THREADS = 256;
+constexpr int SLAB_WAVES = SLAB_THREADS / 64;
+constexpr uint32_t SLAB_MAX_K = 7168;
+constexpr uint32_t SLAB_MAX_ROWS = 1024;
+
+static_assert(8 * 5 * 64 <= SLAB_MAX_K && 16 * 7 * 64 <= SLAB_MAX_K, "slab geometries read inside the LDS row");
+
+struct slab_shared {
+    int8_t  q[SLAB_MAX_K];
+    int32_t dots[SLAB_MAX_ROWS];
+    float   red_f[SLAB_WAVES];
+    int     red_i[SLAB_WAVES];
+};
+
+// Every load of the slab kernel is unconditional: a skipped load (a branch
+// around it, or an exec-masked block the wave jumps over when no lane needs
+// it) leaves the compiler unsure how many loads are outstanding where paths
+// meet, and it then waits for all of them, draining the prefetch. Weights
+// are read through a buffer resource bounded by the tensor's size (the host
+// keeps slab tensors below 4 GiB): a chunk slot past the end of the last row
+// reads zeros instead of faulting, so lane slot u is simply the lane's
+// offset plus a constant. A lane whose row lies past the slab re-reads the
+// slab's last row (lines already being fetched); slab_dot zeroes what it
+// must not use -- those rows, and slots past the end of a row, which read
+// the next row.
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tensor_rsrc(const gemv_job &job) {
+    const uint32_t bytes = job.n_rows * (job.k >> 2) + 32u;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(job.w), (short) 0, (int) bytes,
+                                             0x00020000);    // raw buffer, 32-bit data format
+}
+
+constexpr int CPOL_NT = 2;      // nontemporal: weights are read once
+
+template <int LPR, int CPL>
+__device__ __forceinline__ void slab_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t row_bytes, uint32_t base,
+                                          uint32_t last_row, u32x4 (&buf)[CPL]) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = min(base + (uint32_t) (lane / LPR), last_row);
+    const uint32_t off = row * row_bytes + (uint32_t) (lane % LPR) * 16u;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        buf[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int) (off + (uint32_t) (u * LPR * 16)), 0, CPOL_NT);
     }
 }
 
-constexpr int MAX_WAVES = 16;
+// Dots of one wave's rows [row0, row0 + 64/LPR) (rows past n_rows masked)
+// into dots[0 .. 64/LPR).
+template <int LPR, int CPL>
+__device__ __forceinline__ void slab_dot(uint32_t chunks, uint32_t row0, uint32_t n_rows,
+                                         const u32x4 (&buf)[CPL], const int8_t *q_lds, int32_t *dots) {
+    const int lane = threadIdx.x & 63, sub = lane % LPR;
+    const uint32_t row = row0 + (uint32_t) (lane / LPR);
+    const bool valid = row < n_rows;
+    // Chunk slot u of this lane is chunk sub + u*LPR: with LPR even its
+    // activation quarter starts at (sub/2)*128 + (sub&1)*16 + u*LPR*64, one
+    // base plus constant offsets. Slots past the row (zeroed below) read
+    // inside the LDS row all the same: LPR*CPL*64 <= SLAB_MAX_K. The base is
+    // hidden from loop-invariant code motion: hoisted, the activation reads
+    // of every group would stay in registers across the loop.
+    uint32_t lds_lane = (uint32_t) (sub >> 1) * 128u + (uint32_t) (sub & 1) * 16u;
+    asm volatile("" : "+v"(lds_lane));
+    dot4acc acc = { 0, 0, 0, 0 };
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        const bool use = valid && (uint32_t) (sub + u * LPR) < chunks;
+        const u32x4 zero = { 0, 0, 0, 0 };
+        chunk_dot(use ? buf[u] : zero, q_lds + lds_lane + (uint32_t) (u * LPR * 64), acc);
+    }
+    const int dot = group_sum<LPR>(finish(acc));      // whole wave active here
+    if (valid && sub == 0) dots[lane / LPR] = dot;
+}
 
-// The activation of a job, in LDS, with its scale and sum. Either staged from
-// a quantised row, or quantised here from x -- the same operations as
-// quant_row, so every workgroup of the job derives identical bits. All
-// threads of the block call this; it ends with q_lds complete and visible.
-__device__ __forceinline__ void activation_to_lds(const gemv_job &job, uint32_t local_wg,
-                                                  int8_t *q_lds, float *red_f, int *red_i,
-                                                  float &scale, int32_t &sum) {
-    const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6;
-    const int nw = nthr >> 6;
-    const uint32_t k = job.k;
-    if (job.x == nullptr) {
-        stage_q(job.q, k, q_lds);
-        // act is only required (and only given) when the epilogue runs
-        scale = 0.0f;
-        sum = 0;
-        if (job.act != nullptr) {
-            scale = G_CAST(const float, job.act)[0];
-            sum = G_CAST(const int32_t, job.act)[1];
+// LPR lanes per row, CPL chunks per lane (LPR * CPL * 64 >= K), XV f32x4 and
+// QV 16-byte activation loads per thread (covering K). QUANT: the job carries
+// f32 x (quantised here) rather than a quantised row; it is a template
+// argument so that each instantiation is one straight path and the compiler
+// never has to assume the other input's loads might still be in flight.
+//
+// A job's rows are cut into groups of G = 4 * 64/LPR rows, one per pass of
+// the workgroup's four waves; slab a of b takes the a-th run of consecutive
+// groups. (Dealing the groups round-robin instead, so that a job's slabs
+// sweep it side by side, measured no faster.)
+template <int LPR, int CPL, int XV, int QV, bool QUANT>
+__device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, uint32_t n_slabs,
+                                           uint32_t flags, slab_shared &S) {
+    constexpr uint32_t RPW = 64 / LPR;
+    constexpr uint32_t G = SLAB_WAVES * RPW;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) tid >> 6);
+    const uint32_t k = job.k, chunks = k >> 6, row_bytes = k >> 2;
+    const uint32_t n_rows = job.n_rows, last_row = n_rows - 1;
+    const __amdgpu_buffer_rsrc_t rsrc = tensor_rsrc(job);
+    // this slab's groups: first .. first + T - 1
+    const uint32_t n_groups = (n_rows + G - 1) / G;
+    const uint32_t per = (n_groups + n_slabs - 1) / n_slabs;
+    const uint32_t first = slab * per;
+    const uint32_t T = first < n_groups ? min(per, n_groups - first) : 0u;
+    if (T == 0) return;                        // uniform: no group here
+    // the wave's first row in its t-th group; past the end, the last group again
+    const uint32_t wave_row = wave * RPW;
+    auto group_row = [&](uint32_t t) { return (first + min(t, T - 1)) * G + wave_row; };
+
+    // (1) the activation first -- f32 x to quantise here, or the int8 row --
+    // so that waiting for it leaves the weight loads behind it in flight
+    f32x4 xv[XV];
+    u32x4 qv[QV];
+    float scale = 0.0f;
+    int32_t asum = 0;
+    if (QUANT) {
+#pragma unroll
+        for (int u = 0; u < XV; ++u) {
+            const uint32_t i = 4u * (uint32_t) (tid + u * SLAB_THREADS);
+            xv[u] = *G_CAST(const f32x4, job.x + min(i, k - 4));
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < QV; ++u) {
+            const uint32_t i = 16u * (uint32_t) (tid + u * SLAB_THREADS);
+            qv[u] = *G_CAST(const u32x4, job.q + min(i, k - 16));
+        }
+        // act is optional without an epilogue; read a valid address either way
+        const GLOBAL int32_t *ap = G_CAST(const int32_t, job.act != nullptr ? (const void *) job.act
+                                                                          : (const void *) job.w);
+        const float sc = __int_as_float(ap[0]);
+        const int32_t sm = ap[1];
+        scale = job.act != nullptr ? sc : 0.0f;
+        asum = job.act != nullptr ? sm : 0;
+    }
+    // w_scale for the epilogue; without one, read row 0 instead of a tail
+    // the caller need not have given (no branch around the load)
+    const uint8_t *ws_at = job.out_f != nullptr ? job.w + (size_t) job.n_rows * row_bytes : job.w;
+    const float ws = *G_CAST(const float, ws_at);
+    // keep the scheduler from moving activation loads behind the weight loads
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (2) the wave's first row group
+    u32x4 bufa[CPL], bufb[CPL];
+    slab_load<LPR, CPL>(rsrc, row_bytes, group_row(0), last_row, bufa);
+
+    // (3) the activation into LDS
+    if (QUANT) {
+        float m = 0.0f;        // fmaxf drops NaN exactly as the reference's `a > amax` does
+#pragma unroll
+        for (int u = 0; u < XV; ++u) {
+            const uint32_t i = 4u * (uint32_t) (tid + u * SLAB_THREADS);
+            const f32x4 v = xv[u];
+            const float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            m = fmaxf(m, i < k ? a : 0.0f);
+        }
+        m = wave_max(m);
+        if (lane == 0) S.red_f[wave] = m;
+        __syncthreads();
+        m = S.red_f[0];
+#pragma unroll
+        for (int w = 1; w < SLAB_WAVES; ++w) m = fmaxf(m, S.red_f[w]);
+        const float s = m > 0.0f ? 127.0f / m : 0.0f;
+        int ls = 0;
+#pragma unroll
+        for (int u = 0; u < XV; ++u) {
+            const uint32_t i = 4u * (uint32_t) (tid + u * SLAB_THREADS);
+            if (i < k) {
+                const f32x4 v = xv[u];
+                const int a = quant_one(v[0] * s), b = quant_one(v[1] * s);
+                const int c = quant_one(v[2] * s), d = quant_one(v[3] * s);
+                ls += a + b + c + d;
+                *reinterpret_cast<uint32_t *>(S.q + i) =
+                    (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) |
+                    ((uint32_t) (c & 0xff) << 16) | ((uint32_t) (d & 0xff) << 24);
+            }
+        }
+        ls = wave_sum(ls);
+        if (lane == 0) S.red_i[wave] = ls;
+        __syncthreads();
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < SLAB_WAVES; ++w) t += S.red_i[w];
+        scale = s;
+        asum = t;
+    } else {
+#pragma unroll
+        for (int u = 0; u < QV; ++u) {
+            const uint32_t i = 16u * (uint32_t) (tid + u * SLAB_THREADS);
+            if (i < k) *reinterpret_cast<u32x4 *>(S.q + i) = qv[u];
         }
         __syncthreads();
-        return;
     }
-    const float *x = job.x;
-    float m = 0.0f;
-    for (uint32_t i = 4u * tid; i < k; i += 4u * nthr) {
-        const f32x4 v = *G_CAST(const f32x4, x + i);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+
+    // (4) the groups, double-buffered: pairs of groups with the next group
+    // always loaded (the last one again past the end) before the current one
+    // is reduced, then a trailing odd group. The loop has one exit and no
+    // load behind a branch, so every wait names exactly the buffer it needs.
+    // Dots of group t go to S.dots[t*G ..].
+    int32_t *dots = S.dots + wave_row;
+    uint32_t t = 0;
+    for (uint32_t pair = 0; pair < T / 2; ++pair) {
+        slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufb);
+        slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
+        ++t;
+        slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufa);
+        slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufb, S.q, dots + t * G);
+        ++t;
     }
-    m = wave_max(m);
-    if (lane == 0) red_f[wave] = m;
+    if (T & 1u) slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
     __syncthreads();
-    m = red_f[0];
-    for (int w = 1; w < nw; ++w) m = fmaxf(m, red_f[w]);
-    const float s = m > 0.0f ? 127.0f / m : 0.0f;
-    int ls = 0;
-    for (uint32_t i = 4u * tid; i < k; i += 4u * nthr) {
-        const f32x4 v = *G_CAST(const f32x4, x + i);
-        const int a = quant_one(v[0] * s), b = quant_one(v[1] * s);
-        const int c = quant_one(v[2] * s), d = quant_one(v[3] * s);
-        ls += a + b + c + d;
-        *reinterpret_cast<uint32_t *>(q_lds + i) =
-            (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) |
-            ((uint32_t) (c & 0xff) << 16) | ((uint32_t) (d & 0xff) << 24);
+
+    // (5) raw dots and the epilogue (src/i2s_gemm.c:271-290): post once per
+    // column, then (float)(dot - sum) * post per row
+    const float post = job.out_f != nullptr ? ws / scale : 0.0f;
+    for (uint32_t i = (uint32_t) tid; i < T * G; i += SLAB_THREADS) {
+        const uint32_t row = first * G + i;
+        if (row < n_rows) {
+            const int32_t d = S.dots[i];
+            if (job.out_i != nullptr) G_CAST(int32_t, job.out_i)[row] = d;
+            if (job.out_f != nullptr) G_CAST(float, job.out_f)[row] = (float) (d - asum) * post;
+        }
     }
-    ls = wave_sum(ls);
-    if (lane == 0) red_i[wave] = ls;
-    __syncthreads();
-    int t = 0;
-    for (int w = 0; w < nw; ++w) t += red_i[w];
-    scale = s;
-    sum = t;
-    if (local_wg == 0) {       // one workgroup publishes the quantised row
+
+    // (6) one workgroup of the job publishes the row it quantised
+    if ((flags & WG_PUBLISH) && QUANT) {
         if (job.q != nullptr) {
-            for (uint32_t i = 16u * tid; i < k; i += 16u * nthr) {
-                *G_CAST(u32x4, job.q + i) = *reinterpret_cast<const u32x4 *>(q_lds + i);
+#pragma unroll
+            for (int u = 0; u < QV; ++u) {
+                const uint32_t i = 16u * (uint32_t) (tid + u * SLAB_THREADS);
+                if (i < k) *G_CAST(u32x4, job.q + i) = *reinterpret_cast<const u32x4 *>(S.q + i);
             }
         }
         if (job.act != nullptr && tid == 0) {
-            G_CAST(float, job.act)[0] = s;
-            G_CAST(int32_t, job.act)[1] = t;
+            G_CAST(float, job.act)[0] = scale;
+            G_CAST(int32_t, job.act)[1] = asum;
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// streaming GEMV (any K up to the LDS limit): waves loop over row groups,
-// 8 loads in flight per lane. Reads a quantised activation (x must be null).
+// streaming GEMV (any K up to the LDS limit): waves loop over row groups with
+// UNROLL loads in flight per lane, reading a quantised activation staged in
+// LDS (x must be null: the plan quantises such jobs first).
 // ---------------------------------------------------------------------------
 
 constexpr int UNROLL = 8;
@@ -303,7 +494,7 @@ __device__ __forceinline__ void stream_rows(const gemv_job &job, uint32_t row_be
                                             int32_t asum, float post) {
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int wave = (int) __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
     const int sub = lane % LPR;
     const uint32_t k = job.k, chunks = k >> 6, row_bytes = k >> 2;
 
@@ -328,148 +519,61 @@ __device__ __forceinline__ void stream_rows(const gemv_job &job, uint32_t row_be
             }
         }
         const int dot = group_sum<LPR>(finish(acc));
-        if (valid && sub == 0) store_row(job, row, dot, asum, post);
+        if (valid && sub == 0) {
+            if (job.out_i != nullptr) G_CAST(int32_t, job.out_i)[row] = dot;
+            if (job.out_f != nullptr) G_CAST(float, job.out_f)[row] = (float) (dot - asum) * post;
+        }
     }
 }
 
 template <int LPR>
-__device__ __forceinline__ void stream_block(const gemv_job &job, uint32_t local_wg) {
+__device__ __forceinline__ void stream_block(const gemv_job &job, uint32_t row_begin, uint32_t row_end) {
     extern __shared__ __attribute__((aligned(16))) int8_t q_lds[];
-    const uint32_t row_begin = local_wg * job.rows_per_wg;
-    if (row_begin >= job.n_rows) return;           // uniform across the block
-    const uint32_t row_end = min(job.n_rows, row_begin + job.rows_per_wg);
-    stage_q(job.q, job.k, q_lds);
-    __syncthreads();
+    const uint32_t k = job.k;
+    const uint32_t step = 16u * blockDim.x;
+    // stage the activation: four loads in flight per thread between waits
+    for (uint32_t i0 = 16u * threadIdx.x; i0 < k; i0 += 4u * step) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + (uint32_t) u * step;
+            if (i < k) v[u] = *G_CAST(const u32x4, job.q + i);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + (uint32_t) u * step;
+            if (i < k) *reinterpret_cast<u32x4 *>(q_lds + i) = v[u];
+        }
+    }
     float post = 0.0f;
     int32_t asum = 0;
     if (job.out_f != nullptr) {
-        post = epilogue_post(job, G_CAST(const float, job.act)[0]);
+        post = tensor_scale(job) / G_CAST(const float, job.act)[0];
         asum = G_CAST(const int32_t, job.act)[1];
     }
+    __syncthreads();
     stream_rows<LPR>(job, row_begin, row_end, q_lds, asum, post);
 }
 
-// ---------------------------------------------------------------------------
-// row-group GEMV. A block owns rows_per_wg consecutive rows of one job; its
-// waves take turns over row groups of 64/LPR rows (LPR lanes per row, each
-// lane CPL 16-byte chunks of its row), double-buffered: the loads of a
-// wave's next row group are issued before the current one is reduced, so a
-// wave never waits a full memory round trip between groups. The first
-// group's loads are issued before the activation is built in LDS --
-// quantised from x in-kernel when the job carries it -- which costs one read
-// of x per block, a few percent of the block's weight bytes.
-// Geometry per K class (the `variant` of a job):
-//   0: LPR 8,  CPL 5    K <= 2560
-//   1: LPR 16, CPL 7    K <= 7168
-//   2: LPR 8,  CPL 14   K <= 7168
-//   3: LPR 16, CPL 16   K <= 16384
-// ---------------------------------------------------------------------------
-
-// The loads are unconditional, so the loop stays straight-line and the
-// compiler can wait for one buffer while the other is still in flight. A
-// lane whose row lies past row_end, or whose chunk slot lies past the row,
-// re-reads the last valid row / chunk (lines already being fetched: no extra
-// HBM traffic) and rg_reduce zeroes those weights. base < row_end always.
-template <int LPR, int CPL>
-__device__ __forceinline__ void rg_load(const gemv_job &job, uint32_t base, uint32_t row_end,
-                                        u32x4 (&buf)[CPL]) {
-    const int lane = threadIdx.x & 63, sub = lane % LPR;
-    const uint32_t chunks = job.k >> 6, row_bytes = job.k >> 2;
-    const uint32_t row = min(base + (uint32_t) (lane / LPR), row_end - 1);
-    const GLOBAL u32x4 *wr = G_CAST(const u32x4, job.w + (size_t) row * row_bytes);
-#pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-        const uint32_t c = min((uint32_t) (sub + u * LPR), chunks - 1);
-        buf[u] = __builtin_nontemporal_load(wr + c);
+// A streaming workgroup's job and rows: from the descriptor table, or -- for
+// a single-job launch (descs null) -- rows [blockIdx.x * single_rows, +single_rows)
+// of `single`.
+__device__ __forceinline__ bool stream_share(const gemv_job *__restrict__ jobs,
+                                             const wg_desc *__restrict__ descs, uint32_t n_wg,
+                                             const gemv_job &single, uint32_t single_rows,
+                                             gemv_job &job, uint32_t &row_begin, uint32_t &row_end) {
+    if (descs != nullptr) {
+        const wg_desc d = descs[xcd_slot(n_wg)];
+        if (d.a >= d.b) return false;
+        job = jobs[d.job];
+        row_begin = d.a;
+        row_end = d.b;
+        return true;
     }
-}
-
-template <int LPR, int CPL>
-__device__ __forceinline__ void rg_reduce(const gemv_job &job, uint32_t base, uint32_t row_end,
-                                          const u32x4 (&buf)[CPL], const int8_t *q_lds,
-                                          int32_t asum, float post) {
-    const int lane = threadIdx.x & 63, sub = lane % LPR;
-    const uint32_t chunks = job.k >> 6;
-    const uint32_t row = base + (uint32_t) (lane / LPR);
-    const bool valid = row < row_end;
-    // The activation reads are the same for every row group of the wave; left
-    // alone the compiler keeps all of them in registers across the loop,
-    // which halves occupancy. Re-reading them from LDS is cheaper: hide the
-    // base from loop-invariant code motion.
-    uint32_t lds_base = 0;
-    asm volatile("" : "+v"(lds_base));
-    dot4acc acc = { 0, 0, 0, 0 };
-#pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-        const uint32_t slot = (uint32_t) (sub + u * LPR);
-        const uint32_t c = min(slot, chunks - 1);
-        const bool use = valid && slot < chunks;
-        const u32x4 zero = { 0, 0, 0, 0 };
-        chunk_dot(use ? buf[u] : zero, q_lds + lds_base + (c >> 1) * 128u + (c & 1u) * 16u, acc);
-    }
-    const int dot = group_sum<LPR>(finish(acc));      // whole wave active here
-    if (valid && sub == 0) store_row(job, row, dot, asum, post);
-}
-
-template <int LPR, int CPL>
-__device__ __forceinline__ void rowgroup_block(const gemv_job &job, uint32_t local_wg, int8_t *q_lds,
-                                               float *red_f, int *red_i) {
-    constexpr uint32_t RPW = 64 / LPR;
-    const uint32_t wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const uint32_t row_begin = local_wg * job.rows_per_wg;
-    if (row_begin >= job.n_rows) return;           // uniform across the block
-    const uint32_t row_end = min(job.n_rows, row_begin + job.rows_per_wg);
-    const uint32_t stride = waves * RPW;
-
-    // wave-uniform first row of this wave's current group; a wave whose first
-    // group is already past the block's rows still takes part in the barriers
-    uint32_t base = row_begin + wave * RPW;
-    u32x4 bufa[CPL], bufb[CPL];
-    rg_load<LPR, CPL>(job, min(base, row_end - 1), row_end, bufa);
-
-    float scale;
-    int32_t asum;
-    activation_to_lds(job, local_wg, q_lds, red_f, red_i, scale, asum);
-    const float post = job.out_f != nullptr ? epilogue_post(job, scale) : 0.0f;
-
-    while (base < row_end) {
-        rg_load<LPR, CPL>(job, min(base + stride, row_end - 1), row_end, bufb);
-        rg_reduce<LPR, CPL>(job, base, row_end, bufa, q_lds, asum, post);
-        base += stride;
-        if (base >= row_end) break;
-        rg_load<LPR, CPL>(job, min(base + stride, row_end - 1), row_end, bufa);
-        rg_reduce<LPR, CPL>(job, base, row_end, bufb, q_lds, asum, post);
-        base += stride;
-    }
-}
-
-// Variants are compiled into three kernel classes so that the register
-// budget of the wide ones does not lower the occupancy of the common ones:
-// class 0 = variants 0 and 1 (the K classes of the BitNet-2B projections),
-// class 1 = variant 2, class 2 = variant 3.
-template <int CLASS>
-__device__ __forceinline__ void rowgroup_dispatch(const gemv_job &job, uint32_t local_wg) {
-    extern __shared__ __attribute__((aligned(16))) int8_t q_lds[];
-    __shared__ float red_f[MAX_WAVES];
-    __shared__ int red_i[MAX_WAVES];
-    if (CLASS == 0) {
-        if (job.variant == 0) rowgroup_block<8, 5>(job, local_wg, q_lds, red_f, red_i);
-        else rowgroup_block<16, 7>(job, local_wg, q_lds, red_f, red_i);
-    } else if (CLASS == 1) {
-        rowgroup_block<8, 14>(job, local_wg, q_lds, red_f, red_i);
-    } else {
-        rowgroup_block<16, 16>(job, local_wg, q_lds, red_f, red_i);
-    }
-}
-
-// jobs are sorted by wg_begin; the block's job is the last with wg_begin <= blockIdx.x
-__device__ __forceinline__ gemv_job find_job(const gemv_job *__restrict__ jobs, uint32_t n_jobs) {
-    uint32_t lo = 0, hi = n_jobs;
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (jobs[mid].wg_begin <= blockIdx.x) lo = mid; else hi = mid;
-    }
-    return jobs[lo];
+    job = single;
+    row_begin = blockIdx.x * single_rows;
+    row_end = min(single.n_rows, row_begin + single_rows);
+    return row_begin < row_end;
 }
 
 } // namespace
@@ -506,32 +610,51 @@ sllm_k_quant_list(const quant_job *__restrict__ jobs) {
     quant_row(j.x, j.n, j.q, j.act, red_f, red_i);
 }
 
-#define SLLM_STREAM_ENTRY(L)                                                            \
-    extern "C" __global__ void __launch_bounds__(1024)                                  \
-    sllm_k_gemv_l##L(gemv_job job) { stream_block<L>(job, blockIdx.x); }                \
-    extern "C" __global__ void __launch_bounds__(1024)                                  \
-    sllm_k_gemv_group_l##L(const gemv_job *__restrict__ jobs, uint32_t n_jobs) {        \
-        const gemv_job job = find_job(jobs, n_jobs);                                    \
-        stream_block<L>(job, blockIdx.x - job.wg_begin);                                \
+// Slab GEMV: blocks of SLAB_THREADS, static LDS. With descs null this is a
+// single-job launch: slab blockIdx.x of gridDim.x slabs of `single`.
+extern "C" __global__ void __launch_bounds__(SLAB_THREADS)
+sllm_k_gemv_slab(const gemv_job *__restrict__ jobs, const wg_desc *__restrict__ descs,
+                 uint32_t n_wg, gemv_job single, uint32_t single_flags) {
+    __shared__ slab_shared S;
+    gemv_job job;
+    uint32_t slab, n_slabs, flags;
+    if (descs != nullptr) {
+        const wg_desc d = descs[xcd_slot(n_wg)];
+        if (d.b == 0) return;
+        job = jobs[d.job];
+        slab = d.a;
+        n_slabs = d.b;
+        flags = d.flags;
+    } else {
+        job = single;
+        slab = blockIdx.x;
+        n_slabs = gridDim.x;
+        flags = (single_flags & ~WG_PUBLISH) | (blockIdx.x == 0 ? WG_PUBLISH : 0u);
+    }
+    const bool quant = job.x != nullptr;
+    if (job.variant == 0) {                                                      // K <= 2560
+        if (quant) slab_block<8, 5, 3, 1, true>(job, slab, n_slabs, flags, S);
+        else slab_block<8, 5, 3, 1, false>(job, slab, n_slabs, flags, S);
+    } else {                                                                     // K <= 7168
+        if (quant) slab_block<16, 7, 7, 2, true>(job, slab, n_slabs, flags, S);
+        else slab_block<16, 7, 7, 2, false>(job, slab, n_slabs, flags, S);
+    }
+}
+
+// Streaming GEMV: any block size up to 1024, K bytes of dynamic LDS.
+#define SLLM_STREAM_ENTRY(L)                                                                  \
+    extern "C" __global__ void __launch_bounds__(1024)                                        \
+    sllm_k_gemv_stream_l##L(const gemv_job *__restrict__ jobs, const wg_desc *__restrict__ descs, \
+                            uint32_t n_wg, gemv_job single, uint32_t single_rows) {           \
+        gemv_job job;                                                                         \
+        uint32_t row_begin, row_end;                                                          \
+        if (!stream_share(jobs, descs, n_wg, single, single_rows, job, row_begin, row_end)) return; \
+        stream_block<L>(job, row_begin, row_end);                                             \
     }
 
 SLLM_STREAM_ENTRY(4)
 SLLM_STREAM_ENTRY(8)
 SLLM_STREAM_ENTRY(16)
-
-// Row-group kernels, one per class: at most 4 waves per block.
-#define SLLM_RG_ENTRY(C)                                                                \
-    extern "C" __global__ void __launch_bounds__(256)                                   \
-    sllm_k_gemv_rg_c##C(gemv_job job) { rowgroup_dispatch<C>(job, blockIdx.x); }        \
-    extern "C" __global__ void __launch_bounds__(256)                                   \
-    sllm_k_gemv_rg_group_c##C(const gemv_job *__restrict__ jobs, uint32_t n_jobs) {     \
-        const gemv_job job = find_job(jobs, n_jobs);                                    \
-        rowgroup_dispatch<C>(job, blockIdx.x - job.wg_begin);                           \
-    }
-
-SLLM_RG_ENTRY(0)
-SLLM_RG_ENTRY(1)
-SLLM_RG_ENTRY(2)
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

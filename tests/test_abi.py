@@ -51,7 +51,8 @@ def test_library_embeds_a_gfx950_code_object():
     assert "sllm_gfx950_open" in out
     blob = open(os.path.join(ROOT, "saphira-llm_amd", "libsllm_gfx950.so"), "rb").read()
     assert b"amdgcn-amd-amdhsa--gfx950" in blob
-    for k in (b"sllm_k_quant_act", b"sllm_k_gemv_l4", b"sllm_k_gemv_group_l16"):
+    for k in (b"sllm_k_quant_act", b"sllm_k_quant_list", b"sllm_k_gemv_slab", b"sllm_k_gemv_stream_l4",
+              b"sllm_k_gemv_stream_l8", b"sllm_k_gemv_stream_l16"):
         assert k in blob
 
 

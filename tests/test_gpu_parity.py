@@ -94,13 +94,15 @@ def test_quant_act_edge_rows(amd, orc, dev):
 SHAPES = [(2560, 2560), (6912, 2560), (2560, 6912), (640, 2560), (1, 128), (3, 384),
           (17, 1280), (1001, 6912), (77, 16384), (129, 65536)]
 
-# (path, variant, lanes_per_row, waves, rows_per_wg[, fuse_quant]): every kernel geometry
-GEOMETRIES = [(1, -1, 4, 1, 0), (1, -1, 8, 4, 0), (1, -1, 16, 2, 0), (1, -1, 8, 2, 48),
-              (2, 0, 0, 1, 0), (2, 0, 0, 2, 0), (2, 1, 0, 2, 0), (2, 1, 0, 4, 0),
-              (2, 2, 0, 2, 0), (2, 3, 0, 1, 0), (2, 3, 0, 4, 0),
-              (2, 0, 0, 2, 8), (2, 1, 0, 4, 24), (2, 3, 0, 2, 40), (2, 0, 0, 4, 1000),
-              (0, -1, 0, 0, 0)]
-FUSED = [(2, -1, 0, 2, 0, 1), (2, 3, 0, 4, 0, 1), (2, 0, 0, 1, 24, 1)]
+# (path, variant, lanes_per_row, waves, rows_per_wg[, slab_kib]): every kernel geometry.
+# path 1 = streaming kernel (lanes per row, waves, rows per workgroup);
+# path 2 = slab kernel (variant, KiB of weights per workgroup); 0 = automatic.
+STREAMING = [(1, -1, 4, 1, 0), (1, -1, 8, 4, 0), (1, -1, 16, 2, 0), (1, -1, 8, 2, 48)]
+SLABS = [(2, -1, 0, 0, 0), (2, 0, 0, 0, 0), (2, 1, 0, 0, 0), (2, -1, 0, 0, 0, 1), (2, -1, 0, 0, 0, 3),
+         (2, 1, 0, 0, 0, 40), (2, -1, 0, 0, 0, 4096), (2, 1, 0, 0, 0, 2), (2, -1, 0, 0, 0, 5)]
+GEOMETRIES = STREAMING + SLABS + [(0, -1, 0, 0, 0)]
+# the slab kernel quantises f32 x in-kernel; these cover both of its variants
+FUSED = [(2, -1, 0, 0, 0, 2), (2, 1, 0, 0, 0, 16), (2, -1, 0, 0, 0, 4096), (2, -1, 0, 0, 0, 3)]
 
 
 @pytest.mark.parametrize("n_rows,n", SHAPES)
@@ -154,7 +156,7 @@ def test_linear_matches_oracle(amd, orc, dev, n_rows, n):
     bw, bx = dev.put(w), dev.put(x)
     bq, ba, by, bi = dev.alloc(n), dev.alloc(8), dev.alloc(4 * n_rows), dev.alloc(4 * n_rows)
     try:
-        for geom in [(0, -1, 0, 0, 0), (2, -1, 0, 1, 0), (2, 3, 0, 4, 0), (1, -1, 8, 2, 0)] + FUSED:
+        for geom in [(0, -1, 0, 0, 0), (1, -1, 8, 2, 0), (1, -1, 16, 4, 0)] + FUSED:
             dev.set_tuning(*geom)
             for b, fill in ((bq, np.zeros(n, np.int8)), (ba, np.zeros(2, np.int32)),
                             (by, np.zeros(n_rows, np.float32)), (bi, np.zeros(n_rows, np.int32))):
@@ -167,8 +169,8 @@ def test_linear_matches_oracle(amd, orc, dev, n_rows, n):
             assert a[:4].view(np.float32)[0] == s_o and a[4:].view(np.int32)[0] == t_o, geom
             np.testing.assert_array_equal(bi.download(np.int32, n_rows), d_o, err_msg=str(geom))
             assert f32_bits_equal(by.download(np.float32, n_rows), y_o), geom
-        # without q / act outputs: library row scratch, or in-kernel
-        for geom in [(0, -1, 0, 0, 0)] + FUSED:
+        # without q / act outputs: library row scratch (streaming), or in-kernel
+        for geom in [(0, -1, 0, 0, 0), (1, -1, 8, 2, 0)] + FUSED:
             dev.set_tuning(*geom)
             by.upload(np.zeros(n_rows, np.float32))
             dev.linear(bw.vp, n_rows, n, bx.vp, None, None, by.vp)
@@ -257,8 +259,9 @@ def test_batch_and_plan_over_a_block_match_oracle(amd, orc, dev):
 
 
 def test_mixed_plan_runs_every_launch_kind(amd, orc, dev):
-    """One plan holding row-group jobs (fused and pre-quantised) and K > 16384
-    jobs that take the streaming kernel after a quantiser launch."""
+    """One plan holding slab jobs (quantising in-kernel and pre-quantised) and
+    K > 7168 jobs that take the streaming kernel, some after a quantiser
+    launch."""
     specs = [(300, 2560, True), (64, 65536, True), (50, 16384, False), (129, 6912, True), (33, 20480, False)]
     jobs, checks, bufs = [], [], []
     for i, (n_rows, n, fused) in enumerate(specs):
@@ -275,7 +278,7 @@ def test_mixed_plan_runs_every_launch_kind(amd, orc, dev):
             jobs.append(amd.GemvJob(bw.ptr, n_rows, n, None, bq.ptr, ba.ptr, by.ptr, bi.ptr))
         checks.append((by, bi, bq, n_rows, n, y_o, d_o, q_o))
     try:
-        for geom in [(0, -1, 0, 0, 0)] + FUSED:
+        for geom in [(0, -1, 0, 0, 0), (1, -1, 8, 2, 0)] + FUSED:
             say("mixed plan", geom)
             dev.set_tuning(*geom)
             plan = dev.plan(jobs)
@@ -366,9 +369,9 @@ def test_argument_errors_are_reported_not_launched(amd, dev):
     assert lib.sllm_gfx950_gemv(b.vp, 4, 65536 + 128, b.vp, b.vp) == -36  # K above the LDS limit
     assert lib.sllm_gfx950_gemv(b.at(4), 4, 128, b.vp, b.vp) == -1       # misaligned weights
     assert lib.sllm_gfx950_gemv_epilogue(b.vp, 4, 128, b.vp, None, b.vp) == -1
-    assert lib.sllm_gfx950_set_tuning(0, -1, 5, 0, 0, 0) == -1
-    assert lib.sllm_gfx950_set_tuning(2, -1, 0, 8, 0, 0) == -1         # row-group: <= 4 waves
-    assert lib.sllm_gfx950_set_tuning(1, -1, 0, 0, 0, 1) == -1         # only the row-group kernel fuses
+    assert lib.sllm_gfx950_set_tuning(0, -1, 5, 0, 0, 0) == -1         # lanes per row
+    assert lib.sllm_gfx950_set_tuning(2, 2, 0, 0, 0, 0) == -1          # slab variants are 0 and 1
+    assert lib.sllm_gfx950_set_tuning(2, -1, 0, 0, 0, -1) == -1        # slab KiB
     x = dev.alloc(4 * 128)
     job = amd.GemvJob(b.ptr, 4, 128, x.ptr, b.ptr, None, b.ptr, None)  # q without act
     assert lib.sllm_gfx950_gemv_batch(ctypes.byref(job), 1) == -1
