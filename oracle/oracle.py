@@ -51,6 +51,21 @@ _PROTOS = {
     "orc_gemv_epilogue_parallel": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p,
                                           POINTER(Act), c_void_p, c_void_p, c_int]),
     "orc_fnv1a64": (c_uint64, [c_void_p, c_size_t]),
+    "orc_f16_to_f32": (c_float, [ctypes.c_uint16]),
+    "orc_f16_to_f32_embd": (c_float, [ctypes.c_uint16]),
+    "orc_rms_norm": (None, [c_void_p, c_void_p, c_void_p, c_size_t, c_float]),
+    "orc_v_expf": (c_float, [c_float]),
+    "orc_softmax": (None, [c_void_p, c_size_t]),
+    "orc_silu": (None, [c_void_p, c_size_t]),
+    "orc_rope_neox": (None, [c_void_p, c_size_t, c_int32, c_float, c_float]),
+    "orc_rope_cos_sin": (None, [c_size_t, c_int32, c_float, c_float, c_void_p, c_void_p]),
+    "orc_dot_f16": (c_float, [c_void_p, c_void_p, c_size_t]),
+    "orc_argmax": (c_int32, [c_void_p, c_int32]),
+    "orc_ctx_new": (c_void_p, [c_void_p, c_int32]),
+    "orc_ctx_free": (None, [c_void_p]),
+    "orc_ctx_k_cache": (c_void_p, [c_void_p]),
+    "orc_ctx_v_cache": (c_void_p, [c_void_p]),
+    "orc_forward_token": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_int, c_void_p, c_void_p]),
 }
 
 _REF_PROTOS = {
@@ -72,6 +87,18 @@ _REF_PROTOS = {
     "ref_gemv_all": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
     "ref_gemv_epilogue": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, POINTER(Act),
                                  c_void_p, c_void_p, c_int]),
+    "sllm_rms_norm": (None, [c_void_p, c_void_p, c_void_p, c_size_t, c_float]),
+    "sllm_softmax_inplace": (None, [c_void_p, c_size_t]),
+    "sllm_silu_inplace": (None, [c_void_p, c_size_t]),
+    "sllm_rope_inplace": (None, [c_void_p, c_size_t, c_int32, c_float, c_float, c_int]),
+    "sllm_dot_f16_f32": (c_float, [c_void_p, c_void_p, c_size_t]),
+    "ref_model_open": (c_void_p, [c_void_p, c_size_t, POINTER(c_int)]),
+    "ref_model_close": (None, [c_void_p]),
+    "ref_ctx_new": (c_void_p, [c_void_p, c_int32]),
+    "ref_ctx_free": (None, [c_void_p]),
+    "ref_ctx_set_pool": (None, [c_void_p, c_void_p]),
+    "ref_forward": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "ref_argmax": (c_int32, [c_void_p, c_int32]),
 }
 
 # the reference's ISA levels as passed to sllm_i2s_select_level
@@ -233,3 +260,116 @@ def lcg_activation(n):
         v = np.float32((rng >> 8) & 0xFFFF) / np.float32(32768.0)
         out[i] = (np.float32(v) - np.float32(1.0)) * np.float32(3.0)
     return out
+
+
+# ---------------------------------------------------------------------------
+# the decode step
+# ---------------------------------------------------------------------------
+
+class OrcLayer(ctypes.Structure):
+    """orc_layer"""
+    _fields_ = [(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
+                                         "attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm")]
+
+
+class OrcModel(ctypes.Structure):
+    """orc_model"""
+    _fields_ = [("n_layer", c_int32), ("n_embd", c_int32), ("n_ff", c_int32), ("n_head", c_int32),
+                ("n_head_kv", c_int32), ("n_rot", c_int32), ("n_vocab", c_int32), ("eps", c_float),
+                ("rope_base", c_float), ("tok_embd", c_void_p), ("output_norm", c_void_p),
+                ("layers", c_void_p)]
+
+
+def n_trace_dots(cfg):
+    """int32 dots per token in a decode trace: per layer q, k, v, o, gate, up, down."""
+    gqa = cfg["n_embd"] // cfg["n_head"] * cfg["n_head_kv"]
+    return cfg["n_layer"] * (3 * cfg["n_embd"] + 2 * gqa + 2 * cfg["n_ff"])
+
+
+class Decoder:
+    """The oracle's decode step over a model dict (saphira_llm_amd.synth_model);
+    keeps the numpy arrays alive for the C structs that point into them."""
+
+    LAYER_KEYS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
+                  "attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm")
+
+    def __init__(self, model, n_ctx):
+        cfg = model["cfg"]
+        self.model, self.cfg, self.n_ctx = model, cfg, n_ctx
+        self.layers = (OrcLayer * cfg["n_layer"])()
+        for il, layer in enumerate(model["layers"]):
+            for k in self.LAYER_KEYS:
+                setattr(self.layers[il], k, _p(layer[k]).value)
+        self.m = OrcModel(cfg["n_layer"], cfg["n_embd"], cfg["n_ff"], cfg["n_head"], cfg["n_head_kv"],
+                          cfg["n_rot"], cfg["n_vocab"], cfg["eps"], cfg["rope_base"],
+                          _p(model["tok_embd"]).value, _p(model["output_norm"]).value,
+                          ctypes.cast(self.layers, c_void_p).value)
+        self.c = orc().orc_ctx_new(ctypes.byref(self.m), n_ctx)
+        if not self.c:
+            raise MemoryError("orc_ctx_new")
+        hd = cfg["n_embd"] // cfg["n_head"]
+        self.kv_shape = (cfg["n_layer"], cfg["n_head_kv"], n_ctx, hd)
+        self.n_dots = n_trace_dots(cfg)
+
+    def caches(self):
+        """numpy views of the f32 K and V caches [layer][head_kv][pos][head_dim]."""
+        n = int(np.prod(self.kv_shape))
+        k = np.ctypeslib.as_array(ctypes.cast(orc().orc_ctx_k_cache(self.c), POINTER(c_float)), shape=(n,))
+        v = np.ctypeslib.as_array(ctypes.cast(orc().orc_ctx_v_cache(self.c), POINTER(c_float)), shape=(n,))
+        return k.reshape(self.kv_shape), v.reshape(self.kv_shape)
+
+    def forward(self, token, pos, lm_threads=8, trace=False):
+        """logits (and, with trace, every projection's int32 dots and every
+        activation's (scale, sum)) of one token at position pos."""
+        logits = np.empty(self.cfg["n_vocab"], np.float32)
+        dots = np.empty(self.n_dots, np.int32) if trace else None
+        acts = (Act * (4 * self.cfg["n_layer"]))() if trace else None
+        st = orc().orc_forward_token(ctypes.byref(self.m), self.c, token, pos, _p(logits), lm_threads,
+                                     _p(dots) if trace else None, acts)
+        if st != 0:
+            raise ValueError(f"orc_forward_token: bad token {token} or position {pos}")
+        if not trace:
+            return logits
+        return logits, dots, np.array([(a.scale, a.sum) for a in acts],
+                                      dtype=[("scale", "<f4"), ("sum", "<i4")])
+
+    def close(self):
+        if self.c:
+            orc().orc_ctx_free(self.c)
+            self.c = None
+
+
+class RefDecoder:
+    """The reference's own sllm_forward (oracle/_ref) on a GGUF image of the
+    same model."""
+
+    def __init__(self, model, n_ctx, threads=1):
+        from oracle.gguf_synth import gguf_image
+        self.image = np.frombuffer(gguf_image(model), np.uint8)
+        st = c_int()
+        self.r = ref().ref_model_open(_p(self.image), self.image.nbytes, ctypes.byref(st))
+        if not self.r:
+            raise ValueError(f"ref_model_open: status {st.value}")
+        self.c = ref().ref_ctx_new(self.r, n_ctx)
+        self.pool = ref().ref_pool_create(threads) if threads > 1 else None
+        if self.pool:
+            ref().ref_ctx_set_pool(self.c, self.pool)
+        self.n_vocab = model["cfg"]["n_vocab"]
+
+    def forward(self, token, pos):
+        logits = np.empty(self.n_vocab, np.float32)
+        st = ref().ref_forward(self.r, self.c, token, pos, _p(logits))
+        if st != 0:
+            raise ValueError(f"sllm_forward: status {st}")
+        return logits
+
+    def close(self):
+        if self.c:
+            ref().ref_ctx_free(self.c)
+            self.c = None
+        if self.pool:
+            ref().sllm_pool_destroy(self.pool)
+            self.pool = None
+        if self.r:
+            ref().ref_model_close(self.r)
+            self.r = None

@@ -69,3 +69,58 @@ void ref_gemv_epilogue(sllm_pool *pool, const uint8_t *w, size_t n_rows, size_t 
         y[r] = sllm_i2s_epilogue(dots[r], act->sum, act->scale, ws);
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* the reference's own decode step, on a model held in memory          */
+/* ------------------------------------------------------------------ */
+
+#include <saphira_llm/forward.h>
+#include <saphira_llm/gguf.h>
+
+#include <stdlib.h>
+
+/* A GGUF image parsed in place (src/gguf.c sllm_gguf_open_memory) and the
+ * model loaded from it (src/forward.c:318-455). The image must outlive it. */
+typedef struct ref_model {
+    sllm_gguf   gguf;
+    sllm_model *model;
+} ref_model;
+
+ref_model *ref_model_open(const void *image, size_t size, int *status) {
+    ref_model *r = calloc(1, sizeof *r);
+    if (r == NULL) { *status = SLLM_ERR_NOMEM; return NULL; }
+    char err[256];
+    sllm_status st = sllm_gguf_open_memory(image, size, &r->gguf, err, sizeof err);
+    if (st == SLLM_OK) {
+        st = sllm_model_load(&r->gguf, &r->model);
+        if (st != SLLM_OK) sllm_gguf_close(&r->gguf);
+    }
+    *status = (int) st;
+    if (st != SLLM_OK) { free(r); return NULL; }
+    return r;
+}
+
+void ref_model_close(ref_model *r) {
+    if (r == NULL) return;
+    sllm_model_free(r->model);
+    sllm_gguf_close(&r->gguf);
+    free(r);
+}
+
+sllm_ctx *ref_ctx_new(ref_model *r, int32_t n_ctx) {
+    sllm_ctx *c = NULL;
+    return sllm_ctx_new(r->model, n_ctx, &c) == SLLM_OK ? c : NULL;
+}
+
+void ref_ctx_free(sllm_ctx *c) { sllm_ctx_free(c); }
+
+void ref_ctx_set_pool(sllm_ctx *c, sllm_pool *pool) { sllm_ctx_set_pool(c, pool); }
+
+/* src/forward.c:846-849 */
+int ref_forward(ref_model *r, sllm_ctx *c, int32_t token, int32_t pos, float *logits) {
+    return (int) sllm_forward(r->model, c, token, pos, logits);
+}
+
+/* defined in src/forward.c:876-883 without a header declaration */
+int32_t sllm_argmax(const float *logits, int32_t n);
+int32_t ref_argmax(const float *logits, int32_t n) { return sllm_argmax(logits, n); }

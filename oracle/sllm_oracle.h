@@ -101,6 +101,55 @@ void      orc_gemv_epilogue_parallel(orc_pool *p, const uint8_t *w, size_t n_row
 /* FNV-1a 64 as tests/test_i2s.c:42-50 hashes fixtures */
 uint64_t  orc_fnv1a64(const void *data, size_t n);
 
+/*
+ * The decode step (sllm_oracle_fwd.c): the float operations of
+ * src/ops.c and the token loop of src/forward.c:589-835, in the reference's
+ * order, lane by lane. Pinned against the reference's ops.c / forward.c
+ * compiled into oracle/_ref (tests/test_oracle_fwd.py).
+ */
+float    orc_f16_to_f32(uint16_t h);
+float    orc_f16_to_f32_embd(uint16_t h);                                                  /* src/forward.c:239-262 */
+void     orc_rms_norm(float *dst, const float *x, const float *weight, size_t n, float eps); /* src/ops.c:254-322 */
+float    orc_v_expf(float x);                                                              /* src/ops.c:342-379 */
+void     orc_softmax(float *x, size_t n);                                                  /* src/ops.c:386-422 */
+void     orc_silu(float *x, size_t n);                                                     /* src/ops.c:428-440 */
+void     orc_rope_neox(float *x, size_t n_rot, int32_t pos, float theta, float freq_scale); /* src/ops.c:467-549 */
+void     orc_rope_cos_sin(size_t n_rot, int32_t pos, float theta, float freq_scale, float *cs, float *sn);
+float    orc_dot_f16(const uint16_t *row, const float *x, size_t n);                       /* src/ops.c:106-154 */
+int32_t  orc_argmax(const float *logits, int32_t n);                                       /* src/forward.c:876-883 */
+
+/* A BitNet-b1.58 model held in host memory (the fields of sllm_model that
+ * the decode step reads, src/forward.c:318-455). I2_S tensors include their
+ * 32-byte tails. */
+typedef struct orc_layer {
+    const uint8_t *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    const float   *attn_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
+} orc_layer;
+
+typedef struct orc_model {
+    int32_t          n_layer, n_embd, n_ff, n_head, n_head_kv, n_rot, n_vocab;
+    float            eps, rope_base;
+    const uint16_t  *tok_embd;       /* n_vocab x n_embd f16, also the lm_head */
+    const float     *output_norm;
+    const orc_layer *layers;
+} orc_model;
+
+typedef struct orc_ctx orc_ctx;
+orc_ctx *orc_ctx_new(const orc_model *m, int32_t n_ctx);
+void     orc_ctx_free(orc_ctx *c);
+/* [layer][head_kv][pos][head_dim] f32 caches (src/forward.c:466-518) */
+float   *orc_ctx_k_cache(orc_ctx *c);
+float   *orc_ctx_v_cache(orc_ctx *c);
+/*
+ * One token at position pos (src/forward.c:589-835, n = 1): logits of every
+ * vocabulary row. dots_trace, when not NULL, receives every projection's raw
+ * int32 dots in order (per layer q, k, v, o, gate, up, down); act_trace, when
+ * not NULL, every activation's scale/sum (per layer: attn, o, ffn, down).
+ * lm_threads splits the lm_head rows (results do not depend on it).
+ */
+int      orc_forward_token(const orc_model *m, orc_ctx *c, int32_t token, int32_t pos, float *logits,
+                           int lm_threads, int32_t *dots_trace, orc_act *act_trace);
+
 #ifdef __cplusplus
 }
 #endif

@@ -105,6 +105,7 @@ SYNTH_PROTOTYPES = {
     "sllm_synth_codes": (None, [c_uint64, c_size_t, c_size_t, c_void_p]),
     "sllm_synth_i2s": (c_int, [c_uint64, c_size_t, c_size_t, c_void_p, c_int]),
     "sllm_synth_normal": (None, [c_uint64, c_size_t, c_void_p]),
+    "sllm_synth_normal_f16": (None, [c_uint64, c_size_t, c_void_p, c_int]),
 }
 
 _lib = None
@@ -314,3 +315,49 @@ def synth_normal(seed, count):
     out = np.empty(count, dtype=np.float32)
     synth_lib().sllm_synth_normal(seed, count, ptr(out))
     return out
+
+
+def synth_normal_f16(seed, count, threads=None):
+    """synth_normal(seed, count) rounded to binary16, as uint16 bits."""
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    out = np.empty(count, dtype=np.uint16)
+    synth_lib().sllm_synth_normal_f16(seed, count, ptr(out), threads)
+    return out
+
+
+# BitNet-b1.58-2B shapes (the reference's PHASE4 contract: 30 layers, n_embd
+# 2560, n_ff 6912, 20 query heads of 128, 5 KV heads, vocab 128256, RoPE
+# NeoX base 500000, eps 1e-5)
+BITNET_2B = dict(n_layer=30, n_embd=2560, n_ff=6912, n_head=20, n_head_kv=5, n_rot=128,
+                 n_vocab=128256, eps=1e-5, rope_base=500000.0)
+
+LAYER_I2S = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+LAYER_NORMS = ("attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm")
+
+
+def synth_model(cfg, seed_set=0, threads=None):
+    """A random-init BitNet-b1.58 model of shape `cfg` (see BITNET_2B):
+    uniform ternary I2_S projections with per-tensor scales U(0.5, 2), norm
+    weights N(1, 0.1^2), an F16 N(0, 1) token embedding (also the lm_head).
+    Returns {"cfg": cfg, "tok_embd": uint16[n_vocab * n_embd],
+    "output_norm": f32[n_embd], "layers": [{name: array}]}; I2_S arrays are
+    the packed bytes with their 32-byte tails."""
+    e, f = cfg["n_embd"], cfg["n_ff"]
+    gqa = e // cfg["n_head"] * cfg["n_head_kv"]
+    shapes = {"wq": (e, e), "wk": (gqa, e), "wv": (gqa, e), "wo": (e, e),
+              "w_gate": (f, e), "w_up": (f, e), "w_down": (e, f)}
+    norm_len = {"attn_norm": e, "attn_sub_norm": e, "ffn_norm": e, "ffn_sub_norm": f}
+    model = {"cfg": dict(cfg), "layers": []}
+    model["tok_embd"] = synth_normal_f16(synth_seed(4, seed_set, 0, 900), cfg["n_vocab"] * e, threads)
+    model["output_norm"] = (np.float32(1) + np.float32(0.1) * synth_normal(synth_seed(4, seed_set, 0, 901), e)).astype(np.float32)
+    for il in range(cfg["n_layer"]):
+        layer = {}
+        for m, name in enumerate(LAYER_I2S):
+            n_rows, n = shapes[name]
+            layer[name] = synth_i2s(synth_seed(4, seed_set, il, m), n_rows, n, threads)
+        for m, name in enumerate(LAYER_NORMS):
+            layer[name] = (np.float32(1) + np.float32(0.1) * synth_normal(synth_seed(4, seed_set, il, 16 + m),
+                                                                          norm_len[name])).astype(np.float32)
+        model["layers"].append(layer)
+    return model

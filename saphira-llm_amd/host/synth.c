@@ -130,3 +130,68 @@ void sllm_synth_normal(uint64_t seed, size_t count, float *out) {
         if (i + 1 < count) out[i + 1] = (float) (rad * sin(two_pi * u2));
     }
 }
+
+/* IEEE binary32 -> binary16, round to nearest even (overflow to infinity,
+ * gradual underflow to subnormals) */
+static uint16_t f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t) (sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t) (sign | 0x7C00u);          /* >= 65520: infinity */
+    if (ax < 0x38800000u) {                                               /* below 2^-14: subnormal */
+        float a;
+        memcpy(&a, &ax, sizeof a);
+        return (uint16_t) (sign | (uint32_t) nearbyintf(a * 0x1p24f));   /* exact scaling, RNE */
+    }
+    uint32_t h = ((ax >> 23) - 112u) << 10 | ((ax >> 13) & 0x3FFu);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;           /* may carry into the exponent */
+    return (uint16_t) (sign | h);
+}
+
+typedef struct {
+    uint64_t seed;
+    size_t i0, i1;
+    uint16_t *out;
+} f16_job;
+
+static void normal_f16_range(const f16_job *j) {
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = j->i0; i < j->i1; i += 2) {
+        const uint64_t a = splitmix_at(j->seed, i), b = splitmix_at(j->seed, i + 1);
+        const double u1 = ((double) (a >> 11) + 1.0) * 0x1p-53;
+        const double u2 = (double) (b >> 11) * 0x1p-53;
+        const double rad = sqrt(-2.0 * log(u1));
+        j->out[i] = f32_to_f16((float) (rad * cos(two_pi * u2)));
+        if (i + 1 < j->i1) j->out[i + 1] = f32_to_f16((float) (rad * sin(two_pi * u2)));
+    }
+}
+
+static void *f16_thread(void *arg) {
+    normal_f16_range(arg);
+    return NULL;
+}
+
+/* The values of sllm_synth_normal(seed, count, .) rounded to binary16 (round
+ * to nearest even), split over threads on even indices. */
+void sllm_synth_normal_f16(uint64_t seed, size_t count, uint16_t *out, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    f16_job jobs[64];
+    pthread_t tid[64];
+    int started[64] = { 0 };
+    const size_t pairs = (count + 1) / 2;
+    for (int t = 0; t < threads; ++t) {
+        size_t i0 = 2 * (pairs * (size_t) t / (size_t) threads);
+        size_t i1 = 2 * (pairs * (size_t) (t + 1) / (size_t) threads);
+        if (i1 > count) i1 = count;
+        jobs[t] = (f16_job) { seed, i0, i1, out };
+        if (t > 0) started[t] = pthread_create(&tid[t], NULL, f16_thread, &jobs[t]) == 0;
+    }
+    normal_f16_range(&jobs[0]);
+    for (int t = 1; t < threads; ++t) {
+        if (started[t]) pthread_join(tid[t], NULL);
+        else normal_f16_range(&jobs[t]);
+    }
+}
