@@ -100,17 +100,72 @@ class Workload:
         """One step: the plan's launch."""
         self.dev.plan_run(self.plan)
 
-    def check_against_oracle(self, orc, set_idx=0):
-        """Spot-check one set's outputs (parity is the tests' job; this guards
+    def outputs(self, sets):
+        """(weights, N, K, x, GPU output, label) of every GEMV in `sets`, for
+        the oracle check in the CPU leg (parity is the tests' job; this guards
         the timed configuration itself)."""
-        s = set_idx
-        ws = self.host_w[s]
-        for m, (name, n_rows, n) in enumerate(SHAPES):
-            x = self.x_up[s] if n == K_UP else self.x_dn[s]
-            want = orc.linear(ws[m], n_rows, n, x, orc.DOT_VNNI)[0]
-            got = self.b_y[3 * s + m].download(np.float32, n_rows)
-            if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
-                raise SystemExit(f"bench: output mismatch against the oracle in set {s} {name}")
+        out = []
+        for s in sets:
+            for m, (name, n_rows, n) in enumerate(SHAPES):
+                x = self.x_up[s] if n == K_UP else self.x_dn[s]
+                out.append((self.host_w[s][m], n_rows, n, x,
+                            self.b_y[3 * s + m].download(np.float32, n_rows), f"set {s} {name}"))
+        return out
+
+
+# one BitNet-b1.58-2B block: (name, N, K, activation slot); q/k/v share the
+# attention input, gate/up the FFN input (src/forward.c:645-793)
+BLOCK = [("q", 2560, 2560, 0), ("k", 640, 2560, 0), ("v", 640, 2560, 0), ("o", 2560, 2560, 1),
+         ("gate", N_FF, K_UP, 2), ("up", N_FF, K_UP, 2), ("down", K_UP, N_FF, 3)]
+
+
+def measure_block_plan(amd, dev, layers=30, steps=200):
+    """The per-block decode GEMVs of 30 independently seeded layers (521 MB of
+    packed weights), f32 N(0,1) inputs quantised in-kernel, as one plan: one
+    launch of 210 GEMVs, timed like the main workload. Returns the figures and
+    the inputs / outputs of layers 0 and 29 for the oracle check."""
+    bufs, jobs, keep = [], [], []
+    w_bytes = act_bytes = out_bytes = 0
+    for il in range(layers):
+        xs = {}
+        for slot, n in ((0, K_UP), (1, K_UP), (2, K_UP), (3, N_FF)):
+            x = amd.synth_normal(amd.synth_seed(2, 0, il, 200 + slot), n)
+            xs[slot] = (x, dev.put(x))
+            bufs.append(xs[slot][1])
+            act_bytes += 4 * n
+        for m, (name, n_rows, n, slot) in enumerate(BLOCK):
+            w = amd.synth_i2s(amd.synth_seed(2, 0, il, m), n_rows, n)
+            bw, by = dev.put(w), dev.alloc(4 * n_rows)
+            bufs += [bw, by]
+            jobs.append(amd.GemvJob(bw.ptr, n_rows, n, xs[slot][1].ptr, None, None, by.ptr, None))
+            w_bytes += n_rows * n // 4 + 4
+            out_bytes += 4 * n_rows
+            if il in (0, layers - 1):
+                keep.append((w, n_rows, n, xs[slot][0], by, f"layer {il} {name}"))
+    plan = dev.plan(jobs)
+    for _ in range(20):
+        dev.plan_run(plan)
+    dev.sync()
+    checks = [(w, n_rows, n, x, by.download(np.float32, n_rows), what) for w, n_rows, n, x, by, what in keep]
+    dev.events(2)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.record(0)
+    for _ in range(steps):
+        dev.plan_run(plan)
+    dev.record(1)
+    dev.sync()
+    wall_us = (time.perf_counter() - t0) * 1e6 / steps
+    ev_us = dev.elapsed(0, 1) * 1e3 / steps
+    dev.plan_destroy(plan)
+    for b in bufs:
+        b.free()
+    total = w_bytes + act_bytes + out_bytes
+    return checks, {"workload": "30 independently seeded BitNet-2B blocks (q/o 2560x2560, k/v 640x2560, gate/up 6912x2560, "
+                        "down 2560x6912), 210 GEMVs in one launch, f32 inputs quantised in-kernel",
+            "weight_bytes": w_bytes, "bytes_per_launch": total, "us_per_launch": round(ev_us, 2),
+            "GBps": round(total / (ev_us * 1e-6) / 1e9, 1), "wall_us_per_launch": round(wall_us, 2),
+            "frac_of_peak": round(total / (ev_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "steps": steps}
 
 
 def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
@@ -135,16 +190,23 @@ def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
             "read_GBps": round(nbytes / read_ms / 1e6, 1), "bytes": nbytes}
 
 
-def cpu_baseline(wl, seconds=6.0):
-    """The reference's CPU path (or the oracle's restatement) over a bounded
-    sample of the same workload: passes over the 32 sets, each set quantise
-    -> GEMV -> epilogue for gate/up/down, row-parallel over the reference's
-    pool. Timed at 1 thread and at all threads; at all threads both with the
+def cpu_baseline(wl, checks, seconds=6.0):
+    """The CPU leg. First the checker: the GPU outputs kept in `checks`
+    against the oracle, bit for bit. Then the baseline: the reference's CPU
+    path (or the oracle's restatement) over a bounded sample of the same
+    workload -- passes over the 32 sets, each set quantise -> GEMV ->
+    epilogue for gate/up/down, row-parallel over the reference's pool --
+    timed at 1 thread and at all threads; at all threads both with the
     reference's own split policy (src/forward.c:145-205, which keeps GEMVs
     below 512 rows per thread on one thread) and with every GEMV
     distributed; the faster all-thread figure is the baseline."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
+    for w, n_rows, n, x, got, what in checks:
+        want = orc.linear(w, n_rows, n, x, orc.DOT_VNNI)[0]
+        if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+            raise SystemExit(f"bench: output mismatch against the oracle ({what})")
+    log(f"{len(checks)} GPU outputs (sets 0 and 31, block layers 0 and 29) match the oracle bit for bit")
     use_ref = orc.ref_available()
     try:
         threads = min(16, len(os.sched_getaffinity(0)))
@@ -243,12 +305,6 @@ def main():
     for _ in range(args.warmup):
         wl.step()
     dev.sync()
-    if not args.no_cpu:
-        sys.path.insert(0, ROOT)
-        from oracle import oracle as orc
-        wl.check_against_oracle(orc, 0)
-        wl.check_against_oracle(orc, wl.sets - 1)
-        log("outputs of sets 0 and 31 match the oracle bit for bit")
 
     K = args.steps
     dev.events(2)
@@ -276,6 +332,10 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
+    checks = wl.outputs([0, wl.sets - 1])
+    block_checks, block30 = measure_block_plan(amd, dev)
+    log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
+
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
@@ -297,10 +357,11 @@ def main():
             "avg_launch_us": round(gemv_avg * 1e3, 2), "bytes_per_launch": wl.gemv_bytes,
         },
         "calibration": calib,
+        "block30": block30,
     }
     if not args.no_cpu:
         log("timing the CPU baseline")
-        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 
