@@ -1,0 +1,137 @@
+/*
+ * sllm_gfx950_decode.h -- a BitNet-b1.58 decode step on one gfx950 GPU.
+ *
+ * The device-resident form of the reference's forward pass at n = 1
+ * (include/saphira_llm/forward.h:23-165, src/forward.c:589-883): the model's
+ * tensors uploaded once, the KV cache and every activation kept in HBM, one
+ * token per sllm_gfx950_forward. The arithmetic follows the reference
+ * operation for operation, so the logits are the reference's bit for bit and
+ * so is every int8 activation and int32 dot on the way. Statuses are those of
+ * sllm_gfx950.h (the reference's sllm_status values where one applies).
+ *
+ * The library must be open (sllm_gfx950_open). Work is enqueued on the
+ * library stream; calls that return host data synchronise it.
+ */
+#ifndef SAPHIRA_AMD_SLLM_GFX950_DECODE_H
+#define SAPHIRA_AMD_SLLM_GFX950_DECODE_H
+
+#include <saphira_amd/sllm_gfx950.h>
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One block's tensors in host memory, as the reference's sllm_layer holds
+ * them after sllm_model_load (src/forward.c:397-430): I2_S matrices with
+ * their 32-byte tails, f32 norm weights. */
+typedef struct sllm_gfx950_layer_desc {
+    const uint8_t *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    const float   *attn_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
+} sllm_gfx950_layer_desc;
+
+/* The model's hyper-parameters and tensors (the fields of sllm_model the
+ * forward pass reads, src/forward.c:318-455). tok_embd is n_vocab rows of
+ * n_embd binary16 values, the token embedding and the tied output
+ * projection. */
+typedef struct sllm_gfx950_model_desc {
+    int32_t  n_layer, n_embd, n_ff, n_head, n_head_kv, n_rot, n_vocab;
+    float    eps;          /* RMSNorm epsilon */
+    float    rope_base;    /* RoPE frequency base */
+    const uint16_t *tok_embd;
+    const float    *output_norm;
+    const sllm_gfx950_layer_desc *layers;   /* n_layer entries */
+} sllm_gfx950_model_desc;
+
+typedef struct sllm_gfx950_model sllm_gfx950_model;
+typedef struct sllm_gfx950_ctx   sllm_gfx950_ctx;
+
+/* Largest shapes the decode kernels take: head dimension, query heads per KV
+ * head, n_embd / n_ff (the slab GEMV's LDS row), and query heads per KV head
+ * times n_ctx (the softmax rows held in LDS). */
+#define SLLM_GFX950_DEC_MAX_HEAD_DIM 128
+#define SLLM_GFX950_DEC_MAX_GQA      8
+#define SLLM_GFX950_DEC_MAX_WIDTH    7168
+#define SLLM_GFX950_DEC_MAX_GQA_CTX  16384
+
+/*
+ * sllm_model_load (forward.h:33) for the device: copies every tensor of
+ * `desc` into device memory, byte for byte. The host buffers may be freed
+ * afterwards. Shapes are checked as src/forward.c:306-455 checks them
+ * (I2_S widths multiples of 128) plus the kernel limits above:
+ * SLLM_GFX950_ERR_TENSOR_SHAPE or SLLM_GFX950_ERR_TOO_LARGE.
+ */
+int  sllm_gfx950_model_upload(const sllm_gfx950_model_desc *desc, sllm_gfx950_model **out);
+void sllm_gfx950_model_free(sllm_gfx950_model *m);
+
+/*
+ * sllm_ctx_new (forward.h:46): a KV cache of n_ctx positions
+ * ([layer][head_kv][pos][head_dim] f32, as src/forward.c:466-518) and the
+ * activations, all on the device, plus the RoPE table for positions
+ * 0..n_ctx-1 (cos / sin built with the host C library, as the reference's
+ * src/ops.c:467-549 builds them per token).
+ */
+int  sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_ctx **out);
+void sllm_gfx950_ctx_free(sllm_gfx950_ctx *c);
+/* sllm_ctx_reset (forward.h:50): zero the live cache prefix, n_past = 0 */
+int  sllm_gfx950_ctx_reset(sllm_gfx950_ctx *c);
+int32_t sllm_gfx950_ctx_n_past(const sllm_gfx950_ctx *c);
+
+/*
+ * sllm_forward (forward.h:83): one token at `pos`. Refused as the reference
+ * refuses it (src/forward.c:592-608): pos < n_past (rewinding) or
+ * pos >= n_ctx, token outside [0, n_vocab) -> SLLM_GFX950_ERR_ARG. logits:
+ * n_vocab floats of host memory, or NULL to leave them on the device (read
+ * them with sllm_gfx950_ctx_logits). Returns after the step has been
+ * enqueued, or -- logits given -- completed.
+ */
+int  sllm_gfx950_forward(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, int32_t token, int32_t pos,
+                         float *logits);
+
+/*
+ * sllm_generate_greedy (forward.h:124): forward the prompt, then n_new
+ * tokens, each the argmax (src/forward.c:876-883) of the previous logits;
+ * out receives the n_new ids. The token loop runs on the device: each step's
+ * output kernel feeds the next token itself, so the host enqueues the whole
+ * generation and synchronises once. SLLM_GFX950_ERR_TOO_LARGE past n_ctx.
+ */
+int  sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *prompt,
+                                 int32_t n_prompt, int32_t n_new, int32_t *out);
+
+/* The device copy of the last logits (n_vocab floats), and their argmax
+ * (synchronises). */
+const float *sllm_gfx950_ctx_logits(const sllm_gfx950_ctx *c);
+int  sllm_gfx950_ctx_argmax(sllm_gfx950_ctx *c, int32_t *token);
+
+/*
+ * Fill positions [0, n_pos) of the cache from host memory -- k and v laid
+ * out [layer][head_kv][pos][head_dim] with n_pos positions per head -- and
+ * set n_past = n_pos: a restored context (the reference's sllm_state_load,
+ * forward.h:162, without the file).
+ */
+int  sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos);
+
+/*
+ * Capture one token's launches in a HIP graph and replay it for every later
+ * token (on = 1), or launch them one by one (on = 0, the default). The
+ * results are the same; the graph saves host launch time.
+ */
+int  sllm_gfx950_ctx_set_graph(sllm_gfx950_ctx *c, int on);
+
+/*
+ * Parity tracing. dots: device memory for every projection's raw int32 dots
+ * of one token, per layer q, k, v, o, gate, up, down (n_layer * (2*n_embd +
+ * 2*gqa + 3*n_ff) + ... = sllm_gfx950_trace_dots(m) values); acts: device
+ * memory for 4 * n_layer activations (per layer: attn, o, ffn, down
+ * quantisation). NULL, NULL stops tracing. Each forward overwrites them.
+ */
+size_t sllm_gfx950_trace_dots(const sllm_gfx950_model *m);
+int  sllm_gfx950_ctx_trace(sllm_gfx950_ctx *c, int32_t *dots, sllm_gfx950_act *acts);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAPHIRA_AMD_SLLM_GFX950_DECODE_H */

@@ -51,6 +51,20 @@ class KernelRow(ctypes.Structure):
                 ("gemv", ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p))]
 
 
+class LayerDesc(ctypes.Structure):
+    """sllm_gfx950_layer_desc: one block's host tensors."""
+    _fields_ = [(n, c_void_p) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
+                                        "attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm")]
+
+
+class ModelDesc(ctypes.Structure):
+    """sllm_gfx950_model_desc."""
+    _fields_ = [("n_layer", c_int32), ("n_embd", c_int32), ("n_ff", c_int32), ("n_head", c_int32),
+                ("n_head_kv", c_int32), ("n_rot", c_int32), ("n_vocab", c_int32),
+                ("eps", c_float), ("rope_base", c_float),
+                ("tok_embd", c_void_p), ("output_norm", c_void_p), ("layers", POINTER(LayerDesc))]
+
+
 # Every function the C ABI exports: name -> (restype, argtypes).
 PROTOTYPES = {
     "sllm_gfx950_open": (c_int, [c_int]),
@@ -97,6 +111,20 @@ PROTOTYPES = {
     "sllm_kdispatch_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "sllm_kdispatch_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),
     "sllm_kdispatch_gemv": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "sllm_gfx950_model_upload": (c_int, [POINTER(ModelDesc), POINTER(c_void_p)]),
+    "sllm_gfx950_model_free": (None, [c_void_p]),
+    "sllm_gfx950_ctx_new": (c_int, [c_void_p, c_int32, POINTER(c_void_p)]),
+    "sllm_gfx950_ctx_free": (None, [c_void_p]),
+    "sllm_gfx950_ctx_reset": (c_int, [c_void_p]),
+    "sllm_gfx950_ctx_n_past": (c_int32, [c_void_p]),
+    "sllm_gfx950_forward": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "sllm_gfx950_generate_greedy": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "sllm_gfx950_ctx_logits": (c_void_p, [c_void_p]),
+    "sllm_gfx950_ctx_argmax": (c_int, [c_void_p, POINTER(c_int32)]),
+    "sllm_gfx950_ctx_kv_load": (c_int, [c_void_p, c_void_p, c_void_p, c_int32]),
+    "sllm_gfx950_ctx_set_graph": (c_int, [c_void_p, c_int]),
+    "sllm_gfx950_trace_dots": (c_size_t, [c_void_p]),
+    "sllm_gfx950_ctx_trace": (c_int, [c_void_p, c_void_p, c_void_p]),
 }
 
 SYNTH_PROTOTYPES = {
@@ -106,6 +134,7 @@ SYNTH_PROTOTYPES = {
     "sllm_synth_i2s": (c_int, [c_uint64, c_size_t, c_size_t, c_void_p, c_int]),
     "sllm_synth_normal": (None, [c_uint64, c_size_t, c_void_p]),
     "sllm_synth_normal_f16": (None, [c_uint64, c_size_t, c_void_p, c_int]),
+    "sllm_expf_mismatches": (c_uint64, [c_uint64, c_uint64, c_int, POINTER(ctypes.c_uint32)]),
 }
 
 _lib = None
@@ -361,3 +390,110 @@ def synth_model(cfg, seed_set=0, threads=None):
                                                                           norm_len[name])).astype(np.float32)
         model["layers"].append(layer)
     return model
+
+
+def model_desc(model):
+    """(ModelDesc, keep-alive list) describing a synth_model dict's host arrays."""
+    cfg = model["cfg"]
+    keep = []
+
+    def p(a):
+        a = np.ascontiguousarray(a)
+        keep.append(a)
+        return a.ctypes.data_as(c_void_p)
+
+    layers = (LayerDesc * cfg["n_layer"])()
+    for il, L in enumerate(model["layers"]):
+        for name in LAYER_I2S + LAYER_NORMS:
+            setattr(layers[il], name, p(L[name]))
+    keep.append(layers)
+    d = ModelDesc(cfg["n_layer"], cfg["n_embd"], cfg["n_ff"], cfg["n_head"], cfg["n_head_kv"], cfg["n_rot"],
+                  cfg["n_vocab"], cfg["eps"], cfg["rope_base"], p(model["tok_embd"]), p(model["output_norm"]),
+                  layers)
+    return d, keep
+
+
+class DeviceDecoder:
+    """A model uploaded with sllm_gfx950_model_upload and one context of
+    n_ctx positions (sllm_gfx950_ctx_new): the decode step on the GPU."""
+
+    def __init__(self, dev, model, n_ctx):
+        self.dev = dev
+        self.cfg = dict(model["cfg"])
+        L = lib()
+        d, keep = model_desc(model)
+        m = c_void_p()
+        check(L.sllm_gfx950_model_upload(ctypes.byref(d), ctypes.byref(m)), "model_upload")
+        del keep
+        self.m = m
+        c = c_void_p()
+        st = L.sllm_gfx950_ctx_new(m, n_ctx, ctypes.byref(c))
+        if st != 0:
+            L.sllm_gfx950_model_free(m)
+            check(st, "ctx_new")
+        self.c = c
+        self.n_ctx = n_ctx
+
+    def forward(self, token, pos, logits=True):
+        """Logits (float32[n_vocab]) of `token` at `pos`, or None with logits=False."""
+        out = np.empty(self.cfg["n_vocab"], np.float32) if logits else None
+        check(lib().sllm_gfx950_forward(self.m, self.c, token, pos, ptr(out) if logits else None), "forward")
+        return out
+
+    def status_forward(self, token, pos):
+        """The raw status of a forward (for argument checks)."""
+        return lib().sllm_gfx950_forward(self.m, self.c, token, pos, None)
+
+    def argmax(self):
+        t = c_int32()
+        check(lib().sllm_gfx950_ctx_argmax(self.c, ctypes.byref(t)), "ctx_argmax")
+        return t.value
+
+    def generate(self, prompt, n_new):
+        pr = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        check(lib().sllm_gfx950_generate_greedy(self.m, self.c, ptr(pr) if pr.size else None, pr.size, n_new,
+                                                ptr(out)), "generate_greedy")
+        return out[:n_new]
+
+    def kv_load(self, k, v, n_pos):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        check(lib().sllm_gfx950_ctx_kv_load(self.c, ptr(k), ptr(v), n_pos), "ctx_kv_load")
+
+    def reset(self):
+        check(lib().sllm_gfx950_ctx_reset(self.c), "ctx_reset")
+
+    def n_past(self):
+        return lib().sllm_gfx950_ctx_n_past(self.c)
+
+    def set_graph(self, on):
+        check(lib().sllm_gfx950_ctx_set_graph(self.c, 1 if on else 0), "ctx_set_graph")
+
+    def trace_start(self):
+        """Record every projection's dots and every activation's scale/sum."""
+        n = lib().sllm_gfx950_trace_dots(self.m)
+        self.t_dots = self.dev.alloc(4 * n)
+        self.t_acts = self.dev.alloc(8 * 4 * self.cfg["n_layer"])
+        self.t_n = n
+        check(lib().sllm_gfx950_ctx_trace(self.c, self.t_dots.vp, self.t_acts.vp), "ctx_trace")
+
+    def trace_read(self):
+        self.dev.sync()
+        dots = self.t_dots.download(np.int32, self.t_n)
+        raw = self.t_acts.download(np.uint8, 8 * 4 * self.cfg["n_layer"])
+        acts = np.frombuffer(raw.tobytes(), dtype=[("scale", "<f4"), ("sum", "<i4")])
+        return dots, acts
+
+    def trace_stop(self):
+        check(lib().sllm_gfx950_ctx_trace(self.c, None, None), "ctx_trace")
+        self.t_dots.free()
+        self.t_acts.free()
+
+    def close(self):
+        if getattr(self, "c", None):
+            lib().sllm_gfx950_ctx_free(self.c)
+            self.c = None
+        if getattr(self, "m", None):
+            lib().sllm_gfx950_model_free(self.m)
+            self.m = None

@@ -1,0 +1,723 @@
+/*
+ * decode.c -- the BitNet-b1.58 decode step on gfx950 (sllm_gfx950_decode.h).
+ *
+ * Host side of decode_kernels.hip: uploads a model, lays a context out in one
+ * device allocation, and enqueues one token as a fixed sequence of launches
+ * that read the token and position from a device-resident step record, so
+ * the same sequence (or a HIP graph of it) serves every position and the
+ * output kernel can feed the next token itself.
+ *
+ * Argument structs mirror decode_kernels.hip field for field (sizes asserted).
+ */
+#define _POSIX_C_SOURCE 200809L
+
+#include "shim_internal.h"
+
+#include <saphira_amd/sllm_gfx950_decode.h>
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* device-side layouts                                                 */
+/* ------------------------------------------------------------------ */
+
+typedef struct k_dec_step {
+    int32_t        token, pos, next, advance;
+    uint64_t       key;
+    uint32_t       ticket, err;
+    const int32_t *feed;
+    int32_t       *gen;
+    int32_t        n_feed, i_feed, n_gen, cap_gen;
+} k_dec_step;
+
+typedef struct k_dec_stage {
+    const void       *a;
+    const float      *b;
+    float            *v_out;
+    const float      *norm_w;
+    const k_dec_step *step;
+    int8_t           *q_out;
+    sllm_gfx950_act  *act_out;
+    float             eps;
+    uint32_t          k, mode, pad;
+} k_dec_stage;
+
+typedef struct k_dec_attn {
+    const float      *q, *k, *v;
+    float            *k_cache, *v_cache;
+    const float      *rope;
+    float            *scores;
+    float            *out;
+    const k_dec_step *step;
+    float             attn_scale;
+    uint32_t          n_head, n_kv, hd, half, n_ctx, pad;
+} k_dec_attn;
+
+typedef struct k_dec_lm {
+    const float    *a, *b;
+    const float    *norm_w;
+    const uint16_t *embd;
+    float          *logits;
+    k_dec_step     *step;
+    float           eps;
+    uint32_t        n_embd, n_vocab, pad;
+} k_dec_lm;
+
+_Static_assert(sizeof(k_dec_step) == 64, "k_dec_step must match dec_step");
+_Static_assert(sizeof(k_dec_stage) == 72, "k_dec_stage must match dec_stage");
+_Static_assert(sizeof(k_dec_attn) == 104, "k_dec_attn must match dec_attn");
+_Static_assert(sizeof(k_dec_lm) == 64, "k_dec_lm must match dec_lm");
+
+enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2 };
+
+/* kernel constants (decode_kernels.hip) */
+#define ATT_THREADS 256
+#define ATT_POS     64
+#define PV_SLICE    16
+#define LM_THREADS  256
+#define LM_ROWS     64
+#define LM_MAX_E    8192
+
+/* projections of a block, in the reference's order (src/forward.c:642-793) */
+enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, N_PROJ };
+/* GEMV stages of a block */
+enum { S_QKV, S_O, S_FFN, S_DOWN, N_STAGE };
+
+#define BOS_TOKEN 128000   /* src/forward.c:909 */
+
+/* ------------------------------------------------------------------ */
+/* model                                                               */
+/* ------------------------------------------------------------------ */
+
+typedef struct dev_layer {
+    uint8_t *w[N_PROJ];
+    float   *attn_norm, *attn_sub_norm, *ffn_norm, *ffn_sub_norm;
+} dev_layer;
+
+struct sllm_gfx950_model {
+    int32_t    n_layer, n_embd, n_ff, n_head, n_head_kv, n_rot, n_vocab, hd, gqa;
+    float      eps, rope_base;
+    void      *blob;
+    uint16_t  *tok_embd;
+    float     *output_norm;
+    dev_layer *layers;
+};
+
+static size_t align256(size_t v) { return (v + 255u) & ~(size_t) 255u; }
+static size_t i2s_bytes(size_t rows, size_t k) { return rows * k / 4 + 32; }
+
+/* (rows, K) of each projection */
+static void proj_shape(const struct sllm_gfx950_model *m, int p, size_t *rows, size_t *k) {
+    const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
+    static const int kind[N_PROJ] = { 0, 1, 1, 0, 2, 2, 3 };
+    switch (kind[p]) {
+    case 0:  *rows = e; *k = e; break;
+    case 1:  *rows = g; *k = e; break;
+    case 2:  *rows = f; *k = e; break;
+    default: *rows = e; *k = f; break;
+    }
+}
+
+static int check_desc(const sllm_gfx950_model_desc *d) {
+    if (d->n_layer < 1 || d->n_embd < 1 || d->n_ff < 1 || d->n_head < 1 || d->n_head_kv < 1 ||
+        d->n_vocab < 1 || d->n_rot < 0 || d->tok_embd == NULL || d->output_norm == NULL || d->layers == NULL) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "model: missing tensors or non-positive sizes");
+    }
+    for (int32_t il = 0; il < d->n_layer; ++il) {
+        const sllm_gfx950_layer_desc *L = &d->layers[il];
+        if (!L->wq || !L->wk || !L->wv || !L->wo || !L->w_gate || !L->w_up || !L->w_down ||
+            !L->attn_norm || !L->attn_sub_norm || !L->ffn_norm || !L->ffn_sub_norm) {
+            return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "model: layer %d lacks a tensor", il);
+        }
+    }
+    /* need_i2s (src/forward.c:306-316): every I2_S width a multiple of 128 */
+    if (d->n_embd % 128 || d->n_ff % 128) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "model: n_embd %d / n_ff %d not multiples of 128",
+                              d->n_embd, d->n_ff);
+    }
+    if (d->n_embd % d->n_head || d->n_head % d->n_head_kv) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "model: heads do not divide n_embd / n_head");
+    }
+    const int32_t hd = d->n_embd / d->n_head, grp = d->n_head / d->n_head_kv;
+    if (d->n_rot > hd) return sllm_shim_fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "model: n_rot %d > head dim %d", d->n_rot, hd);
+    if (hd > SLLM_GFX950_DEC_MAX_HEAD_DIM || hd % PV_SLICE || grp > SLLM_GFX950_DEC_MAX_GQA ||
+        d->n_embd > SLLM_GFX950_DEC_MAX_WIDTH || d->n_ff > SLLM_GFX950_DEC_MAX_WIDTH) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_TOO_LARGE,
+                              "model: head dim %d (<= %d, multiple of %d), %d query heads per KV head (<= %d), "
+                              "widths %d / %d (<= %d)", hd, SLLM_GFX950_DEC_MAX_HEAD_DIM, PV_SLICE, grp,
+                              SLLM_GFX950_DEC_MAX_GQA, d->n_embd, d->n_ff, SLLM_GFX950_DEC_MAX_WIDTH);
+    }
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_model_upload(const sllm_gfx950_model_desc *d, sllm_gfx950_model **out) {
+    if (!sllm_shim_is_open()) return sllm_shim_fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open");
+    if (d == NULL || out == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "model_upload: NULL argument");
+    *out = NULL;
+    int st = check_desc(d);
+    if (st != SLLM_GFX950_OK) return st;
+    struct sllm_gfx950_model *m = calloc(1, sizeof *m);
+    if (m == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "model_upload: host");
+    m->n_layer = d->n_layer; m->n_embd = d->n_embd; m->n_ff = d->n_ff; m->n_head = d->n_head;
+    m->n_head_kv = d->n_head_kv; m->n_rot = d->n_rot; m->n_vocab = d->n_vocab;
+    m->hd = d->n_embd / d->n_head;
+    m->gqa = m->hd * d->n_head_kv;
+    m->eps = d->eps;
+    m->rope_base = d->rope_base;
+    m->layers = calloc((size_t) d->n_layer, sizeof *m->layers);
+    if (m->layers == NULL) { free(m); return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "model_upload: host"); }
+
+    const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff;
+    size_t total = align256((size_t) m->n_vocab * e * 2) + align256(e * 4);
+    for (int32_t il = 0; il < m->n_layer; ++il) {
+        for (int p = 0; p < N_PROJ; ++p) {
+            size_t rows, k;
+            proj_shape(m, p, &rows, &k);
+            total += align256(i2s_bytes(rows, k));
+        }
+        total += 3 * align256(e * 4) + align256(f * 4);
+    }
+    hipError_t he = hipMalloc(&m->blob, total);
+    if (he != hipSuccess) {
+        free(m->layers);
+        free(m);
+        return sllm_shim_hip_fail(he, "model_upload: hipMalloc");
+    }
+    uint8_t *at = m->blob;
+#define PUT(dst, src, bytes)                                                                   \
+    do {                                                                                       \
+        (dst) = (void *) at;                                                                   \
+        if (he == hipSuccess) he = hipMemcpy(at, (src), (bytes), hipMemcpyHostToDevice);       \
+        at += align256(bytes);                                                                 \
+    } while (0)
+    PUT(m->tok_embd, d->tok_embd, (size_t) m->n_vocab * e * 2);
+    PUT(m->output_norm, d->output_norm, e * 4);
+    for (int32_t il = 0; il < m->n_layer; ++il) {
+        const sllm_gfx950_layer_desc *L = &d->layers[il];
+        dev_layer *D = &m->layers[il];
+        const uint8_t *src[N_PROJ] = { L->wq, L->wk, L->wv, L->wo, L->w_gate, L->w_up, L->w_down };
+        for (int p = 0; p < N_PROJ; ++p) {
+            size_t rows, k;
+            proj_shape(m, p, &rows, &k);
+            PUT(D->w[p], src[p], i2s_bytes(rows, k));
+        }
+        PUT(D->attn_norm, L->attn_norm, e * 4);
+        PUT(D->attn_sub_norm, L->attn_sub_norm, e * 4);
+        PUT(D->ffn_norm, L->ffn_norm, e * 4);
+        PUT(D->ffn_sub_norm, L->ffn_sub_norm, f * 4);
+    }
+#undef PUT
+    if (he != hipSuccess) {
+        hipFree(m->blob);
+        free(m->layers);
+        free(m);
+        return sllm_shim_hip_fail(he, "model_upload: hipMemcpy");
+    }
+    *out = m;
+    return SLLM_GFX950_OK;
+}
+
+void sllm_gfx950_model_free(sllm_gfx950_model *m) {
+    if (m == NULL) return;
+    if (sllm_shim_is_open()) hipFree(m->blob);
+    free(m->layers);
+    free(m);
+}
+
+size_t sllm_gfx950_trace_dots(const sllm_gfx950_model *m) {
+    if (m == NULL) return 0;
+    return (size_t) m->n_layer * (3 * (size_t) m->n_embd + 2 * (size_t) m->gqa + 2 * (size_t) m->n_ff);
+}
+
+/* ------------------------------------------------------------------ */
+/* context                                                             */
+/* ------------------------------------------------------------------ */
+
+typedef struct stage_launch {
+    uint32_t desc_off;     /* first descriptor of the stage */
+    uint32_t n_wg;         /* its workgroups (a multiple of 8) */
+} stage_launch;
+
+struct sllm_gfx950_ctx {
+    const struct sllm_gfx950_model *m;
+    int32_t       n_ctx, n_past;
+    void         *dev;
+    float        *k_cache, *v_cache, *rope, *scores, *logits;
+    float        *x, *ffn_inp, *qkv, *attn, *o, *h, *down;
+    k_dec_step   *step;
+    int32_t      *feed, *gen;
+    k_dec_stage  *stages;          /* device, n_layer * N_STAGE */
+    k_gemv_job   *jobs;            /* device, n_layer * N_PROJ */
+    k_wg_desc    *descs;           /* device */
+    k_gemv_job   *jobs_host;       /* host copy, for tracing */
+    k_dec_stage  *stages_host;
+    stage_launch *launch;          /* n_layer * N_STAGE */
+    k_dec_attn   *attn_args;       /* n_layer */
+    k_dec_lm      lm_args;
+    size_t        kv_per_layer;    /* floats */
+    hipFunction_t f_gemv, f_scores, f_pv, f_lm;
+    int           graph_on, graph_ready;
+    hipGraph_t    graph;
+    hipGraphExec_t graph_exec;
+};
+
+/* Workgroups of a projection's GEMV: one row group each (decode GEMVs are a
+ * few MB, and latency, not bandwidth per workgroup, bounds them). */
+static uint32_t proj_slabs(const struct sllm_gfx950_model *m, int p, int *variant) {
+    size_t rows, k;
+    proj_shape(m, p, &rows, &k);
+    *variant = sllm_shim_slab_variant((uint32_t) k);
+    const uint32_t g = sllm_shim_slab_group_rows(*variant);
+    return (uint32_t) ((rows + g - 1) / g);
+}
+
+static uint32_t pad8(uint32_t v) { return (v + 7u) & ~7u; }
+
+/* the stage each projection belongs to, and whether it leads a gate/up pair */
+static const int proj_stage[N_PROJ] = { S_QKV, S_QKV, S_QKV, S_O, S_FFN, S_FFN, S_DOWN };
+
+static void fill_tables(sllm_gfx950_ctx *c, k_wg_desc *descs, int32_t *trace_dots, sllm_gfx950_act *trace_acts) {
+    const struct sllm_gfx950_model *m = c->m;
+    const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
+    uint32_t nd = 0;
+    int32_t *tr = trace_dots;
+    for (int32_t il = 0; il < m->n_layer; ++il) {
+        const dev_layer *L = &m->layers[il];
+        k_gemv_job *J = c->jobs_host + (size_t) il * N_PROJ;
+        float *out_f[N_PROJ] = { c->qkv, c->qkv + e, c->qkv + e + g, c->o, c->h, NULL, c->down };
+        for (int p = 0; p < N_PROJ; ++p) {
+            size_t rows, k;
+            proj_shape(m, p, &rows, &k);
+            int variant;
+            (void) proj_slabs(m, p, &variant);
+            J[p] = (k_gemv_job) { L->w[p], NULL, NULL, NULL, out_f[p], tr, (uint32_t) rows, (uint32_t) k,
+                                  (uint32_t) variant, 0 };
+            if (tr != NULL) tr += rows;
+        }
+        k_dec_stage *S = c->stages_host + (size_t) il * N_STAGE;
+        const k_dec_stage *dev_st = c->stages + (size_t) il * N_STAGE;
+        (void) dev_st;
+        sllm_gfx950_act *ta = trace_acts != NULL ? trace_acts + (size_t) il * 4 : NULL;
+        S[S_QKV] = (k_dec_stage) {
+            il == 0 ? (const void *) m->tok_embd : (const void *) c->down, il == 0 ? NULL : c->ffn_inp,
+            c->x, L->attn_norm, c->step, NULL, ta ? ta + 0 : NULL, m->eps, (uint32_t) e,
+            il == 0 ? IN_EMBED : IN_RESID, 0 };
+        S[S_O] = (k_dec_stage) { c->attn, NULL, NULL, L->attn_sub_norm, c->step, NULL, ta ? ta + 1 : NULL,
+                                 m->eps, (uint32_t) e, IN_PLAIN, 0 };
+        S[S_FFN] = (k_dec_stage) { c->o, c->x, c->ffn_inp, L->ffn_norm, c->step, NULL, ta ? ta + 2 : NULL,
+                                   m->eps, (uint32_t) e, IN_RESID, 0 };
+        S[S_DOWN] = (k_dec_stage) { c->h, NULL, NULL, L->ffn_sub_norm, c->step, NULL, ta ? ta + 3 : NULL,
+                                    m->eps, (uint32_t) f, IN_PLAIN, 0 };
+        /* descriptors: per stage, every projection's slabs; gate and up share
+         * theirs (WG_PAIR on gate, none for up); the stage's first workgroup
+         * publishes */
+        for (int s = 0; s < N_STAGE; ++s) {
+            stage_launch *sl = &c->launch[(size_t) il * N_STAGE + s];
+            sl->desc_off = nd;
+            uint32_t first = nd;
+            for (int p = 0; p < N_PROJ; ++p) {
+                if (proj_stage[p] != s || p == P_UP) continue;
+                int variant;
+                const uint32_t n = proj_slabs(m, p, &variant);
+                for (uint32_t w = 0; w < n; ++w) {
+                    uint32_t flags = (p == P_GATE) ? WG_PAIR : 0u;
+                    if (nd == first) flags |= WG_PUBLISH;
+                    descs[nd++] = (k_wg_desc) { (uint32_t) (il * N_PROJ + p), w, n, flags };
+                }
+            }
+            while ((nd - first) % 8) descs[nd++] = (k_wg_desc) { 0, 0, 0, 0 };
+            sl->n_wg = nd - first;
+        }
+    }
+}
+
+static uint32_t count_descs(const struct sllm_gfx950_model *m) {
+    uint32_t per_layer = 0;
+    for (int s = 0; s < N_STAGE; ++s) {
+        uint32_t n = 0;
+        for (int p = 0; p < N_PROJ; ++p) {
+            if (proj_stage[p] != s || p == P_UP) continue;
+            int variant;
+            n += proj_slabs(m, p, &variant);
+        }
+        per_layer += pad8(n);
+    }
+    return per_layer * (uint32_t) m->n_layer;
+}
+
+/* cos / sin of every (position, pair) as the reference computes them per
+ * token (src/ops.c:467-549): theta_scale = powf(base, -2/n_rot) with n_rot
+ * made even, the angle of pair k at pos is (float)pos times theta_scale k
+ * times over (one f32 product per step), through the C library's cosf / sinf */
+static void rope_table(const struct sllm_gfx950_model *m, int32_t n_ctx, float *out) {
+    const int32_t n_rot = m->n_rot - (m->n_rot % 2);
+    const int32_t half = n_rot / 2;
+    if (half == 0) return;
+    const float theta_scale = powf(m->rope_base, -2.0f / (float) n_rot);
+    for (int32_t pos = 0; pos < n_ctx; ++pos) {
+        float theta = (float) pos;
+        float *row = out + (size_t) pos * (size_t) half * 2;
+        for (int32_t k = 0; k < half; ++k) {
+            const float ang = 1.0f * theta;
+            row[2 * k] = cosf(ang);
+            row[2 * k + 1] = sinf(ang);
+            theta *= theta_scale;
+        }
+    }
+}
+
+static int upload_tables(sllm_gfx950_ctx *c, int32_t *trace_dots, sllm_gfx950_act *trace_acts) {
+    const struct sllm_gfx950_model *m = c->m;
+    const uint32_t n_desc = count_descs(m);
+    k_wg_desc *descs = malloc((size_t) n_desc * sizeof *descs);
+    if (descs == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx: descriptor staging");
+    fill_tables(c, descs, trace_dots, trace_acts);
+    hipError_t he = hipMemcpy(c->jobs, c->jobs_host, (size_t) m->n_layer * N_PROJ * sizeof(k_gemv_job),
+                              hipMemcpyHostToDevice);
+    if (he == hipSuccess) {
+        he = hipMemcpy(c->stages, c->stages_host, (size_t) m->n_layer * N_STAGE * sizeof(k_dec_stage),
+                       hipMemcpyHostToDevice);
+    }
+    if (he == hipSuccess) he = hipMemcpy(c->descs, descs, (size_t) n_desc * sizeof *descs, hipMemcpyHostToDevice);
+    free(descs);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx: tables");
+    c->graph_ready = 0;
+    return SLLM_GFX950_OK;
+}
+
+static int drop_graph(sllm_gfx950_ctx *c) {
+    if (c->graph_exec) hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) hipGraphDestroy(c->graph);
+    c->graph_exec = NULL;
+    c->graph = NULL;
+    c->graph_ready = 0;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_ctx **out) {
+    if (!sllm_shim_is_open()) return sllm_shim_fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open");
+    if (m == NULL || out == NULL || n_ctx < 1) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_new: bad arguments");
+    *out = NULL;
+    const int32_t grp = m->n_head / m->n_head_kv;
+    if ((int64_t) grp * n_ctx > SLLM_GFX950_DEC_MAX_GQA_CTX) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_TOO_LARGE, "ctx_new: %d query heads per KV head x n_ctx %d > %d",
+                              grp, n_ctx, SLLM_GFX950_DEC_MAX_GQA_CTX);
+    }
+    sllm_gfx950_ctx *c = calloc(1, sizeof *c);
+    if (c == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_new: host");
+    c->m = m;
+    c->n_ctx = n_ctx;
+    const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
+    const int32_t half = (m->n_rot - m->n_rot % 2) / 2;
+    c->kv_per_layer = (size_t) m->n_head_kv * (size_t) n_ctx * (size_t) m->hd;
+    const uint32_t n_desc = count_descs(m);
+    const size_t sizes[] = {
+        c->kv_per_layer * (size_t) m->n_layer * 4,          /* k cache */
+        c->kv_per_layer * (size_t) m->n_layer * 4,          /* v cache */
+        (size_t) n_ctx * (size_t) (half > 0 ? half : 1) * 8, /* rope */
+        (size_t) m->n_head * (size_t) n_ctx * 4,            /* scores */
+        (size_t) m->n_vocab * 4,                            /* logits */
+        e * 4, e * 4, (e + 2 * g) * 4, e * 4, e * 4, f * 4, e * 4,   /* x ffn_inp qkv attn o h down */
+        sizeof(k_dec_step),
+        (size_t) n_ctx * 4, (size_t) n_ctx * 4,             /* feed, gen */
+        (size_t) m->n_layer * N_STAGE * sizeof(k_dec_stage),
+        (size_t) m->n_layer * N_PROJ * sizeof(k_gemv_job),
+        (size_t) n_desc * sizeof(k_wg_desc),
+    };
+    enum { N_BUF = sizeof sizes / sizeof sizes[0] };
+    size_t total = 0;
+    for (int i = 0; i < N_BUF; ++i) total += align256(sizes[i]);
+    c->jobs_host = calloc((size_t) m->n_layer * N_PROJ, sizeof *c->jobs_host);
+    c->stages_host = calloc((size_t) m->n_layer * N_STAGE, sizeof *c->stages_host);
+    c->launch = calloc((size_t) m->n_layer * N_STAGE, sizeof *c->launch);
+    c->attn_args = calloc((size_t) m->n_layer, sizeof *c->attn_args);
+    float *rope_host = malloc(sizes[2]);
+    int st = SLLM_GFX950_OK;
+    if (!c->jobs_host || !c->stages_host || !c->launch || !c->attn_args || !rope_host) {
+        st = sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_new: host");
+    }
+    hipError_t he = hipSuccess;
+    if (st == SLLM_GFX950_OK) {
+        he = hipMalloc(&c->dev, total);
+        if (he == hipSuccess) he = hipMemset(c->dev, 0, total);
+        if (he != hipSuccess) st = sllm_shim_hip_fail(he, "ctx_new: device memory");
+    }
+    if (st == SLLM_GFX950_OK) {
+        void *p[N_BUF];
+        uint8_t *at = c->dev;
+        for (int i = 0; i < N_BUF; ++i) { p[i] = at; at += align256(sizes[i]); }
+        c->k_cache = p[0]; c->v_cache = p[1]; c->rope = p[2]; c->scores = p[3]; c->logits = p[4];
+        c->x = p[5]; c->ffn_inp = p[6]; c->qkv = p[7]; c->attn = p[8]; c->o = p[9]; c->h = p[10];
+        c->down = p[11]; c->step = p[12]; c->feed = p[13]; c->gen = p[14]; c->stages = p[15];
+        c->jobs = p[16]; c->descs = p[17];
+        rope_table(m, n_ctx, rope_host);
+        he = hipMemcpy(c->rope, rope_host, sizes[2], hipMemcpyHostToDevice);
+        if (he != hipSuccess) st = sllm_shim_hip_fail(he, "ctx_new: rope table");
+    }
+    free(rope_host);
+    if (st == SLLM_GFX950_OK) st = upload_tables(c, NULL, NULL);
+    if (st == SLLM_GFX950_OK) {
+        const float attn_scale = 1.0f / sqrtf((float) m->hd);      /* src/forward.c:616 */
+        for (int32_t il = 0; il < m->n_layer; ++il) {
+            c->attn_args[il] = (k_dec_attn) {
+                c->qkv, c->qkv + e, c->qkv + e + g,
+                c->k_cache + (size_t) il * c->kv_per_layer, c->v_cache + (size_t) il * c->kv_per_layer,
+                c->rope, c->scores, c->attn, c->step, attn_scale,
+                (uint32_t) m->n_head, (uint32_t) m->n_head_kv, (uint32_t) m->hd, (uint32_t) half,
+                (uint32_t) n_ctx, 0 };
+        }
+        c->lm_args = (k_dec_lm) { c->down, c->ffn_inp, m->output_norm, m->tok_embd, c->logits, c->step, m->eps,
+                                  (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };
+        if ((st = sllm_shim_decode_function("sllm_k_dec_gemv", &c->f_gemv)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_dec_scores", &c->f_scores)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_dec_pv", &c->f_pv)) == SLLM_GFX950_OK) {
+            st = sllm_shim_decode_function("sllm_k_dec_lm_head", &c->f_lm);
+        }
+    }
+    if (st != SLLM_GFX950_OK) {
+        sllm_gfx950_ctx_free(c);
+        return st;
+    }
+    *out = c;
+    return SLLM_GFX950_OK;
+}
+
+void sllm_gfx950_ctx_free(sllm_gfx950_ctx *c) {
+    if (c == NULL) return;
+    if (sllm_shim_is_open()) {
+        hipStreamSynchronize(sllm_shim_stream());
+        drop_graph(c);
+        if (c->dev) hipFree(c->dev);
+    }
+    free(c->jobs_host);
+    free(c->stages_host);
+    free(c->launch);
+    free(c->attn_args);
+    free(c);
+}
+
+int32_t sllm_gfx950_ctx_n_past(const sllm_gfx950_ctx *c) { return c ? c->n_past : 0; }
+
+const float *sllm_gfx950_ctx_logits(const sllm_gfx950_ctx *c) { return c ? c->logits : NULL; }
+
+int sllm_gfx950_ctx_reset(sllm_gfx950_ctx *c) {
+    if (c == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_reset: NULL");
+    const hipStream_t s = sllm_shim_stream();
+    hipError_t he = hipSuccess;
+    if (c->n_past > 0) {
+        /* the live prefix of every (layer, KV head): n_past rows each */
+        const size_t hd = (size_t) c->m->hd, rows = (size_t) c->m->n_layer * (size_t) c->m->n_head_kv;
+        he = hipMemset2DAsync(c->k_cache, (size_t) c->n_ctx * hd * 4, 0, (size_t) c->n_past * hd * 4, rows, s);
+        if (he == hipSuccess) {
+            he = hipMemset2DAsync(c->v_cache, (size_t) c->n_ctx * hd * 4, 0, (size_t) c->n_past * hd * 4, rows, s);
+        }
+    }
+    if (he == hipSuccess) he = hipMemsetAsync(c->step, 0, sizeof(k_dec_step), s);
+    if (he == hipSuccess) he = hipStreamSynchronize(s);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_reset");
+    c->n_past = 0;
+    return SLLM_GFX950_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* one token                                                           */
+/* ------------------------------------------------------------------ */
+
+static int launch_token(sllm_gfx950_ctx *c) {
+    const struct sllm_gfx950_model *m = c->m;
+    int st = SLLM_GFX950_OK;
+    const uint32_t kv_chunks = (uint32_t) ((c->n_ctx + ATT_POS - 1) / ATT_POS);
+    const uint32_t slices = (uint32_t) (m->hd / PV_SLICE);
+    for (int32_t il = 0; il < m->n_layer && st == SLLM_GFX950_OK; ++il) {
+        for (int s = 0; s < N_STAGE && st == SLLM_GFX950_OK; ++s) {
+            const stage_launch *sl = &c->launch[(size_t) il * N_STAGE + s];
+            const k_dec_stage *stage = c->stages + (size_t) il * N_STAGE + s;
+            const k_gemv_job *jobs = c->jobs;
+            const k_wg_desc *descs = c->descs + sl->desc_off;
+            uint32_t n_wg = sl->n_wg;
+            void *args[] = { (void *) &stage, (void *) &jobs, (void *) &descs, &n_wg };
+            st = sllm_shim_launch(c->f_gemv, n_wg, 1, SLLM_SLAB_THREADS, 0, args);
+            if (s == S_QKV && st == SLLM_GFX950_OK) {
+                void *aargs[] = { &c->attn_args[il] };
+                st = sllm_shim_launch(c->f_scores, (uint32_t) m->n_head_kv, kv_chunks, ATT_THREADS, 0, aargs);
+                if (st == SLLM_GFX950_OK) {
+                    st = sllm_shim_launch(c->f_pv, (uint32_t) m->n_head_kv, slices, ATT_THREADS, 0, aargs);
+                }
+            }
+        }
+    }
+    if (st == SLLM_GFX950_OK) {
+        void *largs[] = { &c->lm_args };
+        st = sllm_shim_launch(c->f_lm, (uint32_t) ((m->n_vocab + LM_ROWS - 1) / LM_ROWS), 1, LM_THREADS, 0, largs);
+    }
+    return st;
+}
+
+static int enqueue_token(sllm_gfx950_ctx *c) {
+    if (!c->graph_on) return launch_token(c);
+    const hipStream_t s = sllm_shim_stream();
+    if (!c->graph_ready) {
+        drop_graph(c);
+        hipError_t he = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (he != hipSuccess) return sllm_shim_hip_fail(he, "graph: begin capture");
+        const int st = launch_token(c);
+        hipGraph_t graph = NULL;
+        he = hipStreamEndCapture(s, &graph);
+        if (st != SLLM_GFX950_OK) { if (graph) hipGraphDestroy(graph); return st; }
+        if (he != hipSuccess) return sllm_shim_hip_fail(he, "graph: end capture");
+        c->graph = graph;
+        he = hipGraphInstantiate(&c->graph_exec, graph, NULL, NULL, 0);
+        if (he != hipSuccess) { drop_graph(c); return sllm_shim_hip_fail(he, "graph: instantiate"); }
+        c->graph_ready = 1;
+    }
+    hipError_t he = hipGraphLaunch(c->graph_exec, s);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "graph: launch");
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_ctx_set_graph(sllm_gfx950_ctx *c, int on) {
+    if (c == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_set_graph: NULL");
+    c->graph_on = on != 0;
+    if (!c->graph_on) {
+        hipStreamSynchronize(sllm_shim_stream());
+        drop_graph(c);
+    }
+    return SLLM_GFX950_OK;
+}
+
+/* write the step record: token at pos, then the given feed / gen state */
+static int set_step(sllm_gfx950_ctx *c, const k_dec_step *hs) {
+    hipError_t he = hipMemcpyAsync(c->step, hs, sizeof *hs, hipMemcpyHostToDevice, sllm_shim_stream());
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "step record");
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_forward(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, int32_t token, int32_t pos,
+                        float *logits) {
+    if (m == NULL || c == NULL || c->m != m) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward: model / context");
+    if (pos < c->n_past || pos >= c->n_ctx) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward: pos %d outside [n_past %d, n_ctx %d)", pos, c->n_past, c->n_ctx);
+    }
+    if (token < 0 || token >= m->n_vocab) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward: token %d out of range", token);
+    k_dec_step hs;
+    memset(&hs, 0, sizeof hs);
+    hs.token = token;
+    hs.pos = pos;
+    int st = set_step(c, &hs);
+    if (st == SLLM_GFX950_OK) st = enqueue_token(c);
+    if (st != SLLM_GFX950_OK) return st;
+    c->n_past = pos + 1;
+    if (logits != NULL) {
+        const hipStream_t s = sllm_shim_stream();
+        hipError_t he = hipMemcpyAsync(logits, c->logits, (size_t) m->n_vocab * 4, hipMemcpyDeviceToHost, s);
+        if (he == hipSuccess) he = hipStreamSynchronize(s);
+        if (he != hipSuccess) return sllm_shim_hip_fail(he, "forward: logits");
+    }
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_ctx_argmax(sllm_gfx950_ctx *c, int32_t *token) {
+    if (c == NULL || token == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_argmax: NULL");
+    k_dec_step hs;
+    hipError_t he = hipMemcpyAsync(&hs, c->step, sizeof hs, hipMemcpyDeviceToHost, sllm_shim_stream());
+    if (he == hipSuccess) he = hipStreamSynchronize(sllm_shim_stream());
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_argmax");
+    *token = hs.next;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *prompt,
+                                int32_t n_prompt, int32_t n_new, int32_t *out) {
+    if (m == NULL || c == NULL || c->m != m || out == NULL || n_prompt < 0 || n_new < 0 ||
+        (n_prompt > 0 && prompt == NULL)) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "generate_greedy: bad arguments");
+    }
+    if ((int64_t) n_prompt + n_new + c->n_past > c->n_ctx) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_TOO_LARGE, "generate_greedy: %d + %d + %d positions > n_ctx %d",
+                              n_prompt, n_new, c->n_past, c->n_ctx);
+    }
+    for (int32_t i = 0; i < n_prompt; ++i) {
+        if (prompt[i] < 0 || prompt[i] >= m->n_vocab) {
+            return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "generate_greedy: prompt token %d out of range", prompt[i]);
+        }
+    }
+    const int32_t base = c->n_past;
+    const hipStream_t s = sllm_shim_stream();
+    k_dec_step hs;
+    memset(&hs, 0, sizeof hs);
+    hs.pos = base;
+    hs.advance = 1;
+    int32_t steps;
+    int32_t gen_at = 0;
+    if (n_prompt > 0) {
+        /* the prompt, then n_new tokens; the argmax after the last prompt
+         * token is out[0] (src/forward.c:921-934) */
+        hs.token = prompt[0];
+        hs.feed = c->feed;
+        hs.n_feed = n_prompt;
+        hs.i_feed = 1;
+        hs.gen = c->gen;
+        hs.cap_gen = n_new;
+        steps = n_prompt + n_new;
+        hipError_t he = hipMemcpyAsync(c->feed, prompt, (size_t) n_prompt * 4, hipMemcpyHostToDevice, s);
+        if (he != hipSuccess) return sllm_shim_hip_fail(he, "generate_greedy: prompt");
+    } else {
+        /* no prompt: start from the last logits' argmax, or BOS in a fresh
+         * context (src/forward.c:909-920); out[0] is that token */
+        if (n_new == 0) return SLLM_GFX950_OK;
+        int32_t first = BOS_TOKEN;
+        if (base > 0) {
+            const int st = sllm_gfx950_ctx_argmax(c, &first);
+            if (st != SLLM_GFX950_OK) return st;
+        }
+        if (first < 0 || first >= m->n_vocab) {
+            return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "generate_greedy: first token %d out of range", first);
+        }
+        out[0] = first;
+        hs.token = first;
+        hs.gen = c->gen;
+        hs.cap_gen = n_new - 1;
+        gen_at = 1;
+        steps = n_new;
+    }
+    int st = set_step(c, &hs);
+    for (int32_t i = 0; i < steps && st == SLLM_GFX950_OK; ++i) st = enqueue_token(c);
+    if (st != SLLM_GFX950_OK) return st;
+    c->n_past = base + steps;
+    const int32_t n_copy = n_new - gen_at;
+    hipError_t he = hipSuccess;
+    if (n_copy > 0) he = hipMemcpyAsync(out + gen_at, c->gen, (size_t) n_copy * 4, hipMemcpyDeviceToHost, s);
+    if (he == hipSuccess) he = hipStreamSynchronize(s);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "generate_greedy: tokens");
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos) {
+    if (c == NULL || k == NULL || v == NULL || n_pos < 0 || n_pos > c->n_ctx) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_kv_load: bad arguments");
+    }
+    const size_t hd = (size_t) c->m->hd, rows = (size_t) c->m->n_layer * (size_t) c->m->n_head_kv;
+    const hipStream_t s = sllm_shim_stream();
+    hipError_t he = hipSuccess;
+    if (n_pos > 0) {
+        const size_t w = (size_t) n_pos * hd * 4, dpitch = (size_t) c->n_ctx * hd * 4;
+        he = hipMemcpy2DAsync(c->k_cache, dpitch, k, w, w, rows, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess) he = hipMemcpy2DAsync(c->v_cache, dpitch, v, w, w, rows, hipMemcpyHostToDevice, s);
+    }
+    if (he == hipSuccess) he = hipStreamSynchronize(s);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_kv_load");
+    c->n_past = n_pos;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_ctx_trace(sllm_gfx950_ctx *c, int32_t *dots, sllm_gfx950_act *acts) {
+    if (c == NULL || (dots == NULL) != (acts == NULL)) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_trace: give both buffers or neither");
+    }
+    hipError_t he = hipStreamSynchronize(sllm_shim_stream());
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_trace");
+    drop_graph(c);
+    return upload_tables(c, dots, acts);
+}

@@ -1,8 +1,9 @@
 /*
  * gfx950_shim.c -- the thin C11 shim between the host code and HIP.
  *
- * Loads the gfx950 code object built from i2s_kernels.hip (embedded in this
- * library at build time) with hipModuleLoadData, launches its entry points
+ * Loads the gfx950 code objects built from i2s_kernels.hip and
+ * decode_kernels.hip (embedded in this library at build time) with
+ * hipModuleLoadData, launches its entry points
  * with hipModuleLaunchKernel on one library-owned stream, and owns the device
  * buffers: registered weight tensors, per-call scratch and job tables.
  *
@@ -11,9 +12,7 @@
  */
 #define _POSIX_C_SOURCE 200809L
 
-#include <saphira_amd/sllm_gfx950.h>
-
-#include <hip/hip_runtime_api.h>
+#include "shim_internal.h"
 
 #include <pthread.h>
 #include <stdarg.h>
@@ -43,36 +42,24 @@ __asm__(".section .rodata.sllm_gfx950_code_object,\"a\",@progbits\n"
         ".byte 0\n"
         ".previous\n");
 
+#ifndef SLLM_GFX950_DEC_HSACO
+#error "SLLM_GFX950_DEC_HSACO must name the decode code object to embed"
+#endif
+
+extern const unsigned char sllm_gfx950_decode_object[];
+__asm__(".section .rodata.sllm_gfx950_decode_object,\"a\",@progbits\n"
+        ".balign 4096\n"
+        ".hidden sllm_gfx950_decode_object\n"
+        ".globl sllm_gfx950_decode_object\n"
+        "sllm_gfx950_decode_object:\n"
+        ".incbin \"" SLLM_GFX950_DEC_HSACO "\"\n"
+        ".byte 0\n"
+        ".previous\n");
+
 /* ------------------------------------------------------------------ */
-/* device-side argument layouts (mirrors of i2s_kernels.hip)           */
+/* device-side argument layouts (k_gemv_job, k_wg_desc: shim_internal.h) */
 /* ------------------------------------------------------------------ */
 
-typedef struct k_gemv_job {
-    const uint8_t         *w;
-    const float           *x;
-    int8_t                *q;
-    sllm_gfx950_act       *act;
-    float                 *out_f;
-    int32_t               *out_i;
-    uint32_t               n_rows;
-    uint32_t               k;
-    uint32_t               variant;
-    uint32_t               pad;
-} k_gemv_job;
-
-/* One workgroup's share of a job (mirror of wg_desc): slab a of b slabs for
- * the slab kernel, rows [a, b) for the streaming kernel. */
-typedef struct k_wg_desc {
-    uint32_t job;
-    uint32_t a;
-    uint32_t b;
-    uint32_t flags;
-} k_wg_desc;
-
-enum { WG_PUBLISH = 1 };
-
-_Static_assert(sizeof(k_gemv_job) == 64, "k_gemv_job must match gemv_job in i2s_kernels.hip");
-_Static_assert(sizeof(k_wg_desc) == 16, "k_wg_desc must match wg_desc in i2s_kernels.hip");
 _Static_assert(sizeof(sllm_gfx950_act) == 8, "sllm_gfx950_act must match sllm_i2s_act");
 
 enum { LPR_4 = 0, LPR_8 = 1, LPR_16 = 2, N_LPR = 3 };
@@ -126,7 +113,7 @@ static struct {
     int            cu;
     size_t         hbm;
     char           name[520];
-    hipModule_t    mod;
+    hipModule_t    mod, dec_mod;
     hipFunction_t  k_quant, k_quant_list;
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
@@ -239,7 +226,13 @@ int sllm_gfx950_open(int device) {
         hipModuleUnload(g.mod);
         goto out;
     }
+    if ((e = hipModuleLoadData(&g.dec_mod, sllm_gfx950_decode_object)) != hipSuccess) {
+        hipModuleUnload(g.mod);
+        st = hip_fail(e, "hipModuleLoadData(decode)");
+        goto out;
+    }
     if ((e = hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking)) != hipSuccess) {
+        hipModuleUnload(g.dec_mod);
         hipModuleUnload(g.mod);
         st = hip_fail(e, "hipStreamCreateWithFlags");
         goto out;
@@ -247,6 +240,7 @@ int sllm_gfx950_open(int device) {
     if ((e = hipEventCreate(&g.ev_start)) != hipSuccess ||
         (e = hipEventCreate(&g.ev_stop)) != hipSuccess) {
         hipStreamDestroy(g.stream);
+        hipModuleUnload(g.dec_mod);
         hipModuleUnload(g.mod);
         st = hip_fail(e, "hipEventCreate");
         goto out;
@@ -255,6 +249,7 @@ int sllm_gfx950_open(int device) {
         hipEventDestroy(g.ev_start);
         hipEventDestroy(g.ev_stop);
         hipStreamDestroy(g.stream);
+        hipModuleUnload(g.dec_mod);
         hipModuleUnload(g.mod);
         st = hip_fail(e, "hipMalloc(row scratch)");
         goto out;
@@ -282,6 +277,7 @@ void sllm_gfx950_close(void) {
         hipEventDestroy(g.ev_start);
         hipEventDestroy(g.ev_stop);
         hipStreamDestroy(g.stream);
+        hipModuleUnload(g.dec_mod);
         hipModuleUnload(g.mod);
         memset(&g, 0, sizeof g);
     }
@@ -405,6 +401,33 @@ static int launch(hipFunction_t f, uint32_t grid, uint32_t block, uint32_t lds, 
     return SLLM_GFX950_OK;
 }
 
+/* what decode.c builds on (shim_internal.h) */
+int sllm_shim_is_open(void) { return g.open; }
+hipStream_t sllm_shim_stream(void) { return g.stream; }
+int sllm_shim_cu(void) { return g.cu; }
+
+int sllm_shim_fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int sllm_shim_hip_fail(hipError_t e, const char *what) { return hip_fail(e, what); }
+
+int sllm_shim_decode_function(const char *name, hipFunction_t *f) {
+    if (!g.open) return fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open");
+    HIP_TRY(hipModuleGetFunction(f, g.dec_mod, name));
+    return SLLM_GFX950_OK;
+}
+
+int sllm_shim_launch(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t block, uint32_t lds, void **args) {
+    if (gx == 0 || gy == 0) return SLLM_GFX950_OK;
+    HIP_TRY(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, lds, g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
 static uint32_t stream_grid(uint64_t n16) {
     const uint64_t cap = (uint64_t) (g.cu > 0 ? g.cu : 256) * 8;
     const uint64_t want = (n16 + 255) / 256;
@@ -484,6 +507,9 @@ static int slab_variant_for(size_t k) {
     }
     return -1;
 }
+
+int sllm_shim_slab_variant(uint32_t k) { return slab_variant_for(k); }
+uint32_t sllm_shim_slab_group_rows(int variant) { return variant == 0 ? 4 * 64 / 8 : 4 * 64 / 16; }
 
 /* does a job of this shape take the slab kernel (else the streaming one) */
 static int slab_path(size_t n_rows, size_t k) {

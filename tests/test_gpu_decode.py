@@ -1,0 +1,252 @@
+"""The decode step on the GPU (sllm_gfx950_decode.h) against the oracle.
+
+The oracle's decode step is pinned bit for bit to the reference's own
+sllm_forward (tests/test_oracle_fwd.py), so agreement here is agreement
+with the reference: logits bit for bit, token after token, and -- through
+the trace -- every projection's int32 dots and every activation's scale /
+sum. Shapes: tiny models (every position from 0, scalar softmax tails of
+every length, a rotary width below the head width, four query heads per KV
+head), one block at BitNet-2B widths, a 1024-position KV prefix holding
+binary16 values, and the full 30-block 2B shape.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_rot=64, n_vocab=1000,
+            eps=1e-5, rope_base=500000.0)
+NARROW_ROT = dict(TINY, n_layer=3, n_embd=512, n_ff=1024, n_head=8, n_head_kv=2, n_rot=48, n_vocab=777)
+
+
+def cfg_label(cfg):
+    return f"{cfg['n_layer']}x{cfg['n_embd']}/{cfg['n_ff']} h{cfg['n_head']}/{cfg['n_head_kv']} rot{cfg['n_rot']}"
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _tokens(n, vocab, seed):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, vocab, n)]
+
+
+def _plant_subnormals(model, tokens):
+    cfg = model["cfg"]
+    emb = np.asarray(model["tok_embd"]).reshape(cfg["n_vocab"], cfg["n_embd"])
+    for i, t in enumerate(tokens[::3]):
+        emb[t, (7 * i) % cfg["n_embd"]] = (0x0001, 0x03FF, 0x8200, 0x0155)[i % 4]
+
+
+def _compare_step(g, o, tok, pos, label):
+    want, wdots, wacts = o.forward(tok, pos, trace=True)
+    got = g.forward(tok, pos)
+    gdots, gacts = g.trace_read()
+    assert np.array_equal(gdots, wdots), f"{label}: int32 dots differ at pos {pos}"
+    assert np.array_equal(gacts["sum"], wacts["sum"]), f"{label}: act sums differ at pos {pos}"
+    assert np.array_equal(bits(gacts["scale"]), bits(wacts["scale"])), f"{label}: act scales differ at pos {pos}"
+    assert np.array_equal(bits(got), bits(want)), f"{label}: logits differ at pos {pos}"
+
+
+@pytest.mark.parametrize("cfg", [TINY, NARROW_ROT], ids=["tiny", "narrow-rot"])
+def test_decode_matches_the_oracle_token_by_token(amd, orc, dev, cfg):
+    model = amd.synth_model(cfg, 3)
+    tokens = _tokens(20, cfg["n_vocab"], 5)
+    _plant_subnormals(model, tokens)
+    print(f"[decode] {cfg['n_layer']} blocks, {len(tokens)} tokens", flush=True)
+    g, o = amd.DeviceDecoder(dev, model, 40), orc.Decoder(model, 40)
+    g.trace_start()
+    try:
+        for pos, tok in enumerate(tokens):
+            _compare_step(g, o, tok, pos, cfg_label(cfg))
+    finally:
+        g.trace_stop()
+        g.close()
+        o.close()
+
+
+def test_argmax_follows_the_first_maximum(amd, orc, dev):
+    cfg = dict(TINY, n_layer=1)
+    model = amd.synth_model(cfg, 8)
+    g, o = amd.DeviceDecoder(dev, model, 16), orc.Decoder(model, 16)
+    try:
+        for pos, tok in enumerate(_tokens(6, cfg["n_vocab"], 9)):
+            want = o.forward(tok, pos)
+            g.forward(tok, pos, logits=False)
+            assert g.argmax() == orc.orc().orc_argmax(orc._p(want), cfg["n_vocab"])
+    finally:
+        g.close()
+        o.close()
+
+
+def test_one_block_at_bitnet_2b_widths(amd, orc, dev):
+    cfg = dict(amd.BITNET_2B, n_layer=1, n_vocab=512)
+    model = amd.synth_model(cfg, 4)
+    print("[decode] one 2B block", flush=True)
+    g, o = amd.DeviceDecoder(dev, model, 16), orc.Decoder(model, 16)
+    g.trace_start()
+    try:
+        for pos, tok in enumerate(_tokens(10, cfg["n_vocab"], 6)):
+            _compare_step(g, o, tok, pos, "2b-block")
+    finally:
+        g.trace_stop()
+        g.close()
+        o.close()
+
+
+def _kv_prefix(cfg, n_pos, seed):
+    """f32 caches [layer][head_kv][pos][head_dim] of binary16 N(0,1) values."""
+    hd = cfg["n_embd"] // cfg["n_head"]
+    shape = (cfg["n_layer"], cfg["n_head_kv"], n_pos, hd)
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal(shape).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal(shape).astype(np.float16).astype(np.float32)
+    return k, v
+
+
+@pytest.mark.parametrize("widths", ["tiny", "2b"])
+def test_decode_after_a_1024_position_prefix(amd, orc, dev, widths):
+    """Positions 1024.. over a restored cache: every softmax spans five V
+    chunks and seventeen score workgroups per KV head."""
+    cfg = dict(TINY) if widths == "tiny" else dict(amd.BITNET_2B, n_layer=2, n_vocab=512)
+    model = amd.synth_model(cfg, 12)
+    n_pos, n_ctx = 1024, 1032
+    k, v = _kv_prefix(cfg, n_pos, 13)
+    g, o = amd.DeviceDecoder(dev, model, n_ctx), orc.Decoder(model, n_ctx)
+    ok, ov = o.caches()
+    ok[:, :, :n_pos] = k
+    ov[:, :, :n_pos] = v
+    g.kv_load(k, v, n_pos)
+    assert g.n_past() == n_pos
+    g.trace_start()
+    print(f"[decode] {widths}: prefix {n_pos}", flush=True)
+    try:
+        for i, tok in enumerate(_tokens(5, cfg["n_vocab"], 14)):
+            _compare_step(g, o, tok, n_pos + i, f"prefix-{widths}")
+    finally:
+        g.trace_stop()
+        g.close()
+        o.close()
+
+
+def _oracle_greedy(o, prompt, n_new, n_vocab):
+    from oracle import oracle as orcmod
+    pos = 0
+    logits = None
+    for t in prompt:
+        logits = o.forward(t, pos)
+        pos += 1
+    out = []
+    nxt = orcmod.orc().orc_argmax(orcmod._p(logits), n_vocab)
+    for _ in range(n_new):
+        out.append(nxt)
+        logits = o.forward(nxt, pos)
+        pos += 1
+        nxt = orcmod.orc().orc_argmax(orcmod._p(logits), n_vocab)
+    return out, logits
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["launches", "graph"])
+def test_greedy_generation_runs_on_the_device(amd, orc, dev, graph):
+    """The token loop with no host round trip per token: the output kernel
+    feeds each argmax back. Same ids as the oracle's loop, and the last
+    logits are the oracle's last logits."""
+    cfg = dict(NARROW_ROT, n_layer=2)
+    model = amd.synth_model(cfg, 21)
+    prompt = _tokens(5, cfg["n_vocab"], 22)
+    g, o = amd.DeviceDecoder(dev, model, 64), orc.Decoder(model, 64)
+    g.set_graph(graph)
+    try:
+        got = g.generate(prompt, 12)
+        want, last = _oracle_greedy(o, prompt, 12, cfg["n_vocab"])
+        assert list(got) == want
+        assert g.n_past() == len(prompt) + 12
+        dl = amd.lib().sllm_gfx950_ctx_logits(g.c)
+        dev.sync()
+        glast = np.empty(cfg["n_vocab"], np.float32)
+        amd.check(amd.lib().sllm_gfx950_d2h(amd.ptr(glast), dl, glast.nbytes))
+        assert np.array_equal(bits(glast), bits(last))
+        # no prompt: continue from the last logits (src/forward.c:910-919)
+        more = g.generate([], 4)
+        want2 = []
+        nxt = orc.orc().orc_argmax(orc._p(last), cfg["n_vocab"])
+        pos = len(prompt) + 12
+        for _ in range(4):
+            want2.append(nxt)
+            lg = o.forward(nxt, pos)
+            pos += 1
+            nxt = orc.orc().orc_argmax(orc._p(lg), cfg["n_vocab"])
+        assert list(more) == want2
+    finally:
+        g.close()
+        o.close()
+
+
+def test_graph_replays_match_launches(amd, dev):
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 31)
+    toks = _tokens(12, cfg["n_vocab"], 32)
+    a, b = amd.DeviceDecoder(dev, model, 16), amd.DeviceDecoder(dev, model, 16)
+    b.set_graph(True)
+    try:
+        for pos, t in enumerate(toks):
+            x = a.forward(t, pos)
+            y = b.forward(t, pos)
+            assert np.array_equal(bits(x), bits(y)), pos
+    finally:
+        a.close()
+        b.close()
+
+
+def test_forward_refuses_what_the_reference_refuses(amd, dev):
+    cfg = dict(TINY, n_layer=1)
+    model = amd.synth_model(cfg, 41)
+    g = amd.DeviceDecoder(dev, model, 8)
+    try:
+        assert g.status_forward(cfg["n_vocab"], 0) == -1          # token out of range
+        assert g.status_forward(-1, 0) == -1
+        assert g.status_forward(1, 8) == -1                       # past n_ctx
+        g.forward(1, 0, logits=False)
+        g.forward(2, 3, logits=False)                             # a gap is allowed
+        assert g.status_forward(3, 2) == -1                       # rewinding is not
+        out = np.zeros(8, np.int32)
+        st = amd.lib().sllm_gfx950_generate_greedy(g.m, g.c, None, 0, 8, amd.ptr(out))
+        assert st == -36                                          # past n_ctx
+        g.reset()
+        assert g.n_past() == 0
+        g.forward(5, 0, logits=False)
+    finally:
+        g.close()
+
+
+def test_reset_gives_a_fresh_context(amd, orc, dev):
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 51)
+    toks = _tokens(6, cfg["n_vocab"], 52)
+    g = amd.DeviceDecoder(dev, model, 16)
+    try:
+        first = [g.forward(t, p) for p, t in enumerate(toks)]
+        g.reset()
+        again = [g.forward(t, p) for p, t in enumerate(toks)]
+        for a, b in zip(first, again):
+            assert np.array_equal(bits(a), bits(b))
+    finally:
+        g.close()
+
+
+def test_full_2b_decode_is_bit_exact(amd, orc, dev):
+    """All 30 blocks at BitNet-2B shape with the 128256-row F16 output: every
+    int32 accumulator, every activation and the logits of three tokens."""
+    cfg = dict(amd.BITNET_2B)
+    print("[decode] building the 2B model", flush=True)
+    model = amd.synth_model(cfg, 1)
+    g, o = amd.DeviceDecoder(dev, model, 8), orc.Decoder(model, 8)
+    g.trace_start()
+    try:
+        for pos, tok in enumerate(_tokens(3, cfg["n_vocab"], 2)):
+            print(f"[decode] 2B token {pos}", flush=True)
+            _compare_step(g, o, tok, pos, "2b")
+    finally:
+        g.trace_stop()
+        g.close()
+        o.close()
