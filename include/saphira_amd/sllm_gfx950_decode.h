@@ -52,7 +52,7 @@ typedef struct sllm_gfx950_ctx   sllm_gfx950_ctx;
  * head, n_embd / n_ff (the slab GEMV's LDS row), and query heads per KV head
  * times n_ctx (the softmax rows held in LDS). */
 #define SLLM_GFX950_DEC_MAX_HEAD_DIM 128
-#define SLLM_GFX950_DEC_MAX_GQA      8
+#define SLLM_GFX950_DEC_MAX_GQA      4
 #define SLLM_GFX950_DEC_MAX_WIDTH    7168
 #define SLLM_GFX950_DEC_MAX_GQA_CTX  16384
 

@@ -25,8 +25,8 @@
 
 typedef struct k_dec_step {
     int32_t        token, pos, next, advance;
-    uint64_t       key;
-    uint32_t       ticket, err;
+    uint64_t       reserved0;
+    uint32_t       reserved1, err;
     const int32_t *feed;
     int32_t       *gen;
     int32_t        n_feed, i_feed, n_gen, cap_gen;
@@ -52,7 +52,7 @@ typedef struct k_dec_attn {
     float            *out;
     const k_dec_step *step;
     float             attn_scale;
-    uint32_t          n_head, n_kv, hd, half, n_ctx, pad;
+    uint32_t          n_head, n_kv, hd, half, n_ctx, sc_stride;
 } k_dec_attn;
 
 typedef struct k_dec_lm {
@@ -60,12 +60,23 @@ typedef struct k_dec_lm {
     const float    *norm_w;
     const uint16_t *embd;
     float          *logits;
-    k_dec_step     *step;
+    uint64_t       *partial;
     float           eps;
     uint32_t        n_embd, n_vocab, pad;
 } k_dec_lm;
 
+/* one GEMV stage's kernel arguments (dec_gemv_args) */
+typedef struct k_dec_gemv_args {
+    k_dec_stage st;
+    k_gemv_job  job[3];
+    uint32_t    n_slabs[3];
+    uint32_t    n_wg;
+    uint32_t    pair;
+    uint32_t    pad[3];
+} k_dec_gemv_args;
+
 _Static_assert(sizeof(k_dec_step) == 64, "k_dec_step must match dec_step");
+_Static_assert(sizeof(k_dec_gemv_args) == 296, "k_dec_gemv_args must match dec_gemv_args");
 _Static_assert(sizeof(k_dec_stage) == 72, "k_dec_stage must match dec_stage");
 _Static_assert(sizeof(k_dec_attn) == 104, "k_dec_attn must match dec_attn");
 _Static_assert(sizeof(k_dec_lm) == 64, "k_dec_lm must match dec_lm");
@@ -79,6 +90,7 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2 };
 #define LM_THREADS  256
 #define LM_ROWS     64
 #define LM_MAX_E    8192
+#define LM_WG_PER_CU 4    /* output workgroups per CU (LDS: 32 KiB each) */
 
 /* projections of a block, in the reference's order (src/forward.c:642-793) */
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, N_PROJ };
@@ -235,11 +247,6 @@ size_t sllm_gfx950_trace_dots(const sllm_gfx950_model *m) {
 /* context                                                             */
 /* ------------------------------------------------------------------ */
 
-typedef struct stage_launch {
-    uint32_t desc_off;     /* first descriptor of the stage */
-    uint32_t n_wg;         /* its workgroups (a multiple of 8) */
-} stage_launch;
-
 struct sllm_gfx950_ctx {
     const struct sllm_gfx950_model *m;
     int32_t       n_ctx, n_past;
@@ -248,16 +255,13 @@ struct sllm_gfx950_ctx {
     float        *x, *ffn_inp, *qkv, *attn, *o, *h, *down;
     k_dec_step   *step;
     int32_t      *feed, *gen;
-    k_dec_stage  *stages;          /* device, n_layer * N_STAGE */
-    k_gemv_job   *jobs;            /* device, n_layer * N_PROJ */
-    k_wg_desc    *descs;           /* device */
-    k_gemv_job   *jobs_host;       /* host copy, for tracing */
-    k_dec_stage  *stages_host;
-    stage_launch *launch;          /* n_layer * N_STAGE */
+    uint64_t     *lm_partial;      /* one argmax key per output workgroup */
+    uint32_t      lm_wg;
+    k_dec_gemv_args *gargs;        /* n_layer * N_STAGE kernel argument blocks */
     k_dec_attn   *attn_args;       /* n_layer */
     k_dec_lm      lm_args;
     size_t        kv_per_layer;    /* floats */
-    hipFunction_t f_gemv, f_scores, f_pv, f_lm;
+    hipFunction_t f_gemv, f_scores, f_pv, f_lm, f_argmax;
     int           graph_on, graph_ready;
     hipGraph_t    graph;
     hipGraphExec_t graph_exec;
@@ -275,76 +279,52 @@ static uint32_t proj_slabs(const struct sllm_gfx950_model *m, int p, int *varian
 
 static uint32_t pad8(uint32_t v) { return (v + 7u) & ~7u; }
 
-/* the stage each projection belongs to, and whether it leads a gate/up pair */
-static const int proj_stage[N_PROJ] = { S_QKV, S_QKV, S_QKV, S_O, S_FFN, S_FFN, S_DOWN };
-
-static void fill_tables(sllm_gfx950_ctx *c, k_wg_desc *descs, int32_t *trace_dots, sllm_gfx950_act *trace_acts) {
+static void fill_args(sllm_gfx950_ctx *c, int32_t *trace_dots, sllm_gfx950_act *trace_acts) {
     const struct sllm_gfx950_model *m = c->m;
     const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
-    uint32_t nd = 0;
     int32_t *tr = trace_dots;
     for (int32_t il = 0; il < m->n_layer; ++il) {
         const dev_layer *L = &m->layers[il];
-        k_gemv_job *J = c->jobs_host + (size_t) il * N_PROJ;
+        k_gemv_job J[N_PROJ];
+        uint32_t slabs[N_PROJ];
         float *out_f[N_PROJ] = { c->qkv, c->qkv + e, c->qkv + e + g, c->o, c->h, NULL, c->down };
         for (int p = 0; p < N_PROJ; ++p) {
             size_t rows, k;
             proj_shape(m, p, &rows, &k);
             int variant;
-            (void) proj_slabs(m, p, &variant);
+            slabs[p] = proj_slabs(m, p, &variant);
             J[p] = (k_gemv_job) { L->w[p], NULL, NULL, NULL, out_f[p], tr, (uint32_t) rows, (uint32_t) k,
                                   (uint32_t) variant, 0 };
             if (tr != NULL) tr += rows;
         }
-        k_dec_stage *S = c->stages_host + (size_t) il * N_STAGE;
-        const k_dec_stage *dev_st = c->stages + (size_t) il * N_STAGE;
-        (void) dev_st;
         sllm_gfx950_act *ta = trace_acts != NULL ? trace_acts + (size_t) il * 4 : NULL;
-        S[S_QKV] = (k_dec_stage) {
+        k_dec_gemv_args *A = c->gargs + (size_t) il * N_STAGE;
+        memset(A, 0, N_STAGE * sizeof *A);
+        A[S_QKV].st = (k_dec_stage) {
             il == 0 ? (const void *) m->tok_embd : (const void *) c->down, il == 0 ? NULL : c->ffn_inp,
             c->x, L->attn_norm, c->step, NULL, ta ? ta + 0 : NULL, m->eps, (uint32_t) e,
             il == 0 ? IN_EMBED : IN_RESID, 0 };
-        S[S_O] = (k_dec_stage) { c->attn, NULL, NULL, L->attn_sub_norm, c->step, NULL, ta ? ta + 1 : NULL,
-                                 m->eps, (uint32_t) e, IN_PLAIN, 0 };
-        S[S_FFN] = (k_dec_stage) { c->o, c->x, c->ffn_inp, L->ffn_norm, c->step, NULL, ta ? ta + 2 : NULL,
-                                   m->eps, (uint32_t) e, IN_RESID, 0 };
-        S[S_DOWN] = (k_dec_stage) { c->h, NULL, NULL, L->ffn_sub_norm, c->step, NULL, ta ? ta + 3 : NULL,
-                                    m->eps, (uint32_t) f, IN_PLAIN, 0 };
-        /* descriptors: per stage, every projection's slabs; gate and up share
-         * theirs (WG_PAIR on gate, none for up); the stage's first workgroup
-         * publishes */
-        for (int s = 0; s < N_STAGE; ++s) {
-            stage_launch *sl = &c->launch[(size_t) il * N_STAGE + s];
-            sl->desc_off = nd;
-            uint32_t first = nd;
-            for (int p = 0; p < N_PROJ; ++p) {
-                if (proj_stage[p] != s || p == P_UP) continue;
-                int variant;
-                const uint32_t n = proj_slabs(m, p, &variant);
-                for (uint32_t w = 0; w < n; ++w) {
-                    uint32_t flags = (p == P_GATE) ? WG_PAIR : 0u;
-                    if (nd == first) flags |= WG_PUBLISH;
-                    descs[nd++] = (k_wg_desc) { (uint32_t) (il * N_PROJ + p), w, n, flags };
-                }
-            }
-            while ((nd - first) % 8) descs[nd++] = (k_wg_desc) { 0, 0, 0, 0 };
-            sl->n_wg = nd - first;
+        A[S_O].st = (k_dec_stage) { c->attn, NULL, NULL, L->attn_sub_norm, c->step, NULL, ta ? ta + 1 : NULL,
+                                    m->eps, (uint32_t) e, IN_PLAIN, 0 };
+        A[S_FFN].st = (k_dec_stage) { c->o, c->x, c->ffn_inp, L->ffn_norm, c->step, NULL, ta ? ta + 2 : NULL,
+                                      m->eps, (uint32_t) e, IN_RESID, 0 };
+        A[S_DOWN].st = (k_dec_stage) { c->h, NULL, NULL, L->ffn_sub_norm, c->step, NULL, ta ? ta + 3 : NULL,
+                                       m->eps, (uint32_t) f, IN_PLAIN, 0 };
+        /* Q, K, V share the attention input; gate and up are one pair whose
+         * slabs cover both (up has none of its own) */
+        A[S_QKV].job[0] = J[P_Q]; A[S_QKV].job[1] = J[P_K]; A[S_QKV].job[2] = J[P_V];
+        A[S_QKV].n_slabs[0] = slabs[P_Q]; A[S_QKV].n_slabs[1] = slabs[P_K]; A[S_QKV].n_slabs[2] = slabs[P_V];
+        A[S_O].job[0] = J[P_O]; A[S_O].job[1] = J[P_O]; A[S_O].job[2] = J[P_O];
+        A[S_O].n_slabs[0] = slabs[P_O];
+        A[S_FFN].job[0] = J[P_GATE]; A[S_FFN].job[1] = J[P_UP]; A[S_FFN].job[2] = J[P_GATE];
+        A[S_FFN].n_slabs[0] = slabs[P_GATE];
+        A[S_FFN].pair = 1;
+        A[S_DOWN].job[0] = J[P_DOWN]; A[S_DOWN].job[1] = J[P_DOWN]; A[S_DOWN].job[2] = J[P_DOWN];
+        A[S_DOWN].n_slabs[0] = slabs[P_DOWN];
+        for (int st = 0; st < N_STAGE; ++st) {
+            A[st].n_wg = pad8(A[st].n_slabs[0] + A[st].n_slabs[1] + A[st].n_slabs[2]);
         }
     }
-}
-
-static uint32_t count_descs(const struct sllm_gfx950_model *m) {
-    uint32_t per_layer = 0;
-    for (int s = 0; s < N_STAGE; ++s) {
-        uint32_t n = 0;
-        for (int p = 0; p < N_PROJ; ++p) {
-            if (proj_stage[p] != s || p == P_UP) continue;
-            int variant;
-            n += proj_slabs(m, p, &variant);
-        }
-        per_layer += pad8(n);
-    }
-    return per_layer * (uint32_t) m->n_layer;
 }
 
 /* cos / sin of every (position, pair) as the reference computes them per
@@ -368,21 +348,8 @@ static void rope_table(const struct sllm_gfx950_model *m, int32_t n_ctx, float *
     }
 }
 
-static int upload_tables(sllm_gfx950_ctx *c, int32_t *trace_dots, sllm_gfx950_act *trace_acts) {
-    const struct sllm_gfx950_model *m = c->m;
-    const uint32_t n_desc = count_descs(m);
-    k_wg_desc *descs = malloc((size_t) n_desc * sizeof *descs);
-    if (descs == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx: descriptor staging");
-    fill_tables(c, descs, trace_dots, trace_acts);
-    hipError_t he = hipMemcpy(c->jobs, c->jobs_host, (size_t) m->n_layer * N_PROJ * sizeof(k_gemv_job),
-                              hipMemcpyHostToDevice);
-    if (he == hipSuccess) {
-        he = hipMemcpy(c->stages, c->stages_host, (size_t) m->n_layer * N_STAGE * sizeof(k_dec_stage),
-                       hipMemcpyHostToDevice);
-    }
-    if (he == hipSuccess) he = hipMemcpy(c->descs, descs, (size_t) n_desc * sizeof *descs, hipMemcpyHostToDevice);
-    free(descs);
-    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx: tables");
+static int set_args(sllm_gfx950_ctx *c, int32_t *trace_dots, sllm_gfx950_act *trace_acts) {
+    fill_args(c, trace_dots, trace_acts);
     c->graph_ready = 0;
     return SLLM_GFX950_OK;
 }
@@ -412,30 +379,29 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
     const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
     const int32_t half = (m->n_rot - m->n_rot % 2) / 2;
     c->kv_per_layer = (size_t) m->n_head_kv * (size_t) n_ctx * (size_t) m->hd;
-    const uint32_t n_desc = count_descs(m);
+    const uint32_t sc_stride = (uint32_t) ((n_ctx + 7) & ~7);
+    const uint32_t n_pass = (uint32_t) ((m->n_vocab + LM_ROWS - 1) / LM_ROWS);
+    const uint32_t lm_cap = (uint32_t) (sllm_shim_cu() > 0 ? sllm_shim_cu() : 256) * LM_WG_PER_CU;
+    const uint32_t lm_wg = n_pass < lm_cap ? n_pass : lm_cap;
     const size_t sizes[] = {
         c->kv_per_layer * (size_t) m->n_layer * 4,          /* k cache */
         c->kv_per_layer * (size_t) m->n_layer * 4,          /* v cache */
         (size_t) n_ctx * (size_t) (half > 0 ? half : 1) * 8, /* rope */
-        (size_t) m->n_head * (size_t) n_ctx * 4,            /* scores */
+        (size_t) m->n_head * (size_t) sc_stride * 4,        /* scores */
         (size_t) m->n_vocab * 4,                            /* logits */
         e * 4, e * 4, (e + 2 * g) * 4, e * 4, e * 4, f * 4, e * 4,   /* x ffn_inp qkv attn o h down */
         sizeof(k_dec_step),
         (size_t) n_ctx * 4, (size_t) n_ctx * 4,             /* feed, gen */
-        (size_t) m->n_layer * N_STAGE * sizeof(k_dec_stage),
-        (size_t) m->n_layer * N_PROJ * sizeof(k_gemv_job),
-        (size_t) n_desc * sizeof(k_wg_desc),
+        (size_t) lm_wg * 8,                                 /* output argmax keys */
     };
     enum { N_BUF = sizeof sizes / sizeof sizes[0] };
     size_t total = 0;
     for (int i = 0; i < N_BUF; ++i) total += align256(sizes[i]);
-    c->jobs_host = calloc((size_t) m->n_layer * N_PROJ, sizeof *c->jobs_host);
-    c->stages_host = calloc((size_t) m->n_layer * N_STAGE, sizeof *c->stages_host);
-    c->launch = calloc((size_t) m->n_layer * N_STAGE, sizeof *c->launch);
+    c->gargs = calloc((size_t) m->n_layer * N_STAGE, sizeof *c->gargs);
     c->attn_args = calloc((size_t) m->n_layer, sizeof *c->attn_args);
     float *rope_host = malloc(sizes[2]);
     int st = SLLM_GFX950_OK;
-    if (!c->jobs_host || !c->stages_host || !c->launch || !c->attn_args || !rope_host) {
+    if (!c->gargs || !c->attn_args || !rope_host) {
         st = sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_new: host");
     }
     hipError_t he = hipSuccess;
@@ -450,14 +416,14 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
         for (int i = 0; i < N_BUF; ++i) { p[i] = at; at += align256(sizes[i]); }
         c->k_cache = p[0]; c->v_cache = p[1]; c->rope = p[2]; c->scores = p[3]; c->logits = p[4];
         c->x = p[5]; c->ffn_inp = p[6]; c->qkv = p[7]; c->attn = p[8]; c->o = p[9]; c->h = p[10];
-        c->down = p[11]; c->step = p[12]; c->feed = p[13]; c->gen = p[14]; c->stages = p[15];
-        c->jobs = p[16]; c->descs = p[17];
+        c->down = p[11]; c->step = p[12]; c->feed = p[13]; c->gen = p[14]; c->lm_partial = p[15];
+        c->lm_wg = lm_wg;
         rope_table(m, n_ctx, rope_host);
         he = hipMemcpy(c->rope, rope_host, sizes[2], hipMemcpyHostToDevice);
         if (he != hipSuccess) st = sllm_shim_hip_fail(he, "ctx_new: rope table");
     }
     free(rope_host);
-    if (st == SLLM_GFX950_OK) st = upload_tables(c, NULL, NULL);
+    if (st == SLLM_GFX950_OK) st = set_args(c, NULL, NULL);
     if (st == SLLM_GFX950_OK) {
         const float attn_scale = 1.0f / sqrtf((float) m->hd);      /* src/forward.c:616 */
         for (int32_t il = 0; il < m->n_layer; ++il) {
@@ -466,14 +432,15 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
                 c->k_cache + (size_t) il * c->kv_per_layer, c->v_cache + (size_t) il * c->kv_per_layer,
                 c->rope, c->scores, c->attn, c->step, attn_scale,
                 (uint32_t) m->n_head, (uint32_t) m->n_head_kv, (uint32_t) m->hd, (uint32_t) half,
-                (uint32_t) n_ctx, 0 };
+                (uint32_t) n_ctx, sc_stride };
         }
-        c->lm_args = (k_dec_lm) { c->down, c->ffn_inp, m->output_norm, m->tok_embd, c->logits, c->step, m->eps,
-                                  (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };
+        c->lm_args = (k_dec_lm) { c->down, c->ffn_inp, m->output_norm, m->tok_embd, c->logits, c->lm_partial,
+                                  m->eps, (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };
         if ((st = sllm_shim_decode_function("sllm_k_dec_gemv", &c->f_gemv)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_dec_scores", &c->f_scores)) == SLLM_GFX950_OK &&
-            (st = sllm_shim_decode_function("sllm_k_dec_pv", &c->f_pv)) == SLLM_GFX950_OK) {
-            st = sllm_shim_decode_function("sllm_k_dec_lm_head", &c->f_lm);
+            (st = sllm_shim_decode_function("sllm_k_dec_pv", &c->f_pv)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_dec_lm_head", &c->f_lm)) == SLLM_GFX950_OK) {
+            st = sllm_shim_decode_function("sllm_k_dec_argmax", &c->f_argmax);
         }
     }
     if (st != SLLM_GFX950_OK) {
@@ -491,9 +458,7 @@ void sllm_gfx950_ctx_free(sllm_gfx950_ctx *c) {
         drop_graph(c);
         if (c->dev) hipFree(c->dev);
     }
-    free(c->jobs_host);
-    free(c->stages_host);
-    free(c->launch);
+    free(c->gargs);
     free(c->attn_args);
     free(c);
 }
@@ -532,13 +497,9 @@ static int launch_token(sllm_gfx950_ctx *c) {
     const uint32_t slices = (uint32_t) (m->hd / PV_SLICE);
     for (int32_t il = 0; il < m->n_layer && st == SLLM_GFX950_OK; ++il) {
         for (int s = 0; s < N_STAGE && st == SLLM_GFX950_OK; ++s) {
-            const stage_launch *sl = &c->launch[(size_t) il * N_STAGE + s];
-            const k_dec_stage *stage = c->stages + (size_t) il * N_STAGE + s;
-            const k_gemv_job *jobs = c->jobs;
-            const k_wg_desc *descs = c->descs + sl->desc_off;
-            uint32_t n_wg = sl->n_wg;
-            void *args[] = { (void *) &stage, (void *) &jobs, (void *) &descs, &n_wg };
-            st = sllm_shim_launch(c->f_gemv, n_wg, 1, SLLM_SLAB_THREADS, 0, args);
+            k_dec_gemv_args *A = &c->gargs[(size_t) il * N_STAGE + s];
+            void *args[] = { A };
+            st = sllm_shim_launch(c->f_gemv, A->n_wg, 1, SLLM_SLAB_THREADS, 0, args);
             if (s == S_QKV && st == SLLM_GFX950_OK) {
                 void *aargs[] = { &c->attn_args[il] };
                 st = sllm_shim_launch(c->f_scores, (uint32_t) m->n_head_kv, kv_chunks, ATT_THREADS, 0, aargs);
@@ -550,7 +511,15 @@ static int launch_token(sllm_gfx950_ctx *c) {
     }
     if (st == SLLM_GFX950_OK) {
         void *largs[] = { &c->lm_args };
-        st = sllm_shim_launch(c->f_lm, (uint32_t) ((m->n_vocab + LM_ROWS - 1) / LM_ROWS), 1, LM_THREADS, 0, largs);
+        st = sllm_shim_launch(c->f_lm, c->lm_wg, 1, LM_THREADS, 0, largs);
+    }
+    if (st == SLLM_GFX950_OK) {
+        const uint64_t *partial = c->lm_partial;
+        const float *logits = c->logits;
+        k_dec_step *step = c->step;
+        uint32_t n = c->lm_wg;
+        void *aargs[] = { (void *) &partial, &n, (void *) &logits, (void *) &step };
+        st = sllm_shim_launch(c->f_argmax, 1, 1, 256, 0, aargs);
     }
     return st;
 }
@@ -719,5 +688,5 @@ int sllm_gfx950_ctx_trace(sllm_gfx950_ctx *c, int32_t *dots, sllm_gfx950_act *ac
     hipError_t he = hipStreamSynchronize(sllm_shim_stream());
     if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_trace");
     drop_graph(c);
-    return upload_tables(c, dots, acts);
+    return set_args(c, dots, acts);
 }

@@ -14,8 +14,8 @@
 //              sllm_k_dec_gemv   gate, up  (prologue: residual, ffn_norm, quantise;
 //                                           epilogue: silu(gate) * up)
 //              sllm_k_dec_gemv   down      (prologue: ffn_sub_norm, quantise)
-//   then       sllm_k_dec_lm_head          (residual, output_norm, F16 rows,
-//                                           argmax, next token)
+//   then       sllm_k_dec_lm_head          (residual, output_norm, F16 rows)
+//              sllm_k_dec_argmax           (argmax, next token)
 //
 // Floating-point contract: IEEE single and double, correctly rounded division
 // and square root, no contraction (explicit fmaf where the reference calls an
@@ -39,8 +39,8 @@ struct dec_step {
     int32_t        pos;         // its position
     int32_t        next;        // argmax of the last logits
     int32_t        advance;     // nonzero: the step moves on by itself (greedy loop)
-    uint64_t       key;         // running argmax key of the current step (0: none)
-    uint32_t       ticket;      // lm_head workgroups done with the current step
+    uint64_t       reserved0;
+    uint32_t       reserved1;
     uint32_t       err;
     const int32_t *feed;        // prompt tokens still to consume: feed[i_feed .. n_feed)
     int32_t       *gen;         // generated tokens
@@ -169,10 +169,6 @@ struct dec_stage {
 };
 static_assert(sizeof(dec_stage) == 72, "dec_stage must match decode.c");
 
-// The workgroup's slab covers job d.job (gate) and the same rows of job
-// d.job + 1 (up); it writes silu(gate) * up into the gate job's out_f.
-constexpr uint32_t WG_PAIR = 2;
-
 struct dec_shared {
     int8_t  q[SLAB_MAX_K];
     int32_t dots[SLAB_MAX_ROWS];
@@ -191,20 +187,18 @@ __device__ __forceinline__ float stage_elem(const dec_stage &st, int32_t token, 
 }
 
 template <int LPR, int CPL, int XV, int QV, int MODE, bool PAIR>
-__device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job *__restrict__ jobs,
-                                          const wg_desc d, dec_shared &S) {
+__device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job &job0, const gemv_job &job1,
+                                          uint32_t slab, uint32_t n_slabs, uint32_t flags, dec_shared &S) {
     constexpr uint32_t RPW = 64 / LPR;
     constexpr uint32_t G = SLAB_WAVES * RPW;
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) tid >> 6);
-    const gemv_job job0 = jobs[d.job];
-    const gemv_job job1 = PAIR ? jobs[d.job + 1] : job0;
     const uint32_t k = job0.k, chunks = k >> 6, row_bytes = k >> 2;
     const uint32_t n_rows = job0.n_rows, last_row = n_rows - 1;
     const __amdgpu_buffer_rsrc_t rs0 = tensor_rsrc(job0), rs1 = tensor_rsrc(job1);
     const uint32_t n_groups = (n_rows + G - 1) / G;
-    const uint32_t per = (n_groups + d.b - 1) / d.b;
-    const uint32_t first = d.a * per;
+    const uint32_t per = (n_groups + n_slabs - 1) / n_slabs;
+    const uint32_t first = slab * per;
     const uint32_t T = first < n_groups ? min(per, n_groups - first) : 0u;
     if (T == 0) return;                               // uniform
     const uint32_t TT = PAIR ? 2 * T : T;             // groups: job0's, then job1's
@@ -329,7 +323,7 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job *_
     }
 
     // (7) workgroup 0 publishes the residual and the quantised row
-    if (d.flags & WG_PUBLISH) {
+    if (flags & WG_PUBLISH) {
 #pragma unroll
         for (int u = 0; u < XV; ++u) {
             const uint32_t i = 4u * (uint32_t) (tid + u * SLAB_THREADS);
@@ -343,22 +337,36 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job *_
     }
 }
 
+// A decode GEMV stage as kernel arguments: the activation's recipe and up
+// to three jobs sharing it (Q, K, V), or gate and up as one pair. Workgroup
+// b (after the XCD remap) takes slab b of job 0, then job 1's, then job 2's;
+// with a pair, job 1 has no slabs of its own.
+struct dec_gemv_args {
+    dec_stage st;
+    gemv_job  job[3];
+    uint32_t  n_slabs[3];
+    uint32_t  n_wg;            // the grid, a multiple of 8
+    uint32_t  pair;            // jobs 0 and 1 are gate and up
+    uint32_t  pad[3];
+};
+static_assert(sizeof(dec_gemv_args) == 296, "dec_gemv_args must match decode.c");
+
 template <int LPR, int CPL, int XV, int QV>
-__device__ __forceinline__ void dec_variant(const dec_stage &st, const gemv_job *jobs, const wg_desc d,
+__device__ __forceinline__ void dec_variant(const dec_stage &st, const gemv_job &job0, const gemv_job &job1,
+                                            bool pair, uint32_t slab, uint32_t n_slabs, uint32_t flags,
                                             dec_shared &S) {
-    const bool pair = (d.flags & WG_PAIR) != 0;
     switch (st.mode) {
     case IN_EMBED:
-        if (pair) dec_block<LPR, CPL, XV, QV, IN_EMBED, true>(st, jobs, d, S);
-        else dec_block<LPR, CPL, XV, QV, IN_EMBED, false>(st, jobs, d, S);
+        if (pair) dec_block<LPR, CPL, XV, QV, IN_EMBED, true>(st, job0, job1, slab, n_slabs, flags, S);
+        else dec_block<LPR, CPL, XV, QV, IN_EMBED, false>(st, job0, job0, slab, n_slabs, flags, S);
         break;
     case IN_RESID:
-        if (pair) dec_block<LPR, CPL, XV, QV, IN_RESID, true>(st, jobs, d, S);
-        else dec_block<LPR, CPL, XV, QV, IN_RESID, false>(st, jobs, d, S);
+        if (pair) dec_block<LPR, CPL, XV, QV, IN_RESID, true>(st, job0, job1, slab, n_slabs, flags, S);
+        else dec_block<LPR, CPL, XV, QV, IN_RESID, false>(st, job0, job0, slab, n_slabs, flags, S);
         break;
     default:
-        if (pair) dec_block<LPR, CPL, XV, QV, IN_PLAIN, true>(st, jobs, d, S);
-        else dec_block<LPR, CPL, XV, QV, IN_PLAIN, false>(st, jobs, d, S);
+        if (pair) dec_block<LPR, CPL, XV, QV, IN_PLAIN, true>(st, job0, job1, slab, n_slabs, flags, S);
+        else dec_block<LPR, CPL, XV, QV, IN_PLAIN, false>(st, job0, job0, slab, n_slabs, flags, S);
         break;
     }
 }
@@ -372,33 +380,49 @@ struct dec_attn {
     const float    *q, *k, *v;          // projections: q [n_head*hd], k / v [n_kv*hd]
     float          *k_cache, *v_cache;  // this layer's caches [n_kv][n_ctx][hd]
     const float    *rope;               // [n_ctx][half] (cos, sin)
-    float          *scores;             // [n_head][n_ctx]
+    float          *scores;             // [n_head][sc_stride]
     float          *out;                // [n_head*hd]
     const dec_step *step;
     float           attn_scale;
     uint32_t        n_head, n_kv, hd, half, n_ctx;
-    uint32_t        pad;
+    uint32_t        sc_stride;          // scores row stride: n_ctx rounded up to 8
 };
 static_assert(sizeof(dec_attn) == 104, "dec_attn must match decode.c");
 
 constexpr int ATT_THREADS = 256;
 constexpr uint32_t ATT_POS = 64;        // positions per scores workgroup
 constexpr uint32_t ATT_MAX_HD = 128;
-constexpr uint32_t ATT_MAX_GRP = 8;     // query heads per KV head
+constexpr uint32_t ATT_MAX_GRP = 4;     // query heads per KV head
+constexpr uint32_t KT_STRIDE = ATT_MAX_HD + 4;     // LDS key row: 16-byte aligned, rows 4 banks apart
+constexpr int KT_LOADS = ATT_POS * ATT_MAX_HD / 4 / ATT_THREADS;   // float4 per thread
 constexpr uint32_t PV_SLICE = 16;       // head dimensions per p.V workgroup
-constexpr uint32_t PV_CHUNK = 256;      // positions of V staged per pass
-constexpr uint32_t PV_MAX_P = 16384;    // query heads per KV head x positions
+constexpr uint32_t PV_RPOS = 1536;      // positions of p and V staged in LDS per round
+constexpr uint32_t PV_VSTRIDE = PV_RPOS + 4;
+constexpr int PV_VLOADS = (int) (PV_RPOS * PV_SLICE / 4 / ATT_THREADS);   // float4 of V per thread
+static_assert(ATT_MAX_GRP * PV_SLICE <= 64, "one chain wave");
 
-// element d of a head vector after NeoX RoPE (src/ops.c:467-549): pairs
-// (e, e + half) rotate by angle e; dimensions from 2*half on pass through
-__device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t half, const float *cs) {
-    if (d < half) return x[d] * cs[2 * d] - x[d + half] * cs[2 * d + 1];
-    if (d < 2 * half) {
-        const uint32_t e = d - half;
-        return x[e] * cs[2 * e + 1] + x[d] * cs[2 * e];
-    }
-    return x[d];
+// NeoX RoPE (src/ops.c:467-549) of element d of a head vector: pairs
+// (e, e + half) rotate by angle e, x[e] -> x[e] c - x[e+half] s and
+// x[e+half] -> x[e] s + x[e+half] c; dimensions from 2*half on pass through.
+// The operands are loaded first (rope_load, no branches around the loads),
+// the arithmetic applied afterwards (rope_apply).
+struct rope_in {
+    float x, partner, c, s;
+};
+
+__device__ __forceinline__ rope_in rope_load(const float *x, uint32_t d, uint32_t half, const float *cs) {
+    const uint32_t e = d < half ? d : (d < 2 * half ? d - half : 0);
+    const uint32_t partner = d < half ? d + half : (d < 2 * half ? d - half : d);
+    return { x[d], x[partner], cs[2 * e], cs[2 * e + 1] };
 }
+
+__device__ __forceinline__ float rope_apply(const rope_in &r, uint32_t d, uint32_t half) {
+    if (d < half) return r.x * r.c - r.partner * r.s;
+    if (d < 2 * half) return r.partner * r.s + r.x * r.c;
+    return r.x;
+}
+
+constexpr int QR_PER_THREAD = (int) (ATT_MAX_GRP * ATT_MAX_HD / ATT_THREADS);
 
 } // namespace
 
@@ -407,166 +431,292 @@ __device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t ha
 // ---------------------------------------------------------------------------
 
 // One decode GEMV stage. Variant 0 (K <= 2560): 8 lanes per row; variant 1
-// (K <= 7168): 16 lanes per row.
+// (K <= 7168): 16 lanes per row. Everything a workgroup needs arrives in the
+// kernel arguments, so its first loads are the activation and the weights.
 extern "C" __global__ void __launch_bounds__(SLAB_THREADS)
-sllm_k_dec_gemv(const dec_stage *__restrict__ stage, const gemv_job *__restrict__ jobs,
-                const wg_desc *__restrict__ descs, uint32_t n_wg) {
+sllm_k_dec_gemv(dec_gemv_args A) {
     __shared__ dec_shared S;
-    const wg_desc d = descs[xcd_slot(n_wg)];
-    if (d.b == 0) return;
-    const dec_stage st = *stage;
-    if (jobs[d.job].variant == 0) dec_variant<8, 5, 3, 1>(st, jobs, d, S);
-    else dec_variant<16, 7, 7, 2>(st, jobs, d, S);
+    const uint32_t b = xcd_slot(A.n_wg);
+    const uint32_t n0 = A.n_slabs[0], n01 = n0 + A.n_slabs[1], n012 = n01 + A.n_slabs[2];
+    if (b >= n012) return;
+    const uint32_t ji = b < n0 ? 0u : (b < n01 ? 1u : 2u);
+    const uint32_t slab = b - (ji == 0 ? 0u : (ji == 1 ? n0 : n01));
+    const gemv_job job0 = ji == 0 ? A.job[0] : (ji == 1 ? A.job[1] : A.job[2]);
+    const gemv_job job1 = A.job[1];
+    const uint32_t n_slabs = A.n_slabs[ji];
+    const uint32_t flags = b == 0 ? WG_PUBLISH : 0u;
+    const bool pair = A.pair != 0;
+    if (job0.variant == 0) dec_variant<8, 5, 3, 1>(A.st, job0, job1, pair, slab, n_slabs, flags, S);
+    else dec_variant<16, 7, 7, 2>(A.st, job0, job1, pair, slab, n_slabs, flags, S);
 }
 
 // Scores: workgroup (KV head, 64 positions). Every workgroup ropes the query
 // heads of its KV head; the one holding position pos ropes the new key and
 // stores it, with the new value, into the caches (src/forward.c:668-690).
 // Thread (h, r) then takes q_h . k_r over d in order, times 1/sqrt(hd)
-// (src/forward.c:698-705).
+// (src/forward.c:698-705). The chunk's cached keys are loaded first, all at
+// once, and wait in registers while the queries are roped.
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_dec_scores(dec_attn A) {
-    __shared__ float qr[ATT_MAX_GRP][ATT_MAX_HD];
-    __shared__ float kt[ATT_POS][ATT_MAX_HD + 1];
+    __shared__ __attribute__((aligned(16))) float qr[ATT_MAX_GRP][ATT_MAX_HD];
+    __shared__ __attribute__((aligned(16))) float kt[ATT_POS][KT_STRIDE];
     const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tid = threadIdx.x;
     const uint32_t pos = (uint32_t) A.step->pos, npast = pos + 1;
     if (s0 >= npast) return;
-    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, half = A.half;
-    const float *cs = A.rope + (size_t) pos * half * 2;
-    for (uint32_t idx = tid; idx < grp * hd; idx += ATT_THREADS) {
-        const uint32_t hh = idx / hd, d = idx % hd;
-        qr[hh][d] = rope_at(A.q + (size_t) (kvh * grp + hh) * hd, d, half, cs);
-    }
-    const uint32_t n_here = min(ATT_POS, npast - s0);
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, half = A.half, hd4 = hd / 4;
     float *kc = A.k_cache + (size_t) kvh * A.n_ctx * hd;
     float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd;
-    for (uint32_t idx = tid; idx < n_here * hd; idx += ATT_THREADS) {
-        const uint32_t r = idx / hd, d = idx % hd, s = s0 + r;
-        float val;
-        if (s < pos) {
-            val = kc[(size_t) s * hd + d];
-        } else {
-            val = rope_at(A.k + (size_t) kvh * hd, d, half, cs);
-            kc[(size_t) pos * hd + d] = val;
-            vc[(size_t) pos * hd + d] = A.v[(size_t) kvh * hd + d];
-        }
-        kt[r][d] = val;
+    const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
+
+    // (1) every global load first: the chunk's cached keys (rows past pos - 1
+    // re-read a valid row), this thread's query elements and the new key's
+    const uint32_t n_f4 = ATT_POS * hd4, last_cached = pos > 0 ? pos - 1 : 0;
+    f32x4 kv[KT_LOADS];
+#pragma unroll
+    for (int u = 0; u < KT_LOADS; ++u) {
+        const uint32_t f = min(tid + (uint32_t) u * ATT_THREADS, n_f4 - 1);
+        const uint32_t r = f / hd4, c4 = f % hd4;
+        kv[u] = *G_CAST(const f32x4, kc + (size_t) min(s0 + r, last_cached) * hd + 4 * c4);
+    }
+    rope_in qi[QR_PER_THREAD];
+#pragma unroll
+    for (int u = 0; u < QR_PER_THREAD; ++u) {
+        const uint32_t idx = min(tid + (uint32_t) u * ATT_THREADS, grp * hd - 1);
+        qi[u] = rope_load(A.q + (size_t) (kvh * grp + idx / hd) * hd, idx % hd, half, cs);
+    }
+    const rope_in ki = rope_load(A.k + (size_t) kvh * hd, min(tid, hd - 1), half, cs);
+    const float vnew = A.v[(size_t) kvh * hd + min(tid, hd - 1)];
+
+    // (2) roped queries, the new key and value, the cached keys into LDS
+#pragma unroll
+    for (int u = 0; u < QR_PER_THREAD; ++u) {
+        const uint32_t idx = tid + (uint32_t) u * ATT_THREADS;
+        if (idx < grp * hd) qr[idx / hd][idx % hd] = rope_apply(qi[u], idx % hd, half);
+    }
+    if (pos - s0 < ATT_POS && tid < hd) {
+        const float val = rope_apply(ki, tid, half);
+        kt[pos - s0][tid] = val;
+        kc[(size_t) pos * hd + tid] = val;
+        vc[(size_t) pos * hd + tid] = vnew;
+    }
+#pragma unroll
+    for (int u = 0; u < KT_LOADS; ++u) {
+        const uint32_t f = tid + (uint32_t) u * ATT_THREADS;
+        const uint32_t r = f / hd4, c4 = f % hd4;
+        if (f < n_f4 && s0 + r < pos) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
     }
     __syncthreads();
-    const uint32_t r = tid % ATT_POS;
-    if (r < n_here) {
-        for (uint32_t hh = tid / ATT_POS; hh < grp; hh += ATT_THREADS / ATT_POS) {
-            float acc = 0.0f;
-            for (uint32_t d = 0; d < hd; ++d) acc = acc + qr[hh][d] * kt[r][d];
-            A.scores[(size_t) (kvh * grp + hh) * A.n_ctx + s0 + r] = acc * A.attn_scale;
+    // (3) thread (h, r): the dot in order of d
+    const uint32_t r = tid % ATT_POS, hh = tid / ATT_POS;
+    if (r < min(ATT_POS, npast - s0) && hh < grp) {
+        float acc = 0.0f;
+        for (uint32_t d4 = 0; d4 < hd4; ++d4) {
+            const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&kt[r][4 * d4]);
+            const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&qr[hh][4 * d4]);
+            acc = acc + q4[0] * k4[0];
+            acc = acc + q4[1] * k4[1];
+            acc = acc + q4[2] * k4[2];
+            acc = acc + q4[3] * k4[3];
         }
+        A.scores[(size_t) (kvh * grp + hh) * A.sc_stride + s0 + r] = acc * A.attn_scale;
     }
 }
 
-// Softmax and p . V: workgroup (KV head, 16 head dimensions). Wave w takes
-// the softmax of query heads w, w + 4, ... of the KV head (src/ops.c:386-422:
-// max; ggml_v_expf over whole groups of eight, the C library's expf over the
-// rest; the double sum, each eight-group added as ((t0 + t1) + t2) + t3 of
-// t_j = e_j + e_{j+4}; 1/sum narrowed to f32; p = e * inv). Then thread
-// (h, dd) accumulates p_s * v_s over s = 0..pos in order
-// (src/forward.c:706-726), V staged through LDS.
+// Softmax and p . V: workgroup (KV head, 16 head dimensions), four waves.
+//  - The slice of V for the first 1536 positions is loaded first, all of it
+//    in flight (24 float4 per thread).
+//  - Wave w takes the softmax of query head w of the KV head
+//    (src/ops.c:386-422): the max; ggml_v_expf over whole groups of eight,
+//    the C library's expf over the rest; the double sum with each group
+//    added as ((t0 + t1) + t2) + t3 of t_j = e_j + e_{j+4}, in any order,
+//    checked, in the reference's order when the check cannot decide;
+//    inv = 1/sum narrowed to f32; p = e * inv. Each lane holds groups of
+//    eight consecutive scores, so a group's sum never leaves its lane, and
+//    the first round's e go to LDS in the same pass.
+//  - Per round of 1536 positions, p and V (transposed) in LDS; wave 0, one
+//    lane per (head, dimension), adds p_s * v_s to its accumulator in order
+//    of s (src/forward.c:706-726), its LDS reads sixteen positions ahead.
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_dec_pv(dec_attn A) {
-    __shared__ float P[PV_MAX_P];
-    __shared__ float vs[2][PV_CHUNK][PV_SLICE];
-    __shared__ float inv_h[ATT_MAX_GRP];
+    __shared__ __attribute__((aligned(16))) float P[ATT_MAX_GRP][PV_RPOS];
+    __shared__ __attribute__((aligned(16))) float Vt[PV_SLICE][PV_VSTRIDE];
+    __shared__ float stat_inv[ATT_MAX_GRP], stat_m[ATT_MAX_GRP];
+    __shared__ uint64_t tab[32];          // the expf table, next to the lanes that index it
     const uint32_t kvh = blockIdx.x, d0 = blockIdx.y * PV_SLICE, tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
     const uint32_t npast = (uint32_t) A.step->pos + 1;
-    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd;
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
     const uint32_t nb = npast / 8, nt = nb * 8;
+    const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d0;
 
-    // exponentials
-    for (uint32_t hh = wave; hh < grp; hh += ATT_THREADS / 64) {
-        const float *sc = A.scores + (size_t) (kvh * grp + hh) * A.n_ctx;
-        float *p = P + hh * npast;
-        float m = -INFINITY;
-        for (uint32_t s = lane; s < npast; s += 64) m = fmaxf(m, sc[s]);
-        m = wave_max(m);
-        for (uint32_t s = lane; s < npast; s += 64) {
-            const float x = sc[s] - m;
-            p[s] = s < nt ? ggml_v_expf(x) : sllm_libm_expf(x, c_expf_tab);
+    // thread t holds float4 f = t + 256 u of a round: position f / 4,
+    // dimensions 4 (f % 4) .. + 3 of the slice
+    f32x4 vr[PV_VLOADS];
+    auto load_v = [&](uint32_t base) {
+#pragma unroll
+        for (int u = 0; u < PV_VLOADS; ++u) {
+            const uint32_t f = tid + (uint32_t) u * ATT_THREADS;
+            const uint32_t sp = min(base + f / 4, npast - 1);
+            vr[u] = *G_CAST(const f32x4, vc + (size_t) sp * hd + 4 * (f % 4));
         }
-    }
+    };
+    load_v(0);
+    if (tid < 32) tab[tid] = c_expf_tab[tid];
     __syncthreads();
 
-    // sums: any order, checked; the reference's order when the check fails
-    auto block_sum = [](const float *e) {
+    auto group_sum = [](const float (&e)[8]) {
         const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
         const double t2 = (double) e[2] + (double) e[6], t3 = (double) e[3] + (double) e[7];
         return ((t0 + t1) + t2) + t3;
     };
-    for (uint32_t hh = wave; hh < grp; hh += ATT_THREADS / 64) {
-        const float *p = P + hh * npast;
-        double part = 0.0;
-        for (uint32_t b = lane; b < nb; b += 64) part += block_sum(p + 8 * b);
-        if (lane == 0) {
-            for (uint32_t s = nt; s < npast; ++s) part += (double) p[s];
+    // eight scores from position s of a row (clamped inside the row: only
+    // groups wholly past npast move)
+    auto load8 = [&](const float *sc, uint32_t s, float (&v)[8]) {
+        const uint32_t at = min(s, ss - 8);
+        const f32x4 a = *G_CAST(const f32x4, sc + at), b = *G_CAST(const f32x4, sc + at + 4);
+        v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+        v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+    };
+    // e of the group at s (lanes whose group reaches into the tail take the
+    // C library's expf there)
+    auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = v[i] - m;
+            v[i] = s + (uint32_t) i < nt ? ggml_v_expf(x) : sllm_libm_expf(x, tab);
         }
+    };
+    if (wave < grp) {
+        const float *sc = A.scores + (size_t) (kvh * grp + wave) * ss;
+        float *ph = P[wave];
+        float m = -INFINITY;
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            load8(sc, s, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
+        }
+        m = wave_max(m);
+        // e (of the first round into LDS) and the sum of whole groups; the
+        // tail positions, one lane each
+        double part = 0.0;
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            load8(sc, s, v);
+            exps8(v, s, m);
+            if (s + 8 <= npast) part += group_sum(v);
+            if (s < PV_RPOS) {
+                *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
+                *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
+            }
+        }
+        if (lane < npast - nt) part += (double) sllm_libm_expf(sc[nt + lane] - m, tab);
         const double sum = wave_sum_d(part);
         const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
         float inv = (float) (1.0 / (sum - bound));
         if (inv != (float) (1.0 / (sum + bound))) {   // uniform over the wave
             if (lane == 0) {
                 double seq = 0.0;
-                for (uint32_t b = 0; b < nb; ++b) seq += block_sum(p + 8 * b);
-                for (uint32_t s = nt; s < npast; ++s) seq += (double) p[s];
+                for (uint32_t s = 0; s < nt; s += 8) {
+                    float v[8];
+                    load8(sc, s, v);
+                    exps8(v, s, m);
+                    seq += group_sum(v);
+                }
+                for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
                 inv = (float) (1.0 / seq);
             }
             inv = __shfl(inv, 0, 64);
         }
-        if (lane == 0) inv_h[hh] = inv;
+        // p of the first round, in place
+        const uint32_t n0 = min(npast, PV_RPOS);
+        for (uint32_t i = 4 * lane; i < n0; i += 256) {
+            f32x4 e4 = *reinterpret_cast<const f32x4 *>(ph + i);
+            e4[0] = e4[0] * inv; e4[1] = e4[1] * inv; e4[2] = e4[2] * inv; e4[3] = e4[3] * inv;
+            *reinterpret_cast<f32x4 *>(ph + i) = e4;
+        }
+        if (lane == 0) {
+            stat_m[wave] = m;
+            stat_inv[wave] = inv;
+        }
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < grp * npast; i += ATT_THREADS) P[i] = P[i] * inv_h[i / npast];
 
-    // p . V: V[s][d0 .. d0+16) staged PV_CHUNK positions at a time
-    const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d0;
-    const uint32_t chains = grp * PV_SLICE;
-    const uint32_t hh = tid / PV_SLICE, dd = tid % PV_SLICE;
-    const uint32_t n_chunks = (npast + PV_CHUNK - 1) / PV_CHUNK;
-    f32x4 stage[4];
-    auto load_chunk = [&](uint32_t c) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t idx = tid + (uint32_t) u * ATT_THREADS, r = idx / 4, c4 = idx % 4;
-            const uint32_t s = min(c * PV_CHUNK + r, npast - 1);
-            stage[u] = *G_CAST(const f32x4, vc + (size_t) s * hd + 4 * c4);
-        }
-    };
-    auto store_chunk = [&](uint32_t buf) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t idx = tid + (uint32_t) u * ATT_THREADS, r = idx / 4, c4 = idx % 4;
-            *reinterpret_cast<f32x4 *>(&vs[buf][r][4 * c4]) = stage[u];
-        }
-    };
-    load_chunk(0);
-    __syncthreads();                 // P normalised everywhere
-    store_chunk(0);
-    __syncthreads();
+    // rounds of 1536 positions
+    const bool chain = wave == 0 && lane < grp * PV_SLICE;
+    const float *ph = P[lane / PV_SLICE];
+    const float *vt = Vt[lane % PV_SLICE];
     float acc = 0.0f;
-    for (uint32_t c = 0; c < n_chunks; ++c) {
-        if (c + 1 < n_chunks) load_chunk(c + 1);
-        if (tid < chains) {
-            const float *p = P + hh * npast + c * PV_CHUNK;
-            const uint32_t n = min(PV_CHUNK, npast - c * PV_CHUNK);
-            for (uint32_t r = 0; r < n; ++r) acc = acc + p[r] * vs[c & 1][r][dd];
+    for (uint32_t base = 0; base < npast; base += PV_RPOS) {
+        const uint32_t n = min(PV_RPOS, npast - base);
+        if (base > 0) {
+            __syncthreads();                      // stat_* visible; the last round's reads done
+            load_v(base);
+            if (wave < grp) {                     // p of this round, recomputed (the same bits)
+                const float *sc = A.scores + (size_t) (kvh * grp + wave) * ss;
+                const float m = stat_m[wave], inv = stat_inv[wave];
+                for (uint32_t i0 = 0; i0 < n; i0 += 512) {
+                    float v[8];
+                    const uint32_t i = i0 + 8 * lane;
+                    load8(sc, base + i, v);
+                    exps8(v, base + i, m);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if (i + (uint32_t) e < n) P[wave][i + (uint32_t) e] = v[e] * inv;
+                    }
+                }
+            }
         }
-        if (c + 1 < n_chunks) store_chunk((c + 1) & 1);
+#pragma unroll
+        for (int u = 0; u < PV_VLOADS; ++u) {
+            const uint32_t f = tid + (uint32_t) u * ATT_THREADS, r = f / 4, c4 = f % 4;
+            if (r < n) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Vt[4 * c4 + (uint32_t) e][r] = vr[u][e];
+            }
+        }
         __syncthreads();
+        if (chain) {
+            // sixteen positions per step, the next step's reads in flight
+            f32x4 pa[4], va[4], pb[4], vb[4];
+            auto rd = [&](uint32_t at, f32x4 (&pp)[4], f32x4 (&vv)[4]) {
+                const uint32_t c = min(at, PV_RPOS - 16);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    pp[t] = *reinterpret_cast<const f32x4 *>(ph + c + 4 * t);
+                    vv[t] = *reinterpret_cast<const f32x4 *>(vt + c + 4 * t);
+                }
+            };
+            auto add16 = [&](const f32x4 (&pp)[4], const f32x4 (&vv)[4]) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc = acc + pp[t][e] * vv[t][e];
+                }
+            };
+            uint32_t s = 0;
+            rd(0, pa, va);
+            for (; s + 32 <= n; s += 32) {
+                rd(s + 16, pb, vb);
+                add16(pa, va);
+                rd(s + 32, pa, va);
+                add16(pb, vb);
+            }
+            if (s + 16 <= n) {
+                add16(pa, va);
+                s += 16;
+            }
+            for (; s < n; ++s) acc = acc + ph[s] * vt[s];
+        }
     }
-    if (tid < chains) A.out[(size_t) (kvh * grp + hh) * hd + d0 + dd] = acc;
+    if (chain) A.out[(size_t) (kvh * grp + lane / PV_SLICE) * hd + d0 + lane % PV_SLICE] = acc;
 }
 
 // ---------------------------------------------------------------------------
 // output: x = a + b, RMSNorm with output_norm, the F16 rows
-// (src/forward.c:800-827), argmax (src/forward.c:876-883) and the next token
+// (src/forward.c:800-827), then the argmax (src/forward.c:876-883) and the
+// next token in a one-workgroup kernel
 // ---------------------------------------------------------------------------
 
 struct dec_lm {
@@ -574,27 +724,55 @@ struct dec_lm {
     const float    *norm_w;
     const uint16_t *embd;        // [n_vocab][n_embd] f16, the tied output projection
     float          *logits;
-    dec_step       *step;
+    uint64_t       *partial;     // one argmax key per workgroup
     float           eps;
     uint32_t        n_embd, n_vocab, pad;
 };
 static_assert(sizeof(dec_lm) == 64, "dec_lm must match decode.c");
 
 constexpr int LM_THREADS = 256;
-constexpr uint32_t LM_ROWS = 64;        // four lanes per row
+constexpr uint32_t LM_ROWS = 64;        // rows per pass: four lanes per row
 constexpr uint32_t LM_MAX_E = 8192;
-constexpr int LM_UNROLL = 8;
+constexpr int LM_UNROLL = 8;            // 32-element steps per load batch
+
+// The argmax key of one logit: ordered like the float, -0 tied with +0, the
+// lower row winning ties; NaN (never greater than anything) is 0.
+__device__ __forceinline__ uint64_t argmax_key(float s, uint32_t row) {
+    if (__builtin_isnan(s)) return 0;
+    const uint32_t u = __float_as_uint(s == 0.0f ? 0.0f : s);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t) ord << 32) | (uint64_t) (0xffffffffu - row);
+}
 
 // Row . xn as src/ops.c:106-154 orders it: lane j of a row's four holds
 // acc[j][0..7], element 32i + 8j + l going into acc[j][l] by FMA; then
 // acc0 += acc2, acc1 += acc3, acc0 += acc1; t_l = acc0[l] + acc0[l+4];
 // (t0 + t1) + (t2 + t3). n_embd % 32 == 0, so there is no scalar tail.
+// Workgroup w takes the 64-row passes w, w + G, ... (G = gridDim.x); each
+// lane streams its rows in batches of eight 16-byte loads with the next
+// batch always in flight, and the first batch is issued before the norm.
 extern "C" __global__ void __launch_bounds__(LM_THREADS)
 sllm_k_dec_lm_head(dec_lm L) {
     __shared__ __attribute__((aligned(16))) float xn[LM_MAX_E];
     __shared__ double red_d[LM_THREADS / 64], lane_d[4];
     __shared__ uint64_t red_k[LM_THREADS / 64];
     const uint32_t e = L.n_embd, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t j = lane % 4, steps = e / 32, nb = (steps + LM_UNROLL - 1) / LM_UNROLL;
+    const uint32_t n_pass = (L.n_vocab + LM_ROWS - 1) / LM_ROWS;
+    const uint32_t my_passes = blockIdx.x < n_pass ? (n_pass - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const uint32_t total = my_passes * nb;               // (pass, batch) items of this workgroup
+    auto row_of = [&](uint32_t item) {
+        const uint32_t pass = blockIdx.x + (min(item, total - 1) / nb) * gridDim.x;
+        return min(pass * LM_ROWS + wave * 16 + lane / 4, L.n_vocab - 1);
+    };
+    auto load = [&](uint32_t item, u32x4 (&h)[LM_UNROLL]) {
+        const uint32_t it = min(item, total - 1), b = it % nb;
+        const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) row_of(it) * e) + j;
+#pragma unroll
+        for (int u = 0; u < LM_UNROLL; ++u) h[u] = __builtin_nontemporal_load(w + 4 * min(b * LM_UNROLL + u, steps - 1));
+    };
+    u32x4 ha[LM_UNROLL], hb[LM_UNROLL];
+    if (total > 0) load(0, ha);
 
     double part = 0.0;
     for (uint32_t i = tid; i < e; i += LM_THREADS) {
@@ -602,83 +780,102 @@ sllm_k_dec_lm_head(dec_lm L) {
         xn[i] = v;
         part += (double) (v * v);
     }
-    const float mean = rms_mean(part, e, red_d, lane_d, [&](uint32_t j) { return L.a[j] + L.b[j]; });
+    const float mean = rms_mean(part, e, red_d, lane_d, [&](uint32_t k) { return L.a[k] + L.b[k]; });
     const float scale = 1.0f / sqrtf(mean + L.eps);
     for (uint32_t i = tid; i < e; i += LM_THREADS) xn[i] = (scale * xn[i]) * L.norm_w[i];
     __syncthreads();
 
-    const uint32_t row = blockIdx.x * LM_ROWS + wave * 16 + lane / 4, j = lane % 4;
-    const bool valid = row < L.n_vocab;
-    const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) (valid ? row : L.n_vocab - 1) * e) + j;
-    const uint32_t steps = e / 32;
+    uint64_t best = 0;
     float acc[8];
 #pragma unroll
     for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
-    for (uint32_t i0 = 0; i0 < steps; i0 += LM_UNROLL) {
-        u32x4 h[LM_UNROLL];
-#pragma unroll
-        for (int u = 0; u < LM_UNROLL; ++u) h[u] = __builtin_nontemporal_load(w + 4 * min(i0 + u, steps - 1));
+    auto consume = [&](uint32_t item, const u32x4 (&h)[LM_UNROLL]) {
+        const uint32_t b = item % nb;
 #pragma unroll
         for (int u = 0; u < LM_UNROLL; ++u) {
-            if (i0 + u < steps) {
+            const uint32_t step = b * LM_UNROLL + (uint32_t) u;
+            if (step < steps) {
                 const f32x8 hf = __builtin_convertvector(__builtin_bit_cast(f16x8, h[u]), f32x8);
-                const float *x = xn + 32 * (i0 + u) + 8 * j;
+                const float *x = xn + 32 * step + 8 * j;
 #pragma unroll
                 for (int l = 0; l < 8; ++l) acc[l] = fmaf(hf[l], x[l], acc[l]);
             }
         }
-    }
+        if (b == nb - 1) {                                // the row is complete
+            float r[8];
 #pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = acc[l] + __shfl_xor(acc[l], 2, 64);   // acc0 += acc2, acc1 += acc3
+            for (int l = 0; l < 8; ++l) r[l] = acc[l] + __shfl_xor(acc[l], 2, 64);  // acc0 += acc2, acc1 += acc3
 #pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = acc[l] + __shfl_xor(acc[l], 1, 64);   // acc0 += acc1
-    const float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
-    const float s = (t0 + t1) + (t2 + t3);
-
-    uint64_t key = 0;
-    if (valid && j == 0) {
-        G_CAST(float, L.logits)[row] = s;
-        if (!__builtin_isnan(s)) {
-            const uint32_t u = __float_as_uint(s == 0.0f ? 0.0f : s);       // -0 ties with +0
-            const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-            key = ((uint64_t) ord << 32) | (uint64_t) (0xffffffffu - row);  // the first index wins ties
+            for (int l = 0; l < 8; ++l) r[l] = r[l] + __shfl_xor(r[l], 1, 64);      // acc0 += acc1
+            const float t0 = r[0] + r[4], t1 = r[1] + r[5], t2 = r[2] + r[6], t3 = r[3] + r[7];
+            const float sdot = (t0 + t1) + (t2 + t3);
+            const uint32_t pass = blockIdx.x + (item / nb) * gridDim.x;
+            const uint32_t row = pass * LM_ROWS + wave * 16 + lane / 4;
+            if (j == 0 && row < L.n_vocab) {
+                G_CAST(float, L.logits)[row] = sdot;
+                const uint64_t key = argmax_key(sdot, row);
+                best = key > best ? key : best;
+            }
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
         }
+    };
+    // pairs of items: the next batch is loaded before the current one is used
+    uint32_t item = 0;
+    for (; item + 1 < total; item += 2) {
+        load(item + 1, hb);
+        consume(item, ha);
+        load(item + 2, ha);
+        consume(item + 1, hb);
     }
+    if (item < total) consume(item, ha);
+
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t other = __shfl_xor(key, o, 64);
-        key = other > key ? other : key;
+        const uint64_t other = __shfl_xor(best, o, 64);
+        best = other > best ? other : best;
     }
-    if (lane == 0) red_k[wave] = key;
+    if (lane == 0) red_k[wave] = best;
     __syncthreads();
     if (tid == 0) {
         uint64_t k = red_k[0];
         for (int i = 1; i < LM_THREADS / 64; ++i) k = red_k[i] > k ? red_k[i] : k;
-        dec_step *st = L.step;
-        atomicMax((unsigned long long *) &st->key, (unsigned long long) k);
-        __threadfence();
-        const uint32_t done = atomicAdd(&st->ticket, 1u);
-        if (done == gridDim.x - 1) {
-            // the last workgroup: every row's logit and key are in
-            __threadfence();
-            const uint64_t best = __hip_atomic_load(&st->key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            int32_t next = best == 0 ? 0 : (int32_t) (0xffffffffu - (uint32_t) best);
-            const float l0 = __hip_atomic_load(L.logits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (__builtin_isnan(l0)) next = 0;      // a NaN first logit is never beaten
-            st->next = next;
-            st->key = 0;
-            st->ticket = 0;
-            if (st->advance) {
-                if (st->i_feed < st->n_feed) {
-                    st->token = st->feed[st->i_feed];
-                    st->i_feed += 1;
-                } else {
-                    if (st->gen != nullptr && st->n_gen < st->cap_gen) st->gen[st->n_gen] = next;
-                    st->n_gen += 1;
-                    st->token = next;
-                }
-                st->pos += 1;
-            }
+        L.partial[blockIdx.x] = k;
+    }
+}
+
+// The argmax over the output workgroups' keys (first maximum; a NaN first
+// logit is never beaten, src/forward.c:876-883), and the step record moved
+// on: next token from the prompt still to consume, else the argmax, which is
+// also appended to the generated tokens.
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_dec_argmax(const uint64_t *__restrict__ partial, uint32_t n, const float *__restrict__ logits,
+                  dec_step *__restrict__ st) {
+    __shared__ uint64_t red[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    uint64_t best = 0;
+    for (uint32_t i = tid; i < n; i += 256) best = partial[i] > best ? partial[i] : best;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t other = __shfl_xor(best, o, 64);
+        best = other > best ? other : best;
+    }
+    if (lane == 0) red[tid >> 6] = best;
+    __syncthreads();
+    if (tid != 0) return;
+    for (int i = 1; i < 4; ++i) best = red[i] > best ? red[i] : best;
+    int32_t next = best == 0 ? 0 : (int32_t) (0xffffffffu - (uint32_t) best);
+    if (__builtin_isnan(logits[0])) next = 0;
+    st->next = next;
+    if (st->advance) {
+        if (st->i_feed < st->n_feed) {
+            st->token = st->feed[st->i_feed];
+            st->i_feed += 1;
+        } else {
+            if (st->gen != nullptr && st->n_gen < st->cap_gen) st->gen[st->n_gen] = next;
+            st->n_gen += 1;
+            st->token = next;
         }
+        st->pos += 1;
     }
 }
