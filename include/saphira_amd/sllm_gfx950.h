@@ -182,6 +182,32 @@ int  sllm_gfx950_plan_run(const sllm_gfx950_plan *plan);
 int  sllm_gfx950_plan_run_marked(const sllm_gfx950_plan *plan, int event);
 void sllm_gfx950_plan_destroy(sllm_gfx950_plan *plan);
 
+/* ------------------------------------------------------------------ */
+/* several tokens against one tensor (int8 MFMA)                       */
+/* ------------------------------------------------------------------ */
+
+/* The projections of a chunk of m tokens (src/forward.c:589-793 with
+ * n = m > 1, where each token is quantised on its own and runs its own
+ * GEMV and epilogue against the same tensor) as one int8-MFMA GEMM:
+ *   rows_out[t][r] = sum_k code(r,k) * q[t][k]            (int32, exact)
+ *   out[t][r]      = (float)(rows_out[t][r] - act[t].sum) * (w_scale / act[t].scale)
+ * for t < m, r < n_rows; q is m rows of n int8 (n a multiple of 128), act m
+ * scale/sum pairs, out / rows_out m rows of n_rows (either may be NULL, not
+ * both; act is read only for out). w is the whole packed tensor (codes and
+ * tail). Device pointers, 16-byte aligned. The results are the reference's
+ * token by token, bit for bit. */
+int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
+                     const sllm_gfx950_act *act, size_t m, float *out, int32_t *rows_out);
+
+/* Quantise m rows of x (m x n f32, one scale/sum per row, as
+ * sllm_gfx950_quant_act) into q / act, then sllm_gfx950_gemm: two launches. */
+int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const float *x, size_t m,
+                             int8_t *q, sllm_gfx950_act *act, float *out, int32_t *rows_out);
+
+/* GEMM tile override for tuning and tests: 0 automatic (by m), 1: 16 tokens
+ * x 64 rows per workgroup, 2: 32 x 128, 3: 64 x 128. */
+int sllm_gfx950_set_gemm_tile(int tile);
+
 /* Launch-geometry override for tuning sweeps and tests; affects launches
  * and plans created afterwards. All zero (variant -1) is automatic.
  *   path           0 auto and 2: slab kernel for K <= 7168, streaming kernel

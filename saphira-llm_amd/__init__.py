@@ -111,6 +111,10 @@ PROTOTYPES = {
     "sllm_kdispatch_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "sllm_kdispatch_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),
     "sllm_kdispatch_gemv": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "sllm_gfx950_gemm": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "sllm_gfx950_linear_batch": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p, c_void_p,
+                                         c_void_p, c_void_p]),
+    "sllm_gfx950_set_gemm_tile": (c_int, [c_int]),
     "sllm_gfx950_model_upload": (c_int, [POINTER(ModelDesc), POINTER(c_void_p)]),
     "sllm_gfx950_model_free": (None, [c_void_p]),
     "sllm_gfx950_ctx_new": (c_int, [c_void_p, c_int32, POINTER(c_void_p)]),
@@ -303,6 +307,15 @@ class Device:
 
     def plan_destroy(self, p):
         self.lib.sllm_gfx950_plan_destroy(p)
+
+    def gemm(self, w, n_rows, n, q, act, m, out, rows_out=None):
+        check(self.lib.sllm_gfx950_gemm(w, n_rows, n, q, act, m, out, rows_out), "gemm")
+
+    def linear_batch(self, w, n_rows, n, x, m, q, act, out, rows_out=None):
+        check(self.lib.sllm_gfx950_linear_batch(w, n_rows, n, x, m, q, act, out, rows_out), "linear_batch")
+
+    def set_gemm_tile(self, tile=0):
+        check(self.lib.sllm_gfx950_set_gemm_tile(tile), "set_gemm_tile")
 
     def set_tuning(self, path=0, variant=-1, lanes_per_row=0, waves=0, rows_per_wg=0, slab_kib=0):
         check(self.lib.sllm_gfx950_set_tuning(path, variant, lanes_per_row, waves, rows_per_wg, slab_kib),

@@ -118,6 +118,8 @@ static struct {
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
+    hipFunction_t  k_gemm[3];
+    int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
     hipEvent_t     ev_start, ev_stop;
@@ -183,6 +185,9 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_copy, g.mod, "sllm_k_copy"));
     HIP_TRY(hipModuleGetFunction(&g.k_checksum, g.mod, "sllm_k_checksum"));
     HIP_TRY(hipModuleGetFunction(&g.k_slab, g.mod, "sllm_k_gemv_slab"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[0], g.mod, "sllm_k_gemm_mfma_1x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[1], g.mod, "sllm_k_gemm_mfma_2x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[2], g.mod, "sllm_k_gemm_mfma_4x2"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
@@ -891,6 +896,65 @@ int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n, const i
     if (out == NULL || act == NULL || q == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv_epilogue: NULL q, act or out");
     const sllm_gfx950_gemv_job j = { w, n_rows, n, NULL, (int8_t *) q, (sllm_gfx950_act *) act, out, NULL };
     return single_launch(&j);
+}
+
+/* ------------------------------------------------------------------ */
+/* batched GEMM (i2s_kernels.hip: gemm_args)                           */
+/* ------------------------------------------------------------------ */
+
+typedef struct k_gemm_args {
+    const uint8_t         *w;
+    const int8_t          *q;
+    const sllm_gfx950_act *act;
+    float                 *out;
+    int32_t               *out_i;
+    uint32_t               n_rows, k, m, pad;
+} k_gemm_args;
+
+_Static_assert(sizeof(k_gemm_args) == 56, "k_gemm_args must match gemm_args in i2s_kernels.hip");
+
+/* tile shapes: token tiles x row tiles of 16 per wave, four waves along
+ * the rows */
+static const uint32_t k_gemm_tm[3] = { 1, 2, 4 }, k_gemm_tn[3] = { 1, 2, 2 };
+
+int sllm_gfx950_set_gemm_tile(int tile) {
+    if (tile < 0 || tile > 3) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. 3");
+    g.force_gemm_tile = tile;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
+                     const sllm_gfx950_act *act, size_t m, float *out, int32_t *rows_out) {
+    NEED_OPEN();
+    if (m == 0) return SLLM_GFX950_OK;
+    int st = check_weights(w, n_rows, n);
+    if (st != SLLM_GFX950_OK) return st;
+    if (q == NULL || ((uintptr_t) q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemm: q must be given and 16-byte aligned");
+    if (out == NULL && rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: no output");
+    if (out != NULL && act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: the epilogue needs act");
+    if (m > (size_t) UINT32_MAX / 2 || (uint64_t) m * n_rows > (uint64_t) 1 << 40) {
+        return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m = %zu too large", m);
+    }
+    int tile = g.force_gemm_tile - 1;
+    if (tile < 0) tile = m <= 16 ? 0 : (m <= 32 ? 1 : 2);
+    const uint32_t rows_per_wg = 4u * 16u * k_gemm_tn[tile], tok_per_wg = 16u * k_gemm_tm[tile];
+    const uint64_t gx = (n_rows + rows_per_wg - 1) / rows_per_wg, gy = (m + tok_per_wg - 1) / tok_per_wg;
+    if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");
+    k_gemm_args a = { w, q, act, out, rows_out, (uint32_t) n_rows, (uint32_t) n, (uint32_t) m, 0 };
+    void *args[] = { &a };
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm[tile], (uint32_t) gx, (uint32_t) gy, 1, 256, 1, 1, 0, g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const float *x, size_t m,
+                             int8_t *q, sllm_gfx950_act *act, float *out, int32_t *rows_out) {
+    NEED_OPEN();
+    if (m == 0) return SLLM_GFX950_OK;
+    if (x == NULL || q == NULL || act == NULL) return fail(SLLM_GFX950_ERR_ARG, "linear_batch: NULL x, q or act");
+    int st = check_weights(w, n_rows, n);
+    if (st == SLLM_GFX950_OK) st = sllm_gfx950_quant_act(x, n, m, q, act);
+    if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(w, n_rows, n, q, act, m, out, rows_out);
+    return st;
 }
 
 int sllm_gfx950_linear(const uint8_t *w, size_t n_rows, size_t n, const float *x,

@@ -281,6 +281,120 @@ __device__ __forceinline__ bool stream_share(const gemv_job *__restrict__ jobs,
     return row_begin < row_end;
 }
 
+
+// ---------------------------------------------------------------------------
+// batched ternary GEMM on int8 MFMA (several tokens against one tensor: the
+// projections of a chunk, src/forward.c:589-793 with n > 1)
+// ---------------------------------------------------------------------------
+//
+// C[t][n] = sum_k q[t][k] * code[n][k] with v_mfma_i32_16x16x64_i8: A = 16
+// tokens x 64 k, B = 64 k x 16 rows. Lane l holds A[l % 16][16 (l/16) ..
+// + 15] and B[16 (l/16) .. + 15][l % 16] and receives C[4 (l/16) + r][l % 16]
+// (r = 0..3). The 64 k of one instruction are chosen to fit the I2_S layout:
+// half h of 128-element block b, all four fields -- lane group g takes field
+// g, elements 128 b + 32 g + 16 h + (0..15) -- so a lane's B operand is
+// field g of the same 16 packed bytes the other three lane groups read,
+// isolated in place (values 0..2, one per byte), and its A operand is 16
+// consecutive int8 of the token's row. Integer sums do not depend on the
+// order of k, so the dots are exactly the reference's.
+//
+// A workgroup is four waves side by side along the rows; each wave owns TM
+// token tiles x TN row tiles (16 x 16 each), with the next k step's loads in
+// flight while the current step's MFMAs run. No LDS.
+
+typedef int32_t i32x4v __attribute__((ext_vector_type(4)));
+
+struct gemm_args {
+    const uint8_t   *w;          // packed tensor with its tail
+    const int8_t    *q;          // [m][k] int8
+    const act_t     *act;        // [m]
+    float           *out;        // [m][n_rows] epilogue, or null
+    int32_t         *out_i;      // [m][n_rows] raw dots, or null
+    uint32_t         n_rows, k, m, pad;
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_load(const gemm_args &G, uint32_t t0, uint32_t n0, uint32_t step,
+                                          i32x4v (&a)[TM], u32x4 (&b)[TN]) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+    const uint32_t blk = step >> 1, h = step & 1u;
+    const uint32_t kq = 128u * blk + 32u * (uint32_t) g + 16u * h;        // A: k offset of this lane group
+    const uint32_t kw = 32u * blk + 16u * h;                              // B: byte offset in the row
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+        const uint32_t t = min(t0 + 16u * (uint32_t) tm + (uint32_t) li, G.m - 1);
+        a[tm] = *G_CAST(const i32x4v, G.q + (size_t) t * G.k + kq);
+    }
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t n = min(n0 + 16u * (uint32_t) tn + (uint32_t) li, G.n_rows - 1);
+        b[tn] = __builtin_nontemporal_load(G_CAST(const u32x4, G.w + (size_t) n * (G.k >> 2) + kw));
+    }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_mma(const i32x4v (&a)[TM], const u32x4 (&b)[TN], i32x4v (&c)[TM][TN]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    const uint32_t shift = 6u - 2u * (uint32_t) g;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+        i32x4v codes;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) codes[d] = (int32_t) ((b[tn][d] >> shift) & 0x03030303u);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) c[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[tm], codes, c[tm][tn], 0, 0, 0);
+    }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_block(const gemm_args &G) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) threadIdx.x >> 6);
+    const uint32_t t0 = blockIdx.y * 16u * TM;
+    const uint32_t n0 = (blockIdx.x * 4u + wave) * 16u * TN;
+    const uint32_t steps = G.k / 64u;
+    i32x4v c[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
+    }
+    i32x4v a0[TM], a1[TM];
+    u32x4 b0[TN], b1[TN];
+    gemm_load<TM, TN>(G, t0, n0, 0, a0, b0);
+    uint32_t s = 0;
+    for (; s + 2 <= steps; s += 2) {
+        gemm_load<TM, TN>(G, t0, n0, s + 1, a1, b1);
+        gemm_mma<TM, TN>(a0, b0, c);
+        gemm_load<TM, TN>(G, t0, n0, min(s + 2, steps - 1), a0, b0);
+        gemm_mma<TM, TN>(a1, b1, c);
+    }
+    if (s < steps) gemm_mma<TM, TN>(a0, b0, c);
+
+    // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
+    // token, (float)(dot - sum) * post
+    const float ws = *G_CAST(const float, G.w + (size_t) G.n_rows * (G.k >> 2));
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t t = t0 + 16u * (uint32_t) tm + 4u * (uint32_t) g + (uint32_t) r;
+            if (t >= G.m) continue;
+            const act_t at = G.act[t];
+            const float post = ws / at.scale;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const uint32_t n = n0 + 16u * (uint32_t) tn + (uint32_t) li;
+                if (n < G.n_rows) {
+                    const int32_t d = c[tm][tn][r];
+                    if (G.out_i != nullptr) G_CAST(int32_t, G.out_i)[(size_t) t * G.n_rows + n] = d;
+                    if (G.out != nullptr) G_CAST(float, G.out)[(size_t) t * G.n_rows + n] = (float) (d - at.sum) * post;
+                }
+            }
+        }
+    }
+}
+
 } // namespace
 
 // ---------------------------------------------------------------------------
@@ -360,6 +474,17 @@ sllm_k_gemv_slab(const gemv_job *__restrict__ jobs, const wg_desc *__restrict__ 
 SLLM_STREAM_ENTRY(4)
 SLLM_STREAM_ENTRY(8)
 SLLM_STREAM_ENTRY(16)
+
+
+// Batched ternary GEMM: grid (ceil(n_rows / (64 TN)), ceil(m / (16 TM))),
+// blocks of 256. One instantiation per tile shape the host picks by m.
+#define SLLM_GEMM_ENTRY(TM, TN)                                                    \
+    extern "C" __global__ void __launch_bounds__(256)                             \
+    sllm_k_gemm_mfma_##TM##x##TN(gemm_args G) { gemm_block<TM, TN>(G); }
+
+SLLM_GEMM_ENTRY(1, 1)
+SLLM_GEMM_ENTRY(2, 2)
+SLLM_GEMM_ENTRY(4, 2)
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

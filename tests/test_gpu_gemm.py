@@ -1,0 +1,112 @@
+"""Several tokens against one tensor on int8 MFMA (sllm_gfx950_gemm /
+sllm_gfx950_linear_batch) against the oracle, token by token.
+
+The reference runs a chunk's projections one token at a time (each token
+quantised on its own, its own GEMV and epilogue, src/forward.c:589-793), so
+token t of the GEMM must equal the oracle's single-token linear of row t:
+quantised row and scale / sum, every int32 dot and every f32 output, bit
+for bit. Shapes: the BitNet-2B FFN pair (6912 x 2560, 2560 x 6912), a KV
+projection (640 x 2560) and a ragged one (200 rows, K = 384); token counts
+on and off the 16-token MFMA tile, up to the 512-token prefill chunk; every
+tile shape the kernel has.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _case(amd, seed, n_rows, n, m):
+    w = amd.synth_i2s(amd.synth_seed(3, seed, n_rows, n), n_rows, n)
+    x = np.concatenate([amd.synth_normal(amd.synth_seed(3, seed, t, 1000 + n), n) for t in range(m)])
+    return w, x.astype(np.float32)
+
+
+def _run(amd, dev, w, n_rows, n, x, m):
+    bw, bx = dev.put(w), dev.put(x)
+    bq, ba = dev.alloc(m * n), dev.alloc(8 * m)
+    by, bi = dev.alloc(4 * m * n_rows), dev.alloc(4 * m * n_rows)
+    try:
+        dev.linear_batch(bw.vp, n_rows, n, bx.vp, m, bq.vp, ba.vp, by.vp, bi.vp)
+        dev.sync()
+        y = by.download(np.float32, m * n_rows).reshape(m, n_rows)
+        d = bi.download(np.int32, m * n_rows).reshape(m, n_rows)
+        q = bq.download(np.int8, m * n).reshape(m, n)
+        raw = ba.download(np.uint8, 8 * m).tobytes()
+        act = np.frombuffer(raw, dtype=[("scale", "<f4"), ("sum", "<i4")])
+        return y, d, q, act
+    finally:
+        for b in (bw, bx, bq, ba, by, bi):
+            b.free()
+
+
+def _check(orc, w, n_rows, n, x, m, y, d, q, act, label):
+    for t in range(m):
+        yo, qo, do, so, su = orc.linear(w, n_rows, n, x[t * n:(t + 1) * n])
+        assert np.array_equal(q[t], qo), f"{label}: token {t} quantised row"
+        assert act[t]["sum"] == su and bits(act[t]["scale"]) == bits(so), f"{label}: token {t} scale / sum"
+        assert np.array_equal(d[t], do), f"{label}: token {t} dots"
+        assert np.array_equal(bits(y[t]), bits(yo)), f"{label}: token {t} outputs"
+
+
+SHAPES = [(6912, 2560), (2560, 6912), (640, 2560), (200, 384)]
+
+
+@pytest.mark.parametrize("n_rows,n", SHAPES, ids=[f"{a}x{b}" for a, b in SHAPES])
+@pytest.mark.parametrize("m", [1, 3, 4, 16, 17, 64, 100])
+def test_gemm_matches_the_oracle_token_by_token(amd, orc, dev, n_rows, n, m):
+    print(f"[gemm] {n_rows}x{n} m={m}", flush=True)
+    w, x = _case(amd, 1, n_rows, n, m)
+    y, d, q, act = _run(amd, dev, w, n_rows, n, x, m)
+    _check(orc, w, n_rows, n, x, m, y, d, q, act, f"{n_rows}x{n} m={m}")
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3])
+def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
+    n_rows, n, m = 640, 2560, 37
+    w, x = _case(amd, 2, n_rows, n, m)
+    dev.set_gemm_tile(tile)
+    try:
+        y, d, q, act = _run(amd, dev, w, n_rows, n, x, m)
+    finally:
+        dev.set_gemm_tile(0)
+    _check(orc, w, n_rows, n, x, m, y, d, q, act, f"tile {tile}")
+
+
+@pytest.mark.parametrize("n_rows,n", [(6912, 2560), (2560, 6912)], ids=["gate_up", "down"])
+def test_prefill_chunk_of_512_tokens(amd, orc, dev, n_rows, n):
+    """The 512-token prefill shape: every token's quantised row, dots and
+    outputs."""
+    m = 512
+    print(f"[gemm] prefill {n_rows}x{n}", flush=True)
+    w, x = _case(amd, 3, n_rows, n, m)
+    y, d, q, act = _run(amd, dev, w, n_rows, n, x, m)
+    _check(orc, w, n_rows, n, x, m, y, d, q, act, f"prefill {n_rows}x{n}")
+
+
+def test_zero_token_gives_nan_like_the_reference(amd, orc, dev):
+    n_rows, n, m = 256, 256, 5
+    w, x = _case(amd, 4, n_rows, n, m)
+    x[2 * n:3 * n] = 0.0
+    y, d, q, act = _run(amd, dev, w, n_rows, n, x, m)
+    assert np.isnan(y[2]).all() and (d[2] == 0).all() and act[2]["scale"] == 0
+    _check(orc, w, n_rows, n, x, 2, y, d, q, act, "rows before the zero token")
+
+
+def test_gemm_refuses_bad_arguments(amd, dev):
+    lib = amd.lib()
+    w = dev.put(amd.synth_i2s(1, 64, 256))
+    q, a, o = dev.alloc(256 * 2), dev.alloc(16), dev.alloc(4 * 64 * 2)
+    try:
+        assert lib.sllm_gfx950_gemm(w.vp, 64, 200, q.vp, a.vp, 2, o.vp, None) == -34    # K % 128
+        assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, None, 2, o.vp, None) == -1     # epilogue without act
+        assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 2, None, None) == -1     # no output
+        assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 0, o.vp, None) == 0      # nothing to do
+        assert lib.sllm_gfx950_set_gemm_tile(4) == -1
+    finally:
+        for b in (w, q, a, o):
+            b.free()
