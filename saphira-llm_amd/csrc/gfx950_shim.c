@@ -185,7 +185,7 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_copy, g.mod, "sllm_k_copy"));
     HIP_TRY(hipModuleGetFunction(&g.k_checksum, g.mod, "sllm_k_checksum"));
     HIP_TRY(hipModuleGetFunction(&g.k_slab, g.mod, "sllm_k_gemv_slab"));
-    HIP_TRY(hipModuleGetFunction(&g.k_gemm[0], g.mod, "sllm_k_gemm_mfma_1x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[0], g.mod, "sllm_k_gemm_mfma_s1x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[1], g.mod, "sllm_k_gemm_mfma_2x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[2], g.mod, "sllm_k_gemm_mfma_4x2"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
@@ -913,9 +913,9 @@ typedef struct k_gemm_args {
 
 _Static_assert(sizeof(k_gemm_args) == 56, "k_gemm_args must match gemm_args in i2s_kernels.hip");
 
-/* tile shapes: token tiles x row tiles of 16 per wave, four waves along
- * the rows */
-static const uint32_t k_gemm_tm[3] = { 1, 2, 4 }, k_gemm_tn[3] = { 1, 2, 2 };
+/* tile shapes per workgroup: tokens x rows (shape 0 splits K over its four
+ * waves instead of spreading them along the rows) */
+static const uint32_t k_gemm_tokens[3] = { 16, 32, 64 }, k_gemm_rows[3] = { 16, 128, 128 };
 
 int sllm_gfx950_set_gemm_tile(int tile) {
     if (tile < 0 || tile > 3) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. 3");
@@ -937,7 +937,7 @@ int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
     }
     int tile = g.force_gemm_tile - 1;
     if (tile < 0) tile = m <= 16 ? 0 : (m <= 32 ? 1 : 2);
-    const uint32_t rows_per_wg = 4u * 16u * k_gemm_tn[tile], tok_per_wg = 16u * k_gemm_tm[tile];
+    const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];
     const uint64_t gx = (n_rows + rows_per_wg - 1) / rows_per_wg, gy = (m + tok_per_wg - 1) / tok_per_wg;
     if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");
     k_gemm_args a = { w, q, act, out, rows_out, (uint32_t) n_rows, (uint32_t) n, (uint32_t) m, 0 };

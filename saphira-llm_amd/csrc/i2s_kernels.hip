@@ -346,30 +346,62 @@ __device__ __forceinline__ void gemm_mma(const i32x4v (&a)[TM], const u32x4 (&b)
     }
 }
 
-template <int TM, int TN>
+constexpr int GEMM_DEPTH = 4;       // k steps of loads in flight per wave
+
+// SPLIT = 1: the four waves sit side by side along the rows, each over all
+// of K. SPLIT = 4: the four waves share one output tile and take a quarter
+// of the k steps each; their int32 partial sums meet in LDS (exact in any
+// order) and wave 0 writes the tile -- four times the workgroups for the
+// small token counts whose grid would otherwise be a few dozen.
+template <int TM, int TN, int SPLIT>
 __device__ __forceinline__ void gemm_block(const gemm_args &G) {
+    __shared__ i32x4v part[SPLIT > 1 ? SPLIT - 1 : 1][TM][TN][64];
     const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) threadIdx.x >> 6);
     const uint32_t t0 = blockIdx.y * 16u * TM;
-    const uint32_t n0 = (blockIdx.x * 4u + wave) * 16u * TN;
-    const uint32_t steps = G.k / 64u;
+    const uint32_t n0 = (SPLIT > 1 ? blockIdx.x : blockIdx.x * 4u + wave) * 16u * TN;
+    const uint32_t steps_all = G.k / 64u;
+    const uint32_t s_begin = SPLIT > 1 ? steps_all * wave / SPLIT : 0u;
+    const uint32_t s_end = SPLIT > 1 ? steps_all * (wave + 1) / SPLIT : steps_all;
     i32x4v c[TM][TN];
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
     }
-    i32x4v a0[TM], a1[TM];
-    u32x4 b0[TN], b1[TN];
-    gemm_load<TM, TN>(G, t0, n0, 0, a0, b0);
-    uint32_t s = 0;
-    for (; s + 2 <= steps; s += 2) {
-        gemm_load<TM, TN>(G, t0, n0, s + 1, a1, b1);
-        gemm_mma<TM, TN>(a0, b0, c);
-        gemm_load<TM, TN>(G, t0, n0, min(s + 2, steps - 1), a0, b0);
-        gemm_mma<TM, TN>(a1, b1, c);
+    // a ring of GEMM_DEPTH steps: step s lives in slot s % GEMM_DEPTH and is
+    // refilled with step s + GEMM_DEPTH (the last step again past the end)
+    i32x4v a[GEMM_DEPTH][TM];
+    u32x4 bw[GEMM_DEPTH][TN];
+    const uint32_t last = s_end > s_begin ? s_end - 1 : s_begin;
+#pragma unroll
+    for (int i = 0; i < GEMM_DEPTH; ++i) gemm_load<TM, TN>(G, t0, n0, min(s_begin + (uint32_t) i, last), a[i], bw[i]);
+    for (uint32_t s = s_begin; s < s_end; s += GEMM_DEPTH) {
+#pragma unroll
+        for (int i = 0; i < GEMM_DEPTH; ++i) {
+            if (s + (uint32_t) i < s_end) gemm_mma<TM, TN>(a[i], bw[i], c);
+            gemm_load<TM, TN>(G, t0, n0, min(s + (uint32_t) i + GEMM_DEPTH, last), a[i], bw[i]);
+        }
     }
-    if (s < steps) gemm_mma<TM, TN>(a0, b0, c);
+    if (SPLIT > 1) {
+        if (wave > 0) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) part[wave - 1][tm][tn][lane] = c[tm][tn];
+            }
+        }
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < SPLIT - 1; ++w) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) c[tm][tn] += part[w][tm][tn][lane];
+            }
+        }
+    }
 
     // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
     // token, (float)(dot - sum) * post
@@ -380,7 +412,7 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
         for (int r = 0; r < 4; ++r) {
             const uint32_t t = t0 + 16u * (uint32_t) tm + 4u * (uint32_t) g + (uint32_t) r;
             if (t >= G.m) continue;
-            const act_t at = G.act[t];
+            const act_t at = G.act != nullptr ? G.act[t] : act_t { 1.0f, 0 };
             const float post = ws / at.scale;
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
@@ -476,15 +508,16 @@ SLLM_STREAM_ENTRY(8)
 SLLM_STREAM_ENTRY(16)
 
 
-// Batched ternary GEMM: grid (ceil(n_rows / (64 TN)), ceil(m / (16 TM))),
-// blocks of 256. One instantiation per tile shape the host picks by m.
-#define SLLM_GEMM_ENTRY(TM, TN)                                                    \
-    extern "C" __global__ void __launch_bounds__(256)                             \
-    sllm_k_gemm_mfma_##TM##x##TN(gemm_args G) { gemm_block<TM, TN>(G); }
-
-SLLM_GEMM_ENTRY(1, 1)
-SLLM_GEMM_ENTRY(2, 2)
-SLLM_GEMM_ENTRY(4, 2)
+// Batched ternary GEMM, blocks of 256: grid (row tiles, token tiles). One
+// instantiation per tile shape the host picks by token count:
+//   _s1x1  16 tokens x 16 rows, K split over the four waves
+//   _2x2   32 tokens x 128 rows      _4x2   64 tokens x 128 rows
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_mfma_s1x1(gemm_args G) { gemm_block<1, 1, 4>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_mfma_2x2(gemm_args G) { gemm_block<2, 2, 1>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_mfma_4x2(gemm_args G) { gemm_block<4, 2, 1>(G); }
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

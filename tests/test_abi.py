@@ -52,7 +52,7 @@ def test_library_embeds_a_gfx950_code_object():
     blob = open(os.path.join(ROOT, "saphira-llm_amd", "libsllm_gfx950.so"), "rb").read()
     assert b"amdgcn-amd-amdhsa--gfx950" in blob
     for k in (b"sllm_k_quant_act", b"sllm_k_quant_list", b"sllm_k_gemv_slab", b"sllm_k_gemv_stream_l4",
-              b"sllm_k_gemv_stream_l8", b"sllm_k_gemv_stream_l16", b"sllm_k_gemm_mfma_1x1",
+              b"sllm_k_gemv_stream_l8", b"sllm_k_gemv_stream_l16", b"sllm_k_gemm_mfma_s1x1",
               b"sllm_k_gemm_mfma_2x2", b"sllm_k_gemm_mfma_4x2"):
         assert k in blob
 
