@@ -13,6 +13,18 @@ before the timed region.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
+Beside the headline line the JSON carries:
+  block30  the decode GEMVs of 30 independently seeded 2B blocks, one launch;
+  decode   a random-init BitNet-b1.58-2B decode step (30 blocks, F16 output,
+           greedy argmax) after a 1024-position binary16 KV prefix, tokens/s
+           on the device's own token loop, its first token checked bit for bit
+           (logits, every int32 dot and activation) against the oracle, and the
+           reference's own sllm_forward timed on this host from the same
+           prefix (restored through its state file);
+  gemm     several tokens against one tensor (4, 16, 64 and the 512-token
+           prefill chunk) on int8 MFMA beside the GEMV path, with sampled
+           tokens checked against the oracle.
+
 Prints ONE JSON line. `value` is algorithmic bytes per step / wall time per
 step. `roofline` is the slab kernel, the step's only launch: its average
 launch duration is the time between two HIP events recorded on the library
@@ -168,6 +180,145 @@ def measure_block_plan(amd, dev, layers=30, steps=200):
             "frac_of_peak": round(total / (ev_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "steps": steps}
 
 
+# the decode workload: random-init BitNet-b1.58-2B, a 1024-position KV prefix
+# of binary16 N(0,1) values (held as f32, as the reference's cache holds it)
+DECODE_PREFIX = 1024
+
+
+def decode_prefix(amd, cfg, n_pos):
+    """K and V caches [layer][head_kv][pos][head_dim] of binary16 N(0,1)."""
+    hd = cfg["n_embd"] // cfg["n_head"]
+    shape = (cfg["n_layer"], cfg["n_head_kv"], n_pos, hd)
+    n = int(np.prod(shape))
+    k = amd.synth_normal_f16(amd.synth_seed(5, 0, 0, 1), n).view(np.float16).astype(np.float32).reshape(shape)
+    v = amd.synth_normal_f16(amd.synth_seed(5, 0, 0, 2), n).view(np.float16).astype(np.float32).reshape(shape)
+    return k, v
+
+
+def decode_bytes_per_token(cfg, npast):
+    """Algorithmic HBM bytes of one decode token: every I2_S matrix (codes and
+    tail), the F16 output projection, the norm weights, the K and V cache rows
+    attended (f32) and the new K / V rows written."""
+    e, f, L = cfg["n_embd"], cfg["n_ff"], cfg["n_layer"]
+    hd = e // cfg["n_head"]
+    gqa = hd * cfg["n_head_kv"]
+    i2s = L * ((2 * e * e + 2 * gqa * e + 3 * f * e) // 4 + 7 * 32)
+    lm = cfg["n_vocab"] * e * 2
+    norms = L * (3 * e + f) * 4 + e * 4
+    kv = L * 2 * cfg["n_head_kv"] * npast * hd * 4 + L * 2 * gqa * 4
+    return i2s + lm + norms + kv, {"i2s": i2s, "lm_head": lm, "norms": norms, "kv": kv}
+
+
+def measure_decode(amd, dev, tokens=128, warm=8):
+    """The decode step at BitNet-2B shape on the device's own greedy loop
+    (one HIP graph per token, the output kernel feeding the next token): the
+    first token after the prefix is traced for the CPU leg's bit-exact check,
+    then `warm` untimed and `tokens` timed tokens."""
+    cfg = dict(amd.BITNET_2B)
+    t0 = time.perf_counter()
+    model = amd.synth_model(cfg, 0)
+    k, v = decode_prefix(amd, cfg, DECODE_PREFIX)
+    g = amd.DeviceDecoder(dev, model, DECODE_PREFIX + 1 + warm + tokens + 8)
+    g.kv_load(k, v, DECODE_PREFIX)
+    log(f"decode model and {DECODE_PREFIX}-position prefix ready in {time.perf_counter() - t0:.1f}s")
+    tok0 = 128000 % cfg["n_vocab"]
+    g.trace_start()
+    logits0 = g.forward(tok0, DECODE_PREFIX)
+    dots0, acts0 = g.trace_read()
+    g.trace_stop()
+    g.set_graph(True)
+    g.generate([], warm)
+    dev.events(2)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.record(0)
+    ids = g.generate([], tokens)
+    dev.record(1)
+    wall = time.perf_counter() - t0
+    ms = dev.elapsed(0, 1)
+    g.close()
+    tok_s = tokens / (ms * 1e-3)
+    pos_first = DECODE_PREFIX + 1 + warm
+    npast_mean = pos_first + 1 + (tokens - 1) / 2
+    bpt, parts = decode_bytes_per_token(cfg, npast_mean)
+    check = {"model": model, "k": k, "v": v, "token": tok0, "logits": logits0, "dots": dots0, "acts": acts0,
+             "ids": [int(x) for x in ids[:8]]}
+    return check, {
+        "workload": (f"random-init BitNet-b1.58-2B (30 blocks, 2560/6912, 20x128 heads, 5 KV heads, F16 128256 x 2560 "
+                     f"output), KV cache of {DECODE_PREFIX} binary16 N(0,1) positions, greedy decode at positions "
+                     f"{pos_first}..{pos_first + tokens - 1}, batch 1, one HIP graph per token"),
+        "tokens_per_s": round(tok_s, 1), "us_per_token": round(ms * 1e3 / tokens, 1),
+        "wall_tokens_per_s": round(tokens / wall, 1), "tokens": tokens,
+        "bytes_per_token": int(bpt), "bytes_parts": {a: int(b) for a, b in parts.items()},
+        "effective_GBps": round(bpt * tok_s / 1e9, 1), "roofline_tokens_per_s": round(PEAK_HBM_GBS * 1e9 / bpt, 1),
+        "frac_of_roofline": round(tok_s * bpt / (PEAK_HBM_GBS * 1e9), 4),
+        "launches_per_token": 6 * cfg["n_layer"] + 2,
+    }
+
+
+PEAK_INT8_TOPS = 5000.0
+GEMM_SETS = 64
+
+
+def measure_gemm(amd, dev):
+    """Several tokens against one tensor: the int8-MFMA GEMM (q quantised
+    beforehand, timed alone) against the GEMV path (one plan of M jobs
+    sharing the tensor, each quantising its own token in-kernel), over
+    GEMM_SETS rotated weight sets (283 MB: HBM, not the Infinity Cache).
+    Token counts 4, 16, 64 at both FFN shapes, and the 512-token prefill
+    chunk at 6912 x 2560."""
+    rows, checks = [], []
+    for n_rows, k, ms in ((6912, 2560, (4, 16, 64, 512)), (2560, 6912, (4, 16, 64))):
+        ws = [amd.synth_i2s(amd.synth_seed(6, s_, n_rows, k), n_rows, k) for s_ in range(GEMM_SETS)]
+        bws = [dev.put(w) for w in ws]
+        for m in ms:
+            x = np.concatenate([amd.synth_normal(amd.synth_seed(6, 0, t, 77), k) for t in range(m)]).astype(np.float32)
+            bx, bq, ba = dev.put(x), dev.alloc(m * k), dev.alloc(8 * m)
+            by, bi = dev.alloc(4 * m * n_rows), dev.alloc(4 * m * n_rows)
+            dev.quant_act(bx.vp, k, m, bq.vp, ba.vp)
+            for i in range(GEMM_SETS):
+                dev.gemm(bws[i].vp, n_rows, k, bq.vp, ba.vp, m, by.vp)
+            dev.gemm(bws[0].vp, n_rows, k, bq.vp, ba.vp, m, by.vp, bi.vp)
+            dev.sync()
+            pick = sorted({0, m // 2, m - 1})
+            yd = by.download(np.float32, m * n_rows).reshape(m, n_rows)
+            dd = bi.download(np.int32, m * n_rows).reshape(m, n_rows)
+            checks.append((ws[0], n_rows, k, x, m, pick, yd[pick], dd[pick], f"gemm {n_rows}x{k} m={m}"))
+            dev.events(2)
+            reps = 4 * GEMM_SETS
+            dev.record(0)
+            for i in range(reps):
+                dev.gemm(bws[i % GEMM_SETS].vp, n_rows, k, bq.vp, ba.vp, m, by.vp)
+            dev.record(1)
+            mfma_us = dev.elapsed(0, 1) * 1e3 / reps
+            plans = [dev.plan([amd.GemvJob(bws[i].ptr, n_rows, k, bx.ptr + 4 * k * t, None, None, by.ptr + 4 * n_rows * t,
+                                           None) for t in range(m)]) for i in range(GEMM_SETS)]
+            for p in plans:
+                dev.plan_run(p)
+            dev.sync()
+            reps_g = 2 * GEMM_SETS
+            dev.record(0)
+            for i in range(reps_g):
+                dev.plan_run(plans[i % GEMM_SETS])
+            dev.record(1)
+            gemv_us = dev.elapsed(0, 1) * 1e3 / reps_g
+            for p in plans:
+                dev.plan_destroy(p)
+            for b in (bx, bq, ba, by, bi):
+                b.free()
+            ops = 2.0 * m * n_rows * k
+            byts = n_rows * k // 4 + 32 + m * k + 8 * m + 4 * m * n_rows
+            rows.append({"n_rows": n_rows, "k": k, "tokens": m, "mfma_us": round(mfma_us, 2),
+                         "mfma_TOPS": round(ops / mfma_us / 1e6, 1),
+                         "mfma_frac_int8_peak": round(ops / mfma_us / 1e6 / PEAK_INT8_TOPS, 4),
+                         "mfma_GBps": round(byts / mfma_us / 1e3, 1), "gemv_plan_us": round(gemv_us, 2),
+                         "faster": "mfma" if mfma_us < gemv_us else "gemv"})
+            log(f"gemm {n_rows}x{k} m={m}: mfma {mfma_us:.2f} us ({ops / mfma_us / 1e6:.1f} TOPS), gemv plan {gemv_us:.2f} us")
+        for b in bws:
+            b.free()
+    return checks, rows
+
+
 def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
     """Plain device copy and read-only checksum of known size: the achievable
     HBM figure beside the GEMV."""
@@ -188,6 +339,70 @@ def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
         b.free()
     return {"copy_GBps": round(2 * nbytes / copy_ms / 1e6, 1),
             "read_GBps": round(nbytes / read_ms / 1e6, 1), "bytes": nbytes}
+
+
+def cpu_decode(dec_check, seconds=10.0, threads=16):
+    """The decode checker and baseline. Checker: the oracle's decode step on
+    the same model and prefix at the same position -- logits, every int32
+    dot and every activation of the GPU's traced token, bit for bit. Baseline:
+    the reference's own sllm_forward (oracle/_ref) restored to the same
+    prefix through its state file (src/forward.c:963-1100), greedy decode
+    timed for about `seconds` on `threads` threads of this host."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    from oracle.gguf_synth import state_image
+    import tempfile
+    c = dec_check
+    model, cfg = c["model"], c["model"]["cfg"]
+    n_ctx = DECODE_PREFIX + 512
+    o = orc.Decoder(model, n_ctx)
+    ok, ov = o.caches()
+    ok[:, :, :DECODE_PREFIX] = c["k"]
+    ov[:, :, :DECODE_PREFIX] = c["v"]
+    want, wdots, wacts = o.forward(c["token"], DECODE_PREFIX, trace=True)
+    o.close()
+    bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)
+    if not (np.array_equal(bits(want), bits(c["logits"])) and np.array_equal(wdots, c["dots"])
+            and np.array_equal(wacts["sum"], c["acts"]["sum"]) and np.array_equal(bits(wacts["scale"]), bits(c["acts"]["scale"]))):
+        raise SystemExit("bench: the GPU decode step differs from the oracle")
+    log(f"decode at position {DECODE_PREFIX}: logits, {wdots.size} int32 dots and {wacts.size} activations "
+        f"match the oracle bit for bit")
+    if not orc.ref_available():
+        return {"checked": True, "cpu": None}
+    fd, path = tempfile.mkstemp(suffix=".slkv")
+    os.close(fd)
+    try:
+        with open(path, "wb") as f:
+            f.write(state_image(cfg, n_ctx, c["k"], c["v"], want))
+        r = orc.RefDecoder(model, n_ctx, threads=threads)
+        r.state_load(path)
+        tok, pos, n = int(c["token"]), DECODE_PREFIX, 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds and pos < n_ctx:
+            lg = r.forward(tok, pos)
+            tok = int(orc.ref().ref_argmax(orc._p(lg), lg.size))
+            pos += 1
+            n += 1
+        dt = time.perf_counter() - t0
+        r.close()
+    finally:
+        os.remove(path)
+    return {"checked": True, "cpu": {"tokens_per_s": round(n / dt, 2), "tokens": n, "seconds": round(dt, 1),
+                                     "threads": threads, "kind": "reference",
+                                     "sample": f"sllm_forward greedy from position {DECODE_PREFIX} after the same prefix"}}
+
+
+def cpu_gemm_check(checks):
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    n = 0
+    for w, n_rows, k, x, m, pick, yd, dd, what in checks:
+        for i, t in enumerate(pick):
+            yo, qo, do, so, su = orc.linear(w, n_rows, k, x[t * k:(t + 1) * k])
+            if not (np.array_equal(dd[i], do) and np.array_equal(yd[i].view(np.uint32), yo.view(np.uint32))):
+                raise SystemExit(f"bench: {what} token {t} differs from the oracle")
+            n += 1
+    log(f"{n} GEMM tokens (first, middle, last of every run) match the oracle bit for bit")
 
 
 def cpu_baseline(wl, checks, seconds=6.0):
@@ -335,6 +550,10 @@ def main():
     checks = wl.outputs([0, wl.sets - 1])
     block_checks, block30 = measure_block_plan(amd, dev)
     log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
+    dec_check, decode = measure_decode(amd, dev)
+    log(f"decode: {decode['tokens_per_s']} tokens/s ({decode['us_per_token']} us per token, "
+        f"{decode['effective_GBps']} GB/s effective)")
+    gemm_checks, gemm = measure_gemm(amd, dev)
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -358,10 +577,16 @@ def main():
         },
         "calibration": calib,
         "block30": block30,
+        "decode": decode,
+        "gemm": gemm,
     }
     if not args.no_cpu:
         log("timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks, args.cpu_seconds)
+        cpu_gemm_check(gemm_checks)
+        dec = cpu_decode(dec_check, seconds=args.cpu_seconds)
+        out["decode"]["parity"] = "logits, int32 dots and activations of the first token bit-identical to the oracle"
+        out["decode"]["cpu_baseline"] = dec["cpu"]
     print(json.dumps(out), flush=True)
 
 

@@ -1,4 +1,5 @@
-"""A GGUF v3 image of a synthetic BitNet-b1.58 model -- TEST INFRASTRUCTURE.
+"""A GGUF v3 image of a synthetic BitNet-b1.58 model, and a state file of a
+KV-cache prefix -- TEST INFRASTRUCTURE.
 
 Packs the arrays of a model dict (saphira_llm_amd.synth_model) into the
 container the reference loads (FORMAT.md:9-117 there): header, metadata,
@@ -79,3 +80,20 @@ def gguf_image(model, ctx_train=4096):
     meta = head + b"".join(table)
     meta += b"\0" * ((-len(meta)) % ALIGN)
     return meta + b"".join(blobs)
+
+
+STATE_MAGIC, STATE_VERSION = 0x564B4C53, 1
+
+
+def state_image(cfg, n_ctx, k, v, logits):
+    """bytes of a state file in the layout src/forward.c:963-1036 reads and
+    writes: magic, version, n_layer, n_ctx, n_head_kv, head dim, n_past,
+    n_vocab, then per layer and KV head the live K rows then the live V rows,
+    then the last position's logits. k / v: [n_layer][n_head_kv][n_past][hd]."""
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    n_layer, n_kv, n_past, hd = k.shape
+    head = struct.pack("<IIiiiiii", STATE_MAGIC, STATE_VERSION, n_layer, n_ctx, n_kv, hd, n_past,
+                       cfg["n_vocab"])
+    body = b"".join(k[il, h].tobytes() + v[il, h].tobytes() for il in range(n_layer) for h in range(n_kv))
+    return head + body + np.ascontiguousarray(logits, np.float32).tobytes()

@@ -99,6 +99,7 @@ _REF_PROTOS = {
     "ref_ctx_set_pool": (None, [c_void_p, c_void_p]),
     "ref_forward": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "ref_argmax": (c_int32, [c_void_p, c_int32]),
+    "ref_state_load": (c_int, [c_void_p, c_void_p, ctypes.c_char_p]),
 }
 
 # the reference's ISA levels as passed to sllm_i2s_select_level
@@ -355,6 +356,12 @@ class RefDecoder:
         if self.pool:
             ref().ref_ctx_set_pool(self.c, self.pool)
         self.n_vocab = model["cfg"]["n_vocab"]
+
+    def state_load(self, path):
+        """sllm_state_load: the cache prefix and last logits from a state file."""
+        st = ref().ref_state_load(self.r, self.c, path.encode())
+        if st != 0:
+            raise ValueError(f"sllm_state_load: status {st}")
 
     def forward(self, token, pos):
         logits = np.empty(self.n_vocab, np.float32)

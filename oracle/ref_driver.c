@@ -124,3 +124,8 @@ int ref_forward(ref_model *r, sllm_ctx *c, int32_t token, int32_t pos, float *lo
 /* defined in src/forward.c:876-883 without a header declaration */
 int32_t sllm_argmax(const float *logits, int32_t n);
 int32_t ref_argmax(const float *logits, int32_t n) { return sllm_argmax(logits, n); }
+
+/* src/forward.c:1038-1100: restore a saved cache and the last logits */
+int ref_state_load(ref_model *r, sllm_ctx *c, const char *path) {
+    return (int) sllm_state_load(r->model, c, path);
+}

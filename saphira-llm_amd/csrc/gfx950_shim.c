@@ -936,7 +936,7 @@ int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
         return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m = %zu too large", m);
     }
     int tile = g.force_gemm_tile - 1;
-    if (tile < 0) tile = m <= 16 ? 0 : (m <= 32 ? 1 : 2);
+    if (tile < 0) tile = m <= 64 ? 0 : 2;      /* split-K tiles up to 64 tokens (the measured crossover) */
     const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];
     const uint64_t gx = (n_rows + rows_per_wg - 1) / rows_per_wg, gy = (m + tok_per_wg - 1) / tok_per_wg;
     if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");

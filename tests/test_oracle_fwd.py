@@ -250,3 +250,32 @@ def test_decode_step_at_bitnet_2b_widths(amd, orc):
     finally:
         d.close()
         r.close()
+
+
+@needs_ref
+def test_state_file_restores_the_reference_cache(amd, orc, tmp_path):
+    """A cache prefix handed to the reference through its own state file
+    (src/forward.c:963-1100) and the same prefix written into the oracle's
+    cache: the next tokens' logits agree bit for bit -- the layout both use,
+    [layer][head_kv][pos][head_dim], and the position after the prefix."""
+    from oracle.gguf_synth import state_image
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 13)
+    rng = np.random.default_rng(14)
+    hd = cfg["n_embd"] // cfg["n_head"]
+    shape = (cfg["n_layer"], cfg["n_head_kv"], 100, hd)
+    k = rng.standard_normal(shape).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal(shape).astype(np.float16).astype(np.float32)
+    path = tmp_path / "prefix.slkv"
+    path.write_bytes(state_image(cfg, 128, k, v, np.zeros(cfg["n_vocab"], np.float32)))
+    r, d = orc.RefDecoder(model, 128, threads=2), orc.Decoder(model, 128)
+    try:
+        r.state_load(str(path))
+        ok, ov = d.caches()
+        ok[:, :, :100] = k
+        ov[:, :, :100] = v
+        for i, tok in enumerate(_tokens(4, cfg["n_vocab"], 15)):
+            assert np.array_equal(bits(r.forward(tok, 100 + i)), bits(d.forward(tok, 100 + i))), i
+    finally:
+        r.close()
+        d.close()
