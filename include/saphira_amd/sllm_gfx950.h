@@ -205,7 +205,8 @@ int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const fl
                              int8_t *q, sllm_gfx950_act *act, float *out, int32_t *rows_out);
 
 /* GEMM tile override for tuning and tests: 0 automatic (by m), 1: 16 tokens
- * x 16 rows per workgroup (K split over its waves), 2: 32 x 128, 3: 64 x 128. */
+ * x 16 rows per workgroup (K split over its waves), 2: 32 x 128, 3: 64 x 128,
+ * 4: 128 x 128 staged through LDS (K % 256 == 0; tile 3 otherwise). */
 int sllm_gfx950_set_gemm_tile(int tile);
 
 /* Launch-geometry override for tuning sweeps and tests; affects launches

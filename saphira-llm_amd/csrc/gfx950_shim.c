@@ -118,7 +118,7 @@ static struct {
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
-    hipFunction_t  k_gemm[3];
+    hipFunction_t  k_gemm[4];
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -188,6 +188,7 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[0], g.mod, "sllm_k_gemm_mfma_s1x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[1], g.mod, "sllm_k_gemm_mfma_2x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[2], g.mod, "sllm_k_gemm_mfma_4x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[3], g.mod, "sllm_k_gemm_mfma_l128"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
@@ -914,11 +915,12 @@ typedef struct k_gemm_args {
 _Static_assert(sizeof(k_gemm_args) == 56, "k_gemm_args must match gemm_args in i2s_kernels.hip");
 
 /* tile shapes per workgroup: tokens x rows (shape 0 splits K over its four
- * waves instead of spreading them along the rows) */
-static const uint32_t k_gemm_tokens[3] = { 16, 32, 64 }, k_gemm_rows[3] = { 16, 128, 128 };
+ * waves instead of spreading them along the rows; shape 3 stages its tile
+ * through LDS and needs K % 256 == 0) */
+static const uint32_t k_gemm_tokens[4] = { 16, 32, 64, 128 }, k_gemm_rows[4] = { 16, 128, 128, 128 };
 
 int sllm_gfx950_set_gemm_tile(int tile) {
-    if (tile < 0 || tile > 3) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. 3");
+    if (tile < 0 || tile > 4) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. 4");
     g.force_gemm_tile = tile;
     return SLLM_GFX950_OK;
 }
@@ -936,7 +938,14 @@ int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
         return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m = %zu too large", m);
     }
     int tile = g.force_gemm_tile - 1;
-    if (tile < 0) tile = m <= 64 ? 0 : 2;      /* split-K tiles up to 64 tokens (the measured crossover) */
+    if (tile < 0) {
+        /* measured on MI355X: split-K tiles win up to 32 tokens, and up to 64
+         * when the LDS tile's grid would be small (n_rows < 4096); the LDS
+         * tile wins above */
+        if (m <= 32 || (m <= 64 && n_rows < 4096)) tile = 0;
+        else tile = n % 256 == 0 ? 3 : 2;
+    }
+    if (tile == 3 && n % 256 != 0) tile = 2;
     const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];
     const uint64_t gx = (n_rows + rows_per_wg - 1) / rows_per_wg, gy = (m + tok_per_wg - 1) / tok_per_wg;
     if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");

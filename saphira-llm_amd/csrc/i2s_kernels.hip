@@ -427,6 +427,132 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
     }
 }
 
+
+// Large token counts (the prefill chunk): the workgroup stages its tile
+// through LDS so that each byte of the token rows and of the packed weights
+// enters it once, not once per wave. 128 tokens x 128 rows per workgroup,
+// four waves of 64 x 64 (16 MFMAs per k step); K moves in chunks of 256,
+// double-buffered in LDS, with the global loads two chunks ahead in
+// registers. LDS rows are padded (272 bytes per token, 80 per weight row)
+// so that the 16-byte operand reads of a lane group spread over the banks.
+// K must be a multiple of 256.
+constexpr uint32_t GL_BM = 128, GL_BN = 128, GL_BK = 256;
+constexpr uint32_t GL_QS = GL_BK + 16, GL_WS = GL_BK / 4 + 16;
+constexpr int GL_QLOADS = (int) (GL_BM * GL_BK / 16 / 256);
+constexpr int GL_WLOADS = (int) (GL_BN * GL_BK / 4 / 16 / 256);
+
+struct gl_shared {
+    uint8_t q[2][GL_BM * GL_QS];
+    uint8_t w[2][GL_BN * GL_WS];
+};
+
+__device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
+    __shared__ __attribute__((aligned(16))) gl_shared S;
+    const uint32_t tid = threadIdx.x;
+    const int lane = (int) (tid & 63), g = lane >> 4, li = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t t0 = blockIdx.y * GL_BM, n0 = blockIdx.x * GL_BN;
+    const uint32_t wt = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
+    const uint32_t chunks = G.k / GL_BK, kb = G.k >> 2;
+    auto gload = [&](uint32_t c, u32x4 (&q)[GL_QLOADS], u32x4 (&w)[GL_WLOADS]) {
+        const uint32_t cc = min(c, chunks - 1);
+#pragma unroll
+        for (int u = 0; u < GL_QLOADS; ++u) {
+            const uint32_t p = tid + 256u * (uint32_t) u, tok = p / 16u, off = (p % 16u) * 16u;
+            const uint32_t t = min(t0 + tok, G.m - 1);
+            q[u] = *G_CAST(const u32x4, G.q + (size_t) t * G.k + cc * GL_BK + off);
+        }
+#pragma unroll
+        for (int u = 0; u < GL_WLOADS; ++u) {
+            const uint32_t p = tid + 256u * (uint32_t) u, row = p / 4u, off = (p % 4u) * 16u;
+            const uint32_t n = min(n0 + row, G.n_rows - 1);
+            w[u] = __builtin_nontemporal_load(G_CAST(const u32x4, G.w + (size_t) n * kb + cc * (GL_BK / 4) + off));
+        }
+    };
+    auto lstore = [&](int buf, const u32x4 (&q)[GL_QLOADS], const u32x4 (&w)[GL_WLOADS]) {
+#pragma unroll
+        for (int u = 0; u < GL_QLOADS; ++u) {
+            const uint32_t p = tid + 256u * (uint32_t) u, tok = p / 16u, off = (p % 16u) * 16u;
+            *reinterpret_cast<u32x4 *>(&S.q[buf][tok * GL_QS + off]) = q[u];
+        }
+#pragma unroll
+        for (int u = 0; u < GL_WLOADS; ++u) {
+            const uint32_t p = tid + 256u * (uint32_t) u, row = p / 4u, off = (p % 4u) * 16u;
+            *reinterpret_cast<u32x4 *>(&S.w[buf][row * GL_WS + off]) = w[u];
+        }
+    };
+    i32x4v c[4][4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
+    }
+    const uint32_t shift = 6u - 2u * (uint32_t) g;
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int ks = 0; ks < (int) (GL_BK / 64); ++ks) {
+            const uint32_t blk = (uint32_t) ks >> 1, h = (uint32_t) ks & 1u;
+            i32x4v a[4], b[4];
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+                const uint32_t row = wt + 16u * (uint32_t) tm + (uint32_t) li;
+                a[tm] = *reinterpret_cast<const i32x4v *>(&S.q[buf][row * GL_QS + 128u * blk + 32u * (uint32_t) g + 16u * h]);
+            }
+#pragma unroll
+            for (int tn = 0; tn < 4; ++tn) {
+                const uint32_t row = wn + 16u * (uint32_t) tn + (uint32_t) li;
+                const u32x4 raw = *reinterpret_cast<const u32x4 *>(&S.w[buf][row * GL_WS + 32u * blk + 16u * h]);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) b[tn][d] = (int32_t) ((raw[d] >> shift) & 0x03030303u);
+            }
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn) c[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[tm], b[tn], c[tm][tn], 0, 0, 0);
+            }
+        }
+    };
+    u32x4 q0[GL_QLOADS], w0[GL_WLOADS], q1[GL_QLOADS], w1[GL_WLOADS];
+    gload(0, q0, w0);
+    gload(1, q1, w1);
+    lstore(0, q0, w0);
+    __syncthreads();
+    // chunk ch computes from LDS buffer ch & 1; register set ch & 1 is
+    // refilled with chunk ch + 2 while it runs
+    for (uint32_t ch = 0; ch < chunks; ch += 2) {
+        gload(ch + 2, q0, w0);
+        compute(0);
+        lstore(1, q1, w1);
+        __syncthreads();
+        if (ch + 1 >= chunks) break;
+        gload(ch + 3, q1, w1);
+        compute(1);
+        lstore(0, q0, w0);
+        __syncthreads();
+    }
+
+    const float ws = *G_CAST(const float, G.w + (size_t) G.n_rows * kb);
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t t = t0 + wt + 16u * (uint32_t) tm + 4u * (uint32_t) g + (uint32_t) r;
+            if (t >= G.m) continue;
+            const act_t at = G.act != nullptr ? G.act[t] : act_t { 1.0f, 0 };
+            const float post = ws / at.scale;
+#pragma unroll
+            for (int tn = 0; tn < 4; ++tn) {
+                const uint32_t n = n0 + wn + 16u * (uint32_t) tn + (uint32_t) li;
+                if (n < G.n_rows) {
+                    const int32_t d = c[tm][tn][r];
+                    if (G.out_i != nullptr) G_CAST(int32_t, G.out_i)[(size_t) t * G.n_rows + n] = d;
+                    if (G.out != nullptr) G_CAST(float, G.out)[(size_t) t * G.n_rows + n] = (float) (d - at.sum) * post;
+                }
+            }
+        }
+    }
+}
+
 } // namespace
 
 // ---------------------------------------------------------------------------
@@ -512,12 +638,15 @@ SLLM_STREAM_ENTRY(16)
 // instantiation per tile shape the host picks by token count:
 //   _s1x1  16 tokens x 16 rows, K split over the four waves
 //   _2x2   32 tokens x 128 rows      _4x2   64 tokens x 128 rows
+//   _l128  128 tokens x 128 rows staged through LDS (K % 256 == 0)
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_s1x1(gemm_args G) { gemm_block<1, 1, 4>(G); }
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_2x2(gemm_args G) { gemm_block<2, 2, 1>(G); }
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_4x2(gemm_args G) { gemm_block<4, 2, 1>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_mfma_l128(gemm_args G) { gemm_lds_block(G); }
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

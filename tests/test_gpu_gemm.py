@@ -65,7 +65,7 @@ def test_gemm_matches_the_oracle_token_by_token(amd, orc, dev, n_rows, n, m):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"{n_rows}x{n} m={m}")
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
 def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     n_rows, n, m = 640, 2560, 37
     w, x = _case(amd, 2, n_rows, n, m)
@@ -106,7 +106,7 @@ def test_gemm_refuses_bad_arguments(amd, dev):
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, None, 2, o.vp, None) == -1     # epilogue without act
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 2, None, None) == -1     # no output
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 0, o.vp, None) == 0      # nothing to do
-        assert lib.sllm_gfx950_set_gemm_tile(4) == -1
+        assert lib.sllm_gfx950_set_gemm_tile(5) == -1
     finally:
         for b in (w, q, a, o):
             b.free()
