@@ -209,7 +209,7 @@ def decode_bytes_per_token(cfg, npast):
     return i2s + lm + norms + kv, {"i2s": i2s, "lm_head": lm, "norms": norms, "kv": kv}
 
 
-def measure_decode(amd, dev, tokens=128, warm=8):
+def measure_decode(amd, dev, tokens=128, warm=8, graph=True):
     """The decode step at BitNet-2B shape on the device's own greedy loop
     (one HIP graph per token, the output kernel feeding the next token): the
     first token after the prefix is traced for the CPU leg's bit-exact check,
@@ -226,7 +226,7 @@ def measure_decode(amd, dev, tokens=128, warm=8):
     logits0 = g.forward(tok0, DECODE_PREFIX)
     dots0, acts0 = g.trace_read()
     g.trace_stop()
-    g.set_graph(True)
+    g.set_graph(graph)
     g.generate([], warm)
     dev.events(2)
     dev.sync()
@@ -246,7 +246,8 @@ def measure_decode(amd, dev, tokens=128, warm=8):
     return check, {
         "workload": (f"random-init BitNet-b1.58-2B (30 blocks, 2560/6912, 20x128 heads, 5 KV heads, F16 128256 x 2560 "
                      f"output), KV cache of {DECODE_PREFIX} binary16 N(0,1) positions, greedy decode at positions "
-                     f"{pos_first}..{pos_first + tokens - 1}, batch 1, one HIP graph per token"),
+                     f"{pos_first}..{pos_first + tokens - 1}, batch 1, "
+                     + ("one HIP graph per token" if graph else "the token's launches enqueued one by one")),
         "tokens_per_s": round(tok_s, 1), "us_per_token": round(ms * 1e3 / tokens, 1),
         "wall_tokens_per_s": round(tokens / wall, 1), "tokens": tokens,
         "bytes_per_token": int(bpt), "bytes_parts": {a: int(b) for a, b in parts.items()},
@@ -502,6 +503,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="decode leg: enqueue each token's launches instead of replaying a HIP graph "
+                         "(rocprofv3's kernel tracer does not survive graph replay)")
+    ap.add_argument("--legs", default="gemv,block,decode,gemm",
+                    help="comma-separated legs to run beside the headline GEMV (block, decode, gemm); "
+                         "for profiling one leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the I2_S GEMV path runs on a single MI355X and "
@@ -548,12 +555,17 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     checks = wl.outputs([0, wl.sets - 1])
-    block_checks, block30 = measure_block_plan(amd, dev)
-    log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
-    dec_check, decode = measure_decode(amd, dev)
-    log(f"decode: {decode['tokens_per_s']} tokens/s ({decode['us_per_token']} us per token, "
-        f"{decode['effective_GBps']} GB/s effective)")
-    gemm_checks, gemm = measure_gemm(amd, dev)
+    legs = set(args.legs.split(","))
+    block_checks, block30, dec_check, decode, gemm_checks, gemm = [], None, None, None, [], None
+    if "block" in legs:
+        block_checks, block30 = measure_block_plan(amd, dev)
+        log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
+    if "decode" in legs:
+        dec_check, decode = measure_decode(amd, dev, graph=not args.no_graph)
+        log(f"decode: {decode['tokens_per_s']} tokens/s ({decode['us_per_token']} us per token, "
+            f"{decode['effective_GBps']} GB/s effective)")
+    if "gemm" in legs:
+        gemm_checks, gemm = measure_gemm(amd, dev)
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -584,9 +596,10 @@ def main():
         log("timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks, args.cpu_seconds)
         cpu_gemm_check(gemm_checks)
-        dec = cpu_decode(dec_check, seconds=args.cpu_seconds)
-        out["decode"]["parity"] = "logits, int32 dots and activations of the first token bit-identical to the oracle"
-        out["decode"]["cpu_baseline"] = dec["cpu"]
+        if dec_check is not None:
+            dec = cpu_decode(dec_check, seconds=args.cpu_seconds)
+            out["decode"]["parity"] = "logits, int32 dots and activations of the first token bit-identical to the oracle"
+            out["decode"]["cpu_baseline"] = dec["cpu"]
     print(json.dumps(out), flush=True)
 
 
