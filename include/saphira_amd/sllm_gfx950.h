@@ -47,7 +47,18 @@ enum {
     SLLM_GFX950_OK                 = 0,
     SLLM_GFX950_ERR_ARG            = -1,   /* SLLM_ERR_ARG                          */
     SLLM_GFX950_ERR_NOMEM          = -2,   /* SLLM_ERR_NOMEM (host or device)       */
+    SLLM_GFX950_ERR_IO             = -3,   /* SLLM_ERR_IO: a model file unreadable  */
     SLLM_GFX950_ERR_UNSUPPORTED    = -4,   /* SLLM_ERR_UNSUPPORTED                  */
+    SLLM_GFX950_ERR_GGUF_MAGIC     = -10,  /* SLLM_ERR_GGUF_MAGIC: not a GGUF file  */
+    SLLM_GFX950_ERR_GGUF_VERSION   = -11,  /* SLLM_ERR_GGUF_VERSION: not version 3  */
+    SLLM_GFX950_ERR_GGUF_TRUNCATED = -12,  /* SLLM_ERR_GGUF_TRUNCATED               */
+    SLLM_GFX950_ERR_GGUF_TYPE      = -14,  /* SLLM_ERR_GGUF_TYPE: bad value type    */
+    SLLM_GFX950_ERR_GGUF_TENSOR    = -15,  /* SLLM_ERR_GGUF_TENSOR: bad descriptor  */
+    SLLM_GFX950_ERR_GGUF_ALIGNMENT = -16,  /* SLLM_ERR_GGUF_ALIGNMENT               */
+    SLLM_GFX950_ERR_GGUF_LAYOUT    = -17,  /* SLLM_ERR_GGUF_LAYOUT: extent / overlap */
+    SLLM_GFX950_ERR_GGUF_KEYDUP    = -18,  /* SLLM_ERR_GGUF_KEYDUP                  */
+    SLLM_GFX950_ERR_ARCH           = -30,  /* SLLM_ERR_ARCH_UNSUPPORTED             */
+    SLLM_GFX950_ERR_KV_MISSING     = -31,  /* SLLM_ERR_KV_MISSING (or mistyped)     */
     SLLM_GFX950_ERR_TENSOR_SHAPE   = -34,  /* SLLM_ERR_TENSOR_SHAPE: K % 128 != 0   */
     SLLM_GFX950_ERR_TOO_LARGE      = -36,  /* SLLM_ERR_TOO_LARGE: K above the limit */
     SLLM_GFX950_ERR_NO_DEVICE      = -60,  /* no gfx950 device, or library not open */

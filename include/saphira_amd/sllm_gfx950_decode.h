@@ -67,6 +67,30 @@ int  sllm_gfx950_model_upload(const sllm_gfx950_model_desc *desc, sllm_gfx950_mo
 void sllm_gfx950_model_free(sllm_gfx950_model *m);
 
 /*
+ * sllm_gguf_open_memory (include/saphira_llm/gguf.h:144) followed by
+ * sllm_model_load (forward.h:32), then sllm_gfx950_model_upload: a GGUF v3
+ * image of a bitnet-b1.58 model in host memory onto the device. The image is
+ * read in place and may be freed afterwards. A file is accepted or refused
+ * as the reference accepts or refuses it, with its status: the container
+ * (SLLM_GFX950_ERR_GGUF_*, SLLM_GFX950_ERR_TOO_LARGE past the reference's
+ * count and length limits), then the model (SLLM_GFX950_ERR_ARCH,
+ * SLLM_GFX950_ERR_KV_MISSING for an absent or mistyped hyper-parameter,
+ * SLLM_GFX950_ERR_TENSOR_SHAPE for an absent or misshapen tensor); then the
+ * kernel limits of sllm_gfx950_model_upload.
+ */
+int  sllm_gfx950_model_load_gguf(const void *image, size_t size, sllm_gfx950_model **out);
+/* The same from a file, mapped read-only (sllm_gguf_open, gguf.h:141);
+ * SLLM_GFX950_ERR_IO if it cannot be opened or mapped, TRUNCATED if empty. */
+int  sllm_gfx950_model_load_gguf_file(const char *path, sllm_gfx950_model **out);
+/*
+ * The host half of sllm_gfx950_model_load_gguf, needing no device: parse and
+ * check the image and fill `desc` with pointers into it; layers must hold 64
+ * entries (the reference's SLLM_LAYER_MAX, src/forward.c:45).
+ */
+int  sllm_gfx950_gguf_describe(const void *image, size_t size, sllm_gfx950_model_desc *desc,
+                               sllm_gfx950_layer_desc *layers);
+
+/*
  * sllm_ctx_new (forward.h:46): a KV cache of n_ctx positions
  * ([layer][head_kv][pos][head_dim] f32, as src/forward.c:466-518) and the
  * activations, all on the device, plus the RoPE table for positions

@@ -117,6 +117,9 @@ PROTOTYPES = {
     "sllm_gfx950_set_gemm_tile": (c_int, [c_int]),
     "sllm_gfx950_model_upload": (c_int, [POINTER(ModelDesc), POINTER(c_void_p)]),
     "sllm_gfx950_model_free": (None, [c_void_p]),
+    "sllm_gfx950_model_load_gguf": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),
+    "sllm_gfx950_model_load_gguf_file": (c_int, [c_char_p, POINTER(c_void_p)]),
+    "sllm_gfx950_gguf_describe": (c_int, [c_void_p, c_size_t, POINTER(ModelDesc), POINTER(LayerDesc)]),
     "sllm_gfx950_ctx_new": (c_int, [c_void_p, c_int32, POINTER(c_void_p)]),
     "sllm_gfx950_ctx_free": (None, [c_void_p]),
     "sllm_gfx950_ctx_reset": (c_int, [c_void_p]),
@@ -426,18 +429,56 @@ def model_desc(model):
     return d, keep
 
 
-class DeviceDecoder:
-    """A model uploaded with sllm_gfx950_model_upload and one context of
-    n_ctx positions (sllm_gfx950_ctx_new): the decode step on the GPU."""
+GGUF_MAX_LAYERS = 64
 
-    def __init__(self, dev, model, n_ctx):
+
+def gguf_describe(image):
+    """(status, cfg, tensors) of a GGUF image read by sllm_gfx950_gguf_describe
+    (no device needed): cfg holds the hyper-parameters, tensors maps
+    "tok_embd", "output_norm" and (layer, name) to the byte offset in the
+    image where that tensor's data starts. cfg and tensors are None unless
+    the status is 0."""
+    n = len(image)
+    buf = np.frombuffer(image, np.uint8) if n else np.zeros(1, np.uint8)
+    d = ModelDesc()
+    layers = (LayerDesc * GGUF_MAX_LAYERS)()
+    st = lib().sllm_gfx950_gguf_describe(ptr(buf), n, ctypes.byref(d), layers)
+    if st != 0:
+        return st, None, None
+    base = buf.ctypes.data
+    cfg = {"n_layer": d.n_layer, "n_embd": d.n_embd, "n_ff": d.n_ff, "n_head": d.n_head,
+           "n_head_kv": d.n_head_kv, "n_rot": d.n_rot, "n_vocab": d.n_vocab, "eps": d.eps,
+           "rope_base": d.rope_base}
+    tensors = {"tok_embd": d.tok_embd - base, "output_norm": d.output_norm - base}
+    for il in range(d.n_layer):
+        for name in LAYER_I2S + LAYER_NORMS:
+            tensors[(il, name)] = getattr(layers[il], name) - base
+    return st, cfg, tensors
+
+
+class DeviceDecoder:
+    """A model uploaded with sllm_gfx950_model_upload (or, gguf given, read
+    from a GGUF image -- bytes -- or file -- a path -- with
+    sllm_gfx950_model_load_gguf[_file]) and one context of n_ctx positions
+    (sllm_gfx950_ctx_new): the decode step on the GPU."""
+
+    def __init__(self, dev, model, n_ctx, gguf=None):
         self.dev = dev
-        self.cfg = dict(model["cfg"])
         L = lib()
-        d, keep = model_desc(model)
         m = c_void_p()
-        check(L.sllm_gfx950_model_upload(ctypes.byref(d), ctypes.byref(m)), "model_upload")
-        del keep
+        if isinstance(gguf, (str, os.PathLike)):
+            check(L.sllm_gfx950_model_load_gguf_file(os.fsencode(gguf), ctypes.byref(m)), "model_load_gguf_file")
+            with open(gguf, "rb") as fh:
+                self.cfg = gguf_describe(fh.read())[1]
+        elif gguf is not None:
+            buf = np.frombuffer(gguf, np.uint8)
+            check(L.sllm_gfx950_model_load_gguf(ptr(buf), buf.size, ctypes.byref(m)), "model_load_gguf")
+            self.cfg = gguf_describe(gguf)[1]
+        else:
+            self.cfg = dict(model["cfg"])
+            d, keep = model_desc(model)
+            check(L.sllm_gfx950_model_upload(ctypes.byref(d), ctypes.byref(m)), "model_upload")
+            del keep
         self.m = m
         c = c_void_p()
         st = L.sllm_gfx950_ctx_new(m, n_ctx, ctypes.byref(c))

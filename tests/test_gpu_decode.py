@@ -234,6 +234,37 @@ def test_reset_gives_a_fresh_context(amd, orc, dev):
         g.close()
 
 
+def test_a_gguf_model_decodes_like_the_uploaded_one(amd, orc, dev, tmp_path):
+    """sllm_gfx950_model_load_gguf (an image) and _file (a path) on the GGUF
+    the reference loads: logits bit for bit with the oracle, and greedy
+    tokens the same as the uploaded model's."""
+    from oracle import gguf_synth
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 61)
+    toks = _tokens(8, cfg["n_vocab"], 62)
+    _plant_subnormals(model, toks)
+    image = gguf_synth.gguf_image(model)
+    path = tmp_path / "tiny.gguf"
+    path.write_bytes(image)
+    print("[decode] gguf image and file", flush=True)
+    a = amd.DeviceDecoder(dev, None, 24, gguf=image)
+    b = amd.DeviceDecoder(dev, None, 24, gguf=str(path))
+    u = amd.DeviceDecoder(dev, model, 24)
+    o = orc.Decoder(model, 24)
+    try:
+        assert a.cfg["n_layer"] == 2 and b.cfg["n_vocab"] == cfg["n_vocab"]
+        for pos, t in enumerate(toks):
+            want = o.forward(t, pos)
+            for g, label in ((a, "image"), (b, "file")):
+                assert np.array_equal(bits(g.forward(t, pos)), bits(want)), f"{label}: logits differ at pos {pos}"
+        a.reset()
+        u.reset()
+        assert np.array_equal(a.generate(toks[:3], 10), u.generate(toks[:3], 10))
+    finally:
+        for g in (a, b, u, o):
+            g.close()
+
+
 def test_full_2b_decode_is_bit_exact(amd, orc, dev):
     """All 30 blocks at BitNet-2B shape with the 128256-row F16 output: every
     int32 accumulator, every activation and the logits of three tokens."""
