@@ -55,6 +55,9 @@ typedef struct sllm_gfx950_ctx   sllm_gfx950_ctx;
 #define SLLM_GFX950_DEC_MAX_GQA      4
 #define SLLM_GFX950_DEC_MAX_WIDTH    7168
 #define SLLM_GFX950_DEC_MAX_GQA_CTX  16384
+/* Most tokens in one sllm_gfx950_forward_chunk (the reference's
+ * SLLM_MAX_CHUNK, include/saphira_llm/forward.h:90, is 256). */
+#define SLLM_GFX950_DEC_MAX_CHUNK    512
 
 /*
  * sllm_model_load (forward.h:33) for the device: copies every tensor of
@@ -113,6 +116,30 @@ int32_t sllm_gfx950_ctx_n_past(const sllm_gfx950_ctx *c);
  */
 int  sllm_gfx950_forward(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, int32_t token, int32_t pos,
                          float *logits);
+
+/*
+ * sllm_forward_chunk (forward.h:93-109): n tokens as one chunk at positions
+ * base .. base + n - 1, every projection one int8-MFMA GEMM over the n
+ * quantised rows, with the logits of the token-by-token path bit for bit
+ * (src/forward.c:589-835; tests/test_phase5.c:85-150). Refused as the
+ * reference refuses it: n < 1 or n > SLLM_GFX950_DEC_MAX_CHUNK, base <
+ * n_past, base + n > n_ctx, a token out of range -> SLLM_GFX950_ERR_ARG.
+ * logits: n * n_vocab floats of host memory (row t for token t), or NULL
+ * to compute the last token's logits only and leave them on the device. The
+ * last token's logits and argmax are kept as after sllm_gfx950_forward. n = 1
+ * runs the decode step.
+ */
+int  sllm_gfx950_forward_chunk(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *tokens,
+                               int32_t n, int32_t base, float *logits);
+
+/*
+ * sllm_forward_prefill_chunked (forward.h:111-113, src/forward.c:846-868):
+ * tokens 0 .. n - 1 at positions 0 .. n - 1 in chunks of `chunk`; logits:
+ * n * n_vocab floats or NULL. chunk < 1 or above the limit ->
+ * SLLM_GFX950_ERR_ARG; n > n_ctx -> SLLM_GFX950_ERR_TOO_LARGE.
+ */
+int  sllm_gfx950_forward_prefill_chunked(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *tokens,
+                                         int32_t n, int32_t chunk, float *logits);
 
 /*
  * sllm_generate_greedy (forward.h:124): forward the prompt, then n_new

@@ -100,6 +100,8 @@ _REF_PROTOS = {
     "ref_forward": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "ref_argmax": (c_int32, [c_void_p, c_int32]),
     "ref_state_load": (c_int, [c_void_p, c_void_p, ctypes.c_char_p]),
+    "ref_forward_chunk": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "ref_prefill_chunked": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
 }
 
 # the reference's ISA levels as passed to sllm_i2s_select_level
@@ -368,6 +370,24 @@ class RefDecoder:
         st = ref().ref_forward(self.r, self.c, token, pos, _p(logits))
         if st != 0:
             raise ValueError(f"sllm_forward: status {st}")
+        return logits
+
+    def forward_chunk(self, tokens, base):
+        """sllm_forward_chunk: logits [n][n_vocab] of n tokens at base.."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty((t.size, self.n_vocab), np.float32)
+        st = ref().ref_forward_chunk(self.r, self.c, _p(t), t.size, base, _p(logits))
+        if st != 0:
+            raise ValueError(f"sllm_forward_chunk: status {st}")
+        return logits
+
+    def prefill_chunked(self, tokens, chunk):
+        """sllm_forward_prefill_chunked: logits [n][n_vocab]."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty((t.size, self.n_vocab), np.float32)
+        st = ref().ref_prefill_chunked(self.r, self.c, _p(t), t.size, chunk, _p(logits))
+        if st != 0:
+            raise ValueError(f"sllm_forward_prefill_chunked: status {st}")
         return logits
 
     def close(self):

@@ -129,3 +129,12 @@ int32_t ref_argmax(const float *logits, int32_t n) { return sllm_argmax(logits, 
 int ref_state_load(ref_model *r, sllm_ctx *c, const char *path) {
     return (int) sllm_state_load(r->model, c, path);
 }
+
+/* src/forward.c:589-835 (n tokens as one chunk) and :846-868 */
+int ref_forward_chunk(ref_model *r, sllm_ctx *c, const int32_t *tokens, int32_t n, int32_t base, float *logits) {
+    return (int) sllm_forward_chunk(r->model, c, tokens, n, base, logits);
+}
+
+int ref_prefill_chunked(ref_model *r, sllm_ctx *c, const int32_t *tokens, int32_t n, int32_t chunk, float *logits) {
+    return (int) sllm_forward_prefill_chunked(r->model, c, tokens, n, chunk, logits);
+}

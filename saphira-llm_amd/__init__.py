@@ -126,6 +126,8 @@ PROTOTYPES = {
     "sllm_gfx950_ctx_n_past": (c_int32, [c_void_p]),
     "sllm_gfx950_forward": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "sllm_gfx950_generate_greedy": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "sllm_gfx950_forward_chunk": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "sllm_gfx950_forward_prefill_chunked": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "sllm_gfx950_ctx_logits": (c_void_p, [c_void_p]),
     "sllm_gfx950_ctx_argmax": (c_int, [c_void_p, POINTER(c_int32)]),
     "sllm_gfx950_ctx_kv_load": (c_int, [c_void_p, c_void_p, c_void_p, c_int32]),
@@ -493,6 +495,32 @@ class DeviceDecoder:
         out = np.empty(self.cfg["n_vocab"], np.float32) if logits else None
         check(lib().sllm_gfx950_forward(self.m, self.c, token, pos, ptr(out) if logits else None), "forward")
         return out
+
+    def forward_chunk(self, tokens, base, logits=True):
+        """Logits (float32[n][n_vocab]) of n tokens as one chunk at base.., or
+        None with logits=False (the last token's stay on the device)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty((t.size, self.cfg["n_vocab"]), np.float32) if logits else None
+        check(lib().sllm_gfx950_forward_chunk(self.m, self.c, ptr(t) if t.size else None, t.size, base,
+                                              ptr(out) if logits else None), "forward_chunk")
+        return out
+
+    def status_chunk(self, tokens, base):
+        """The raw status of a chunk forward without logits (argument checks)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        return lib().sllm_gfx950_forward_chunk(self.m, self.c, ptr(t) if t.size else None, t.size, base, None)
+
+    def prefill_chunked(self, tokens, chunk, logits=True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty((t.size, self.cfg["n_vocab"]), np.float32) if logits else None
+        check(lib().sllm_gfx950_forward_prefill_chunked(self.m, self.c, ptr(t) if t.size else None, t.size, chunk,
+                                                        ptr(out) if logits else None), "forward_prefill_chunked")
+        return out
+
+    def status_prefill(self, tokens, chunk):
+        t = np.ascontiguousarray(tokens, np.int32)
+        return lib().sllm_gfx950_forward_prefill_chunked(self.m, self.c, ptr(t) if t.size else None, t.size,
+                                                         chunk, None)
 
     def status_forward(self, token, pos):
         """The raw status of a forward (for argument checks)."""

@@ -53,6 +53,7 @@ typedef struct k_dec_attn {
     const k_dec_step *step;
     float             attn_scale;
     uint32_t          n_head, n_kv, hd, half, n_ctx, sc_stride;
+    uint32_t          chunk_base;
 } k_dec_attn;
 
 typedef struct k_dec_lm {
@@ -64,6 +65,26 @@ typedef struct k_dec_lm {
     float           eps;
     uint32_t        n_embd, n_vocab, pad;
 } k_dec_lm;
+
+typedef struct k_chk_prep {
+    const void      *a;
+    const float     *b;
+    const int32_t   *tokens;
+    float           *v_out;
+    const float     *norm_w;
+    int8_t          *q_out;
+    sllm_gfx950_act *act_out;
+    float           *xn_out;
+    float            eps;
+    uint32_t         k, mode, pad;
+} k_chk_prep;
+
+typedef struct k_chk_lm {
+    const float    *xn;
+    const uint16_t *embd;
+    float          *logits;
+    uint32_t        n_embd, n_vocab, n_tok, n_wg;
+} k_chk_lm;
 
 /* one GEMV stage's kernel arguments (dec_gemv_args) */
 typedef struct k_dec_gemv_args {
@@ -80,8 +101,10 @@ _Static_assert(sizeof(k_dec_gemv_args) == 296, "k_dec_gemv_args must match dec_g
 _Static_assert(sizeof(k_dec_stage) == 72, "k_dec_stage must match dec_stage");
 _Static_assert(sizeof(k_dec_attn) == 104, "k_dec_attn must match dec_attn");
 _Static_assert(sizeof(k_dec_lm) == 64, "k_dec_lm must match dec_lm");
+_Static_assert(sizeof(k_chk_prep) == 80, "k_chk_prep must match chk_prep");
+_Static_assert(sizeof(k_chk_lm) == 40, "k_chk_lm must match chk_lm");
 
-enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2 };
+enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 
 /* kernel constants (decode_kernels.hip) */
 #define ATT_THREADS 256
@@ -91,6 +114,9 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2 };
 #define LM_ROWS     64
 #define LM_MAX_E    8192
 #define LM_WG_PER_CU 4    /* output workgroups per CU (LDS: 32 KiB each) */
+#define CHK_THREADS  256
+#define CLM_THREADS  256
+#define CLM_TOK      4    /* tokens per chunk output-head workgroup */
 
 /* projections of a block, in the reference's order (src/forward.c:642-793) */
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, N_PROJ };
@@ -247,6 +273,17 @@ size_t sllm_gfx950_trace_dots(const sllm_gfx950_model *m) {
 /* context                                                             */
 /* ------------------------------------------------------------------ */
 
+/* Device buffers of a chunk of up to `cap` tokens, each [token][width]
+ * (src/forward.c:489-504 holds the same columns on the host). */
+typedef struct chunk_bufs {
+    void            *dev;
+    int32_t          cap;
+    int32_t         *tokens;
+    float           *x, *fi, *q, *k, *v, *attn, *proj, *g, *u, *xn, *scores, *logits;
+    int8_t          *q8;
+    sllm_gfx950_act *act;
+} chunk_bufs;
+
 struct sllm_gfx950_ctx {
     const struct sllm_gfx950_model *m;
     int32_t       n_ctx, n_past;
@@ -262,6 +299,9 @@ struct sllm_gfx950_ctx {
     k_dec_lm      lm_args;
     size_t        kv_per_layer;    /* floats */
     hipFunction_t f_gemv, f_scores, f_pv, f_lm, f_argmax;
+    hipFunction_t f_prep, f_kvs, f_cscores, f_cpv, f_clm, f_keys;
+    uint32_t      sc_stride;
+    chunk_bufs    chk;
     int           graph_on, graph_ready;
     hipGraph_t    graph;
     hipGraphExec_t graph_exec;
@@ -380,6 +420,7 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
     const int32_t half = (m->n_rot - m->n_rot % 2) / 2;
     c->kv_per_layer = (size_t) m->n_head_kv * (size_t) n_ctx * (size_t) m->hd;
     const uint32_t sc_stride = (uint32_t) ((n_ctx + 7) & ~7);
+    c->sc_stride = sc_stride;
     const uint32_t n_pass = (uint32_t) ((m->n_vocab + LM_ROWS - 1) / LM_ROWS);
     const uint32_t lm_cap = (uint32_t) (sllm_shim_cu() > 0 ? sllm_shim_cu() : 256) * LM_WG_PER_CU;
     const uint32_t lm_wg = n_pass < lm_cap ? n_pass : lm_cap;
@@ -432,14 +473,20 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
                 c->k_cache + (size_t) il * c->kv_per_layer, c->v_cache + (size_t) il * c->kv_per_layer,
                 c->rope, c->scores, c->attn, c->step, attn_scale,
                 (uint32_t) m->n_head, (uint32_t) m->n_head_kv, (uint32_t) m->hd, (uint32_t) half,
-                (uint32_t) n_ctx, sc_stride };
+                (uint32_t) n_ctx, sc_stride, 0 };
         }
         c->lm_args = (k_dec_lm) { c->down, c->ffn_inp, m->output_norm, m->tok_embd, c->logits, c->lm_partial,
                                   m->eps, (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };
         if ((st = sllm_shim_decode_function("sllm_k_dec_gemv", &c->f_gemv)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_dec_scores", &c->f_scores)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_dec_pv", &c->f_pv)) == SLLM_GFX950_OK &&
-            (st = sllm_shim_decode_function("sllm_k_dec_lm_head", &c->f_lm)) == SLLM_GFX950_OK) {
+            (st = sllm_shim_decode_function("sllm_k_dec_lm_head", &c->f_lm)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_prep", &c->f_prep)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_kv_store", &c->f_kvs)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_scores", &c->f_cscores)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_pv", &c->f_cpv)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_lm_head", &c->f_clm)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_keys", &c->f_keys)) == SLLM_GFX950_OK) {
             st = sllm_shim_decode_function("sllm_k_dec_argmax", &c->f_argmax);
         }
     }
@@ -457,6 +504,7 @@ void sllm_gfx950_ctx_free(sllm_gfx950_ctx *c) {
         hipStreamSynchronize(sllm_shim_stream());
         drop_graph(c);
         if (c->dev) hipFree(c->dev);
+        if (c->chk.dev) hipFree(c->chk.dev);
     }
     free(c->gargs);
     free(c->attn_args);
@@ -689,4 +737,197 @@ int sllm_gfx950_ctx_trace(sllm_gfx950_ctx *c, int32_t *dots, sllm_gfx950_act *ac
     if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_trace");
     drop_graph(c);
     return set_args(c, dots, acts);
+}
+
+/* ------------------------------------------------------------------ */
+/* chunks of tokens                                                    */
+/* ------------------------------------------------------------------ */
+
+/* the chunk buffers for at least n tokens (kept, grown on demand) */
+static int chunk_reserve(sllm_gfx950_ctx *c, int32_t n) {
+    if (n <= c->chk.cap) return SLLM_GFX950_OK;
+    const struct sllm_gfx950_model *m = c->m;
+    const int32_t cap = (n + 15) & ~15;
+    const size_t t = (size_t) cap, e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
+    const size_t big = e > f ? e : f;
+    const size_t sizes[] = {
+        t * 4,                                              /* tokens */
+        t * e * 4, t * e * 4, t * e * 4, t * g * 4, t * g * 4,   /* x fi q k v */
+        t * e * 4, t * e * 4, t * f * 4, t * f * 4, t * e * 4,   /* attn proj g u xn */
+        t * (size_t) m->n_head * c->sc_stride * 4,          /* scores */
+        t * (size_t) m->n_vocab * 4,                        /* logits */
+        t * big,                                            /* q8 */
+        t * sizeof(sllm_gfx950_act),                        /* act */
+    };
+    enum { N_BUF = sizeof sizes / sizeof sizes[0] };
+    size_t total = 0;
+    for (int i = 0; i < N_BUF; ++i) total += align256(sizes[i]);
+    hipError_t he = hipStreamSynchronize(sllm_shim_stream());
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "chunk buffers");
+    if (c->chk.dev) hipFree(c->chk.dev);
+    memset(&c->chk, 0, sizeof c->chk);
+    void *dev = NULL;
+    he = hipMalloc(&dev, total);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "chunk buffers: hipMalloc");
+    void *p[N_BUF];
+    uint8_t *at = dev;
+    for (int i = 0; i < N_BUF; ++i) { p[i] = at; at += align256(sizes[i]); }
+    chunk_bufs *B = &c->chk;
+    B->dev = dev; B->cap = cap;
+    B->tokens = p[0]; B->x = p[1]; B->fi = p[2]; B->q = p[3]; B->k = p[4]; B->v = p[5];
+    B->attn = p[6]; B->proj = p[7]; B->g = p[8]; B->u = p[9]; B->xn = p[10]; B->scores = p[11];
+    B->logits = p[12]; B->q8 = p[13]; B->act = p[14];
+    return SLLM_GFX950_OK;
+}
+
+static int prep(sllm_gfx950_ctx *c, int32_t n, uint32_t mode, const void *a, const float *b, float *v_out,
+                const float *norm_w, uint32_t k, int quantise, float *xn_out) {
+    k_chk_prep P = { a, b, c->chk.tokens, v_out, norm_w, quantise ? c->chk.q8 : NULL,
+                     quantise ? c->chk.act : NULL, xn_out, c->m->eps, k, mode, 0 };
+    void *args[] = { &P };
+    return sllm_shim_launch(c->f_prep, (uint32_t) n, 1, CHK_THREADS, 0, args);
+}
+
+/* One chunk of n tokens at positions base .. base + n - 1, the chunk's tokens
+ * already in chk.tokens: src/forward.c:589-835 layer by layer, every
+ * projection one MFMA GEMM over the n quantised rows. all_logits: the output
+ * head for every token into chk.logits (and the last row into c->logits);
+ * otherwise for the last token only, straight into c->logits. Either way the
+ * last row's argmax lands in the step record. */
+static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_logits) {
+    const struct sllm_gfx950_model *m = c->m;
+    const chunk_bufs *B = &c->chk;
+    const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
+    const uint32_t pos_blocks = (uint32_t) ((base + n + ATT_POS - 1) / ATT_POS);
+    const uint32_t slices = (uint32_t) (m->hd / PV_SLICE);
+    int st = SLLM_GFX950_OK;
+    for (int32_t il = 0; il < m->n_layer && st == SLLM_GFX950_OK; ++il) {
+        const dev_layer *L = &m->layers[il];
+        /* l_out of the layer below (cproj + cffn_inp), or the embedding; attn_norm */
+        st = il == 0 ? prep(c, n, IN_EMBED, m->tok_embd, NULL, B->x, L->attn_norm, (uint32_t) e, 1, NULL)
+                     : prep(c, n, IN_RESID, B->proj, B->fi, B->x, L->attn_norm, (uint32_t) e, 1, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_Q], e, e, B->q8, B->act, (size_t) n, B->q, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_K], g, e, B->q8, B->act, (size_t) n, B->k, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_V], g, e, B->q8, B->act, (size_t) n, B->v, NULL);
+        k_dec_attn A = c->attn_args[il];
+        A.q = B->q; A.k = B->k; A.v = B->v; A.scores = B->scores; A.out = B->attn;
+        A.chunk_base = (uint32_t) base;
+        void *aargs[] = { &A };
+        if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_kvs, (uint32_t) n, 1, ATT_THREADS, 0, aargs);
+        if (st == SLLM_GFX950_OK) {
+            st = sllm_shim_launch_3d(c->f_cscores, (uint32_t) m->n_head_kv, pos_blocks, (uint32_t) n,
+                                     ATT_THREADS, aargs);
+        }
+        if (st == SLLM_GFX950_OK) {
+            st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, slices, (uint32_t) n, ATT_THREADS, aargs);
+        }
+        /* attn_sub_norm, O */
+        if (st == SLLM_GFX950_OK) st = prep(c, n, IN_PLAIN, B->attn, NULL, NULL, L->attn_sub_norm, (uint32_t) e, 1, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_O], e, e, B->q8, B->act, (size_t) n, B->proj, NULL);
+        /* ffn_inp = attn_out + inpSA; ffn_norm; gate, up */
+        if (st == SLLM_GFX950_OK) st = prep(c, n, IN_RESID, B->proj, B->x, B->fi, L->ffn_norm, (uint32_t) e, 1, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_GATE], f, e, B->q8, B->act, (size_t) n, B->g, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_UP], f, e, B->q8, B->act, (size_t) n, B->u, NULL);
+        /* silu(gate) * up, ffn_sub_norm, down */
+        if (st == SLLM_GFX950_OK) st = prep(c, n, IN_SILU, B->g, B->u, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL);
+        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_DOWN], e, f, B->q8, B->act, (size_t) n, B->proj, NULL);
+    }
+    if (st != SLLM_GFX950_OK) return st;
+    const hipStream_t s = sllm_shim_stream();
+    const float *last = c->logits;
+    if (all_logits) {
+        /* l_out, output_norm per token, every token's row of logits */
+        st = prep(c, n, IN_RESID, B->proj, B->fi, NULL, m->output_norm, (uint32_t) e, 0, B->xn);
+        const uint32_t n_tb = (uint32_t) ((n + CLM_TOK - 1) / CLM_TOK);
+        const uint32_t n_rb = (uint32_t) ((m->n_vocab + CLM_THREADS - 1) / CLM_THREADS);
+        k_chk_lm L = { B->xn, m->tok_embd, B->logits, (uint32_t) e, (uint32_t) m->n_vocab, (uint32_t) n,
+                       pad8(n_tb * n_rb) };
+        void *largs[] = { &L };
+        if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_clm, L.n_wg, 1, CLM_THREADS, 0, largs);
+        if (st == SLLM_GFX950_OK) {
+            hipError_t he = hipMemcpyAsync(c->logits, B->logits + (size_t) (n - 1) * (size_t) m->n_vocab,
+                                           (size_t) m->n_vocab * 4, hipMemcpyDeviceToDevice, s);
+            if (he != hipSuccess) st = sllm_shim_hip_fail(he, "chunk: last logits");
+        }
+        uint64_t *partial = c->lm_partial;
+        uint32_t nv = (uint32_t) m->n_vocab;
+        void *kargs[] = { (void *) &last, &nv, (void *) &partial };
+        if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_keys, c->lm_wg, 1, 256, 0, kargs);
+    } else {
+        /* the last token alone, through the decode step's output kernel */
+        k_dec_lm L = c->lm_args;
+        L.a = B->proj + (size_t) (n - 1) * e;
+        L.b = B->fi + (size_t) (n - 1) * e;
+        void *largs[] = { &L };
+        st = sllm_shim_launch(c->f_lm, c->lm_wg, 1, LM_THREADS, 0, largs);
+    }
+    if (st == SLLM_GFX950_OK) {
+        const uint64_t *partial = c->lm_partial;
+        k_dec_step *step = c->step;
+        uint32_t nw = c->lm_wg;
+        void *aargs[] = { (void *) &partial, &nw, (void *) &last, (void *) &step };
+        st = sllm_shim_launch(c->f_argmax, 1, 1, 256, 0, aargs);
+    }
+    return st;
+}
+
+int sllm_gfx950_forward_chunk(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *tokens, int32_t n,
+                              int32_t base, float *logits) {
+    if (m == NULL || c == NULL || c->m != m || tokens == NULL) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_chunk: model / context / tokens");
+    }
+    if (n < 1 || n > SLLM_GFX950_DEC_MAX_CHUNK) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_chunk: n = %d outside [1, %d]", n, SLLM_GFX950_DEC_MAX_CHUNK);
+    }
+    if (base < c->n_past || (int64_t) base + n > c->n_ctx) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_chunk: positions [%d, %d) outside [n_past %d, n_ctx %d)",
+                              base, base + n, c->n_past, c->n_ctx);
+    }
+    for (int32_t t = 0; t < n; ++t) {
+        if (tokens[t] < 0 || tokens[t] >= m->n_vocab) {
+            return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_chunk: token %d out of range", tokens[t]);
+        }
+    }
+    if (n == 1) return sllm_gfx950_forward(m, c, tokens[0], base, logits);
+    int st = chunk_reserve(c, n);
+    if (st != SLLM_GFX950_OK) return st;
+    const hipStream_t s = sllm_shim_stream();
+    hipError_t he = hipMemcpyAsync(c->chk.tokens, tokens, (size_t) n * 4, hipMemcpyHostToDevice, s);
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "forward_chunk: tokens");
+    k_dec_step hs;
+    memset(&hs, 0, sizeof hs);
+    hs.token = tokens[n - 1];
+    hs.pos = base + n - 1;
+    st = set_step(c, &hs);
+    if (st == SLLM_GFX950_OK) st = launch_chunk(c, n, base, logits != NULL);
+    if (st != SLLM_GFX950_OK) return st;
+    c->n_past = base + n;
+    if (logits != NULL) {
+        he = hipMemcpyAsync(logits, c->chk.logits, (size_t) n * (size_t) m->n_vocab * 4, hipMemcpyDeviceToHost, s);
+        if (he == hipSuccess) he = hipStreamSynchronize(s);
+        if (he != hipSuccess) return sllm_shim_hip_fail(he, "forward_chunk: logits");
+    }
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_forward_prefill_chunked(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *tokens,
+                                        int32_t n, int32_t chunk, float *logits) {
+    if (m == NULL || c == NULL || c->m != m || (tokens == NULL && n > 0) || n < 0) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_prefill_chunked: bad arguments");
+    }
+    if (chunk < 1 || chunk > SLLM_GFX950_DEC_MAX_CHUNK) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_prefill_chunked: chunk %d outside [1, %d]", chunk,
+                              SLLM_GFX950_DEC_MAX_CHUNK);
+    }
+    if (n > c->n_ctx) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_TOO_LARGE, "forward_prefill_chunked: %d tokens > n_ctx %d", n, c->n_ctx);
+    }
+    for (int32_t done = 0; done < n;) {
+        const int32_t take = n - done < chunk ? n - done : chunk;
+        const int st = sllm_gfx950_forward_chunk(m, c, tokens + done, take, done,
+                                                 logits != NULL ? logits + (size_t) done * (size_t) m->n_vocab : NULL);
+        if (st != SLLM_GFX950_OK) return st;
+        done += take;
+    }
+    return SLLM_GFX950_OK;
 }

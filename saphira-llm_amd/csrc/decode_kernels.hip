@@ -386,6 +386,7 @@ struct dec_attn {
     float           attn_scale;
     uint32_t        n_head, n_kv, hd, half, n_ctx;
     uint32_t        sc_stride;          // scores row stride: n_ctx rounded up to 8
+    uint32_t        chunk_base;         // chunk kernels: the position of the chunk's first token
 };
 static_assert(sizeof(dec_attn) == 104, "dec_attn must match decode.c");
 
@@ -451,26 +452,34 @@ sllm_k_dec_gemv(dec_gemv_args A) {
 }
 
 // Scores: workgroup (KV head, 64 positions). Every workgroup ropes the query
-// heads of its KV head; the one holding position pos ropes the new key and
-// stores it, with the new value, into the caches (src/forward.c:668-690).
-// Thread (h, r) then takes q_h . k_r over d in order, times 1/sqrt(hd)
-// (src/forward.c:698-705). The chunk's cached keys are loaded first, all at
-// once, and wait in registers while the queries are roped.
-extern "C" __global__ void __launch_bounds__(ATT_THREADS)
-sllm_k_dec_scores(dec_attn A) {
+// heads of its KV head; in a decode step the one holding position pos ropes
+// the new key and stores it, with the new value, into the caches
+// (src/forward.c:668-690). Thread (h, r) then takes q_h . k_r over d in
+// order, times 1/sqrt(hd) (src/forward.c:698-705). The cached keys are
+// loaded first, all at once, and wait in registers while the queries are
+// roped. CHUNK: grid z is the chunk's token t at position chunk_base + t,
+// whose keys (its own included) are already in the cache; q, scores and out
+// advance by one token's worth per t.
+template <bool CHUNK>
+__device__ __forceinline__ void scores_body(const dec_attn &A) {
     __shared__ __attribute__((aligned(16))) float qr[ATT_MAX_GRP][ATT_MAX_HD];
     __shared__ __attribute__((aligned(16))) float kt[ATT_POS][KT_STRIDE];
     const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tid = threadIdx.x;
-    const uint32_t pos = (uint32_t) A.step->pos, npast = pos + 1;
+    const uint32_t t = CHUNK ? blockIdx.z : 0u;
+    const uint32_t pos = CHUNK ? A.chunk_base + t : (uint32_t) A.step->pos, npast = pos + 1;
     if (s0 >= npast) return;
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, half = A.half, hd4 = hd / 4;
     float *kc = A.k_cache + (size_t) kvh * A.n_ctx * hd;
     float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd;
     const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
+    const float *q = A.q + (size_t) t * A.n_head * hd;
+    float *scores = A.scores + (size_t) t * A.n_head * A.sc_stride;
 
-    // (1) every global load first: the chunk's cached keys (rows past pos - 1
-    // re-read a valid row), this thread's query elements and the new key's
-    const uint32_t n_f4 = ATT_POS * hd4, last_cached = pos > 0 ? pos - 1 : 0;
+    // (1) every global load first: the cached keys (rows past the last
+    // cached one re-read a valid row), this thread's query elements and, in
+    // a decode step, the new key's
+    const uint32_t n_cached = CHUNK ? npast : pos;
+    const uint32_t n_f4 = ATT_POS * hd4, last_cached = n_cached > 0 ? n_cached - 1 : 0;
     f32x4 kv[KT_LOADS];
 #pragma unroll
     for (int u = 0; u < KT_LOADS; ++u) {
@@ -482,10 +491,14 @@ sllm_k_dec_scores(dec_attn A) {
 #pragma unroll
     for (int u = 0; u < QR_PER_THREAD; ++u) {
         const uint32_t idx = min(tid + (uint32_t) u * ATT_THREADS, grp * hd - 1);
-        qi[u] = rope_load(A.q + (size_t) (kvh * grp + idx / hd) * hd, idx % hd, half, cs);
+        qi[u] = rope_load(q + (size_t) (kvh * grp + idx / hd) * hd, idx % hd, half, cs);
     }
-    const rope_in ki = rope_load(A.k + (size_t) kvh * hd, min(tid, hd - 1), half, cs);
-    const float vnew = A.v[(size_t) kvh * hd + min(tid, hd - 1)];
+    rope_in ki = {};
+    float vnew = 0.0f;
+    if (!CHUNK) {
+        ki = rope_load(A.k + (size_t) kvh * hd, min(tid, hd - 1), half, cs);
+        vnew = A.v[(size_t) kvh * hd + min(tid, hd - 1)];
+    }
 
     // (2) roped queries, the new key and value, the cached keys into LDS
 #pragma unroll
@@ -493,7 +506,7 @@ sllm_k_dec_scores(dec_attn A) {
         const uint32_t idx = tid + (uint32_t) u * ATT_THREADS;
         if (idx < grp * hd) qr[idx / hd][idx % hd] = rope_apply(qi[u], idx % hd, half);
     }
-    if (pos - s0 < ATT_POS && tid < hd) {
+    if (!CHUNK && pos - s0 < ATT_POS && tid < hd) {
         const float val = rope_apply(ki, tid, half);
         kt[pos - s0][tid] = val;
         kc[(size_t) pos * hd + tid] = val;
@@ -503,7 +516,7 @@ sllm_k_dec_scores(dec_attn A) {
     for (int u = 0; u < KT_LOADS; ++u) {
         const uint32_t f = tid + (uint32_t) u * ATT_THREADS;
         const uint32_t r = f / hd4, c4 = f % hd4;
-        if (f < n_f4 && s0 + r < pos) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
+        if (f < n_f4 && s0 + r < n_cached) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
     }
     __syncthreads();
     // (3) thread (h, r): the dot in order of d
@@ -518,9 +531,17 @@ sllm_k_dec_scores(dec_attn A) {
             acc = acc + q4[2] * k4[2];
             acc = acc + q4[3] * k4[3];
         }
-        A.scores[(size_t) (kvh * grp + hh) * A.sc_stride + s0 + r] = acc * A.attn_scale;
+        scores[(size_t) (kvh * grp + hh) * A.sc_stride + s0 + r] = acc * A.attn_scale;
     }
 }
+
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_dec_scores(dec_attn A) { scores_body<false>(A); }
+
+// The chunk's scores: grid (KV head, 64-position blocks up to the chunk's
+// last position, token).
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_chk_scores(dec_attn A) { scores_body<true>(A); }
 
 // Softmax and p . V: workgroup (KV head, 16 head dimensions), four waves.
 //  - The slice of V for the first 1536 positions is loaded first, all of it
@@ -536,16 +557,18 @@ sllm_k_dec_scores(dec_attn A) {
 //  - Per round of 1536 positions, p and V (transposed) in LDS; wave 0, one
 //    lane per (head, dimension), adds p_s * v_s to its accumulator in order
 //    of s (src/forward.c:706-726), its LDS reads sixteen positions ahead.
-extern "C" __global__ void __launch_bounds__(ATT_THREADS)
-sllm_k_dec_pv(dec_attn A) {
+template <bool CHUNK>
+__device__ __forceinline__ void pv_body(const dec_attn &A) {
     __shared__ __attribute__((aligned(16))) float P[ATT_MAX_GRP][PV_RPOS];
     __shared__ __attribute__((aligned(16))) float Vt[PV_SLICE][PV_VSTRIDE];
     __shared__ float stat_inv[ATT_MAX_GRP], stat_m[ATT_MAX_GRP];
     __shared__ uint64_t tab[32];          // the expf table, next to the lanes that index it
     const uint32_t kvh = blockIdx.x, d0 = blockIdx.y * PV_SLICE, tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
-    const uint32_t npast = (uint32_t) A.step->pos + 1;
+    const uint32_t t = CHUNK ? blockIdx.z : 0u;
+    const uint32_t npast = (CHUNK ? A.chunk_base + t : (uint32_t) A.step->pos) + 1;
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
+    const float *scores = A.scores + (size_t) t * A.n_head * ss;
     const uint32_t nb = npast / 8, nt = nb * 8;
     const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d0;
 
@@ -587,7 +610,7 @@ sllm_k_dec_pv(dec_attn A) {
         }
     };
     if (wave < grp) {
-        const float *sc = A.scores + (size_t) (kvh * grp + wave) * ss;
+        const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
         float *ph = P[wave];
         float m = -INFINITY;
         for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
@@ -654,7 +677,7 @@ sllm_k_dec_pv(dec_attn A) {
             __syncthreads();                      // stat_* visible; the last round's reads done
             load_v(base);
             if (wave < grp) {                     // p of this round, recomputed (the same bits)
-                const float *sc = A.scores + (size_t) (kvh * grp + wave) * ss;
+                const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
                 const float m = stat_m[wave], inv = stat_inv[wave];
                 for (uint32_t i0 = 0; i0 < n; i0 += 512) {
                     float v[8];
@@ -710,8 +733,15 @@ sllm_k_dec_pv(dec_attn A) {
             for (; s < n; ++s) acc = acc + ph[s] * vt[s];
         }
     }
-    if (chain) A.out[(size_t) (kvh * grp + lane / PV_SLICE) * hd + d0 + lane % PV_SLICE] = acc;
+    if (chain) A.out[(size_t) t * A.n_head * hd + (size_t) (kvh * grp + lane / PV_SLICE) * hd + d0 + lane % PV_SLICE] = acc;
 }
+
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_dec_pv(dec_attn A) { pv_body<false>(A); }
+
+// The chunk's softmax and p . V: grid (KV head, 16-dimension slices, token).
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_chk_pv(dec_attn A) { pv_body<true>(A); }
 
 // ---------------------------------------------------------------------------
 // output: x = a + b, RMSNorm with output_norm, the F16 rows
@@ -877,5 +907,246 @@ sllm_k_dec_argmax(const uint64_t *__restrict__ partial, uint32_t n, const float 
             st->token = next;
         }
         st->pos += 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// chunks of tokens (src/forward.c:589-835 with n > 1): per-token kernels
+// around the batched MFMA GEMM (i2s_kernels.hip), the chunk modes of the
+// attention kernels above, and the output head over every token
+// ---------------------------------------------------------------------------
+
+namespace {
+
+enum : uint32_t { IN_SILU = 3 };
+
+// One token's activation, built, normalised and quantised: row t of a
+// [n][k] layout per workgroup.
+struct chk_prep {
+    const void    *a;          // IN_EMBED: f16 rows [n_vocab][k]; else f32 [n][k] (IN_SILU: gate)
+    const float   *b;          // IN_RESID: added to a; IN_SILU: up
+    const int32_t *tokens;     // IN_EMBED: the chunk's tokens
+    float         *v_out;      // the vector as built, [n][k], or null
+    const float   *norm_w;     // RMSNorm weight, k floats
+    int8_t        *q_out;      // the quantised rows [n][k], or null
+    act_t         *act_out;    // their scale / sum [n], or null
+    float         *xn_out;     // the normalised rows [n][k] (the output head's input), or null
+    float          eps;
+    uint32_t       k, mode, pad;
+};
+static_assert(sizeof(chk_prep) == 80, "chk_prep must match decode.c");
+
+constexpr int CHK_THREADS = 256;
+constexpr uint32_t CHK_MAX_K = 7168;
+
+// The output head over a chunk: logits[t][r] = row r . xn[t] for every
+// token (src/forward.c:800-827 with n > 1).
+struct chk_lm {
+    const float    *xn;        // [n][n_embd]
+    const uint16_t *embd;      // [n_vocab][n_embd] f16
+    float          *logits;    // [n][n_vocab]
+    uint32_t        n_embd, n_vocab, n_tok, n_wg;
+};
+static_assert(sizeof(chk_lm) == 40, "chk_lm must match decode.c");
+
+constexpr int CLM_THREADS = 256;        // one row per lane
+constexpr int CLM_TOK = 4;              // tokens per workgroup
+
+} // namespace
+
+// Workgroup t: token t's vector (the embedding lookup; a residual sum;
+// silu(gate) * up as src/forward.c:776-778), kept in v_out if asked; RMSNorm
+// (src/ops.c:254-322) with the same mean as the decode step's; then either
+// the normalised row (xn_out) or its quantisation (src/i2s_gemm.c:45-83).
+extern "C" __global__ void __launch_bounds__(CHK_THREADS)
+sllm_k_chk_prep(chk_prep P) {
+    __shared__ __attribute__((aligned(16))) float xs[CHK_MAX_K];
+    __shared__ double red_d[CHK_THREADS / 64], lane_d[4];
+    __shared__ float red_f[CHK_THREADS / 64];
+    __shared__ int red_i[CHK_THREADS / 64];
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = P.k;
+    const size_t row = (size_t) t * k;
+    const int32_t token = P.mode == IN_EMBED ? P.tokens[t] : 0;
+    double part = 0.0;
+    for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
+        f32x4 v;
+        if (P.mode == IN_EMBED) {
+            const u32x2 h = *G_CAST(const u32x2, (const uint16_t *) P.a + (size_t) token * k + i);
+            v = (f32x4) { embd_f32(h[0] & 0xffffu), embd_f32(h[0] >> 16), embd_f32(h[1] & 0xffffu),
+                          embd_f32(h[1] >> 16) };
+        } else {
+            v = *G_CAST(const f32x4, (const float *) P.a + row + i);
+            if (P.mode == IN_RESID) {
+                v = v + *G_CAST(const f32x4, P.b + row + i);
+            } else if (P.mode == IN_SILU) {
+                const f32x4 u = *G_CAST(const f32x4, P.b + row + i);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = silu(v[c]) * u[c];
+            }
+        }
+        *reinterpret_cast<f32x4 *>(xs + i) = v;
+        if (P.v_out != nullptr) *G_CAST(f32x4, P.v_out + row + i) = v;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) part += (double) (v[c] * v[c]);
+    }
+    const float mean = rms_mean(part, k, red_d, lane_d, [&](uint32_t j) { return xs[j]; });
+    const float scale = 1.0f / sqrtf(mean + P.eps);
+    float m = 0.0f;
+    for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
+        f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
+        const f32x4 w = *G_CAST(const f32x4, P.norm_w + i);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[c] = (scale * v[c]) * w[c];
+            m = fmaxf(m, fabsf(v[c]));
+        }
+        *reinterpret_cast<f32x4 *>(xs + i) = v;
+        if (P.xn_out != nullptr) *G_CAST(f32x4, P.xn_out + row + i) = v;
+    }
+    if (P.q_out == nullptr) return;                  // uniform
+    m = wave_max(m);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    m = red_f[0];
+#pragma unroll
+    for (int w = 1; w < CHK_THREADS / 64; ++w) m = fmaxf(m, red_f[w]);
+    const float qs = m > 0.0f ? 127.0f / m : 0.0f;
+    int ls = 0;
+    for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
+        const int a = quant_one(v[0] * qs), b = quant_one(v[1] * qs);
+        const int c = quant_one(v[2] * qs), e = quant_one(v[3] * qs);
+        ls += a + b + c + e;
+        *G_CAST(uint32_t, P.q_out + row + i) =
+            (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) | ((uint32_t) (c & 0xff) << 16) |
+            ((uint32_t) (e & 0xff) << 24);
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) red_i[wave] = ls;
+    __syncthreads();
+    if (tid == 0) {
+        int32_t asum = 0;
+#pragma unroll
+        for (int w = 0; w < CHK_THREADS / 64; ++w) asum += red_i[w];
+        G_CAST(float, P.act_out + t)[0] = qs;
+        G_CAST(int32_t, P.act_out + t)[1] = asum;
+    }
+}
+
+// Workgroup t: token t's key roped at its position (NeoX, src/ops.c:467-549)
+// and stored with its value into the caches (src/forward.c:668-690), so that
+// every query of the chunk finds the keys at or before its position.
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_chk_kv_store(dec_attn A) {
+    const uint32_t t = blockIdx.x, pos = A.chunk_base + t, hd = A.hd, half = A.half;
+    const uint32_t gqa = A.n_kv * hd;
+    const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
+    const float *k = A.k + (size_t) t * gqa, *v = A.v + (size_t) t * gqa;
+    for (uint32_t i = threadIdx.x; i < gqa; i += ATT_THREADS) {
+        const uint32_t kvh = i / hd, d = i % hd;
+        const rope_in r = rope_load(k + (size_t) kvh * hd, d, half, cs);
+        const size_t at = ((size_t) kvh * A.n_ctx + pos) * hd + d;
+        A.k_cache[at] = rope_apply(r, d, half);
+        A.v_cache[at] = v[i];
+    }
+}
+
+// The output head over a chunk. Lane = one row; a workgroup takes 256 rows
+// for CLM_TOK tokens. Each row . xn[t] is formed as src/ops.c:106-154 orders
+// it: accumulator 8j + l collects element 32i + 8j + l by FMA over i; then
+// (acc_0 + acc_2) + (acc_1 + acc_3) per l, t_l = a_l + a_{l+4},
+// (t0 + t1) + (t2 + t3). The normalised rows are the same for every lane,
+// so they are read as wave-uniform values. Workgroups for the same rows sit
+// next to each other on one XCD, so the rows come from its L2 after the
+// first token block.
+extern "C" __global__ void __launch_bounds__(CLM_THREADS)
+sllm_k_chk_lm_head(chk_lm L) {
+    const uint32_t n_tb = (L.n_tok + CLM_TOK - 1) / CLM_TOK;
+    const uint32_t b = xcd_slot(L.n_wg);
+    const uint32_t tb = b % n_tb, rb = b / n_tb;
+    const uint32_t e = L.n_embd, steps = e / 32;
+    if (rb * CLM_THREADS >= L.n_vocab) return;
+    const uint32_t row = min(rb * CLM_THREADS + threadIdx.x, L.n_vocab - 1);
+    const uint32_t t0 = tb * CLM_TOK;
+    const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) row * e);
+    // the normalised rows do not change during the launch: constant
+    // address space, so the wave-uniform reads are scalar loads
+    typedef __attribute__((address_space(4))) const float cfloat;
+    cfloat *xb[CLM_TOK];
+#pragma unroll
+    for (int u = 0; u < CLM_TOK; ++u) xb[u] = (cfloat *) (L.xn + (size_t) min(t0 + (uint32_t) u, L.n_tok - 1) * e);
+    float acc[CLM_TOK][32];
+#pragma unroll
+    for (int u = 0; u < CLM_TOK; ++u) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) acc[u][j] = 0.0f;
+    }
+    // 32 elements (64 bytes) of the row per step; steps alternate between
+    // two buffers so that the next step's loads are in flight during this one
+    auto load = [&](uint32_t i, u32x4 (&h)[4]) {
+        const uint32_t at = 4 * min(i, steps - 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) h[c] = w[at + (uint32_t) c];
+    };
+    auto step = [&](uint32_t i, const u32x4 (&h)[4]) {
+        float hf[32];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, h[c]), f32x8);
+#pragma unroll
+            for (int l = 0; l < 8; ++l) hf[8 * c + l] = f[l];
+        }
+#pragma unroll
+        for (int u = 0; u < CLM_TOK; ++u) {
+            cfloat *x = xb[u] + 32 * i;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) acc[u][j] = fmaf(hf[j], x[j], acc[u][j]);
+        }
+    };
+    u32x4 ha[4], hb[4];
+    load(0, ha);
+    uint32_t i = 0;
+    for (; i + 1 < steps; i += 2) {
+        load(i + 1, hb);
+        step(i, ha);
+        load(i + 2, ha);
+        step(i + 1, hb);
+    }
+    if (i < steps) step(i, ha);
+    if (rb * CLM_THREADS + threadIdx.x >= L.n_vocab) return;
+#pragma unroll
+    for (int u = 0; u < CLM_TOK; ++u) {
+        if (t0 + (uint32_t) u < L.n_tok) {
+            float a[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) a[l] = (acc[u][l] + acc[u][16 + l]) + (acc[u][8 + l] + acc[u][24 + l]);
+            const float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+            L.logits[(size_t) (t0 + (uint32_t) u) * L.n_vocab + row] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+// Argmax keys of one logits row (the chunk's last token): workgroup w's key
+// is the largest over rows w*256 + tid + k*gridDim.x*256, for
+// sllm_k_dec_argmax to finish.
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_chk_keys(const float *__restrict__ logits, uint32_t n, uint64_t *__restrict__ partial) {
+    __shared__ uint64_t red[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    uint64_t best = 0;
+    for (uint32_t i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) {
+        const uint64_t key = argmax_key(logits[i], i);
+        best = key > best ? key : best;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t other = __shfl_xor(best, o, 64);
+        best = other > best ? other : best;
+    }
+    if (lane == 0) red[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < 4; ++i) best = red[i] > best ? red[i] : best;
+        partial[blockIdx.x] = best;
     }
 }

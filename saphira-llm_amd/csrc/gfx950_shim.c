@@ -165,7 +165,18 @@ const char *sllm_gfx950_status_string(int status) {
     case SLLM_GFX950_OK:                 return "ok";
     case SLLM_GFX950_ERR_ARG:            return "invalid-argument";
     case SLLM_GFX950_ERR_NOMEM:          return "out-of-memory";
+    case SLLM_GFX950_ERR_IO:             return "io-error";
     case SLLM_GFX950_ERR_UNSUPPORTED:    return "unsupported";
+    case SLLM_GFX950_ERR_GGUF_MAGIC:     return "gguf-bad-magic";
+    case SLLM_GFX950_ERR_GGUF_VERSION:   return "gguf-unsupported-version";
+    case SLLM_GFX950_ERR_GGUF_TRUNCATED: return "gguf-truncated";
+    case SLLM_GFX950_ERR_GGUF_TYPE:      return "gguf-bad-value-type";
+    case SLLM_GFX950_ERR_GGUF_TENSOR:    return "gguf-bad-tensor";
+    case SLLM_GFX950_ERR_GGUF_ALIGNMENT: return "gguf-bad-alignment";
+    case SLLM_GFX950_ERR_GGUF_LAYOUT:    return "gguf-bad-layout";
+    case SLLM_GFX950_ERR_GGUF_KEYDUP:    return "gguf-duplicate-key";
+    case SLLM_GFX950_ERR_ARCH:           return "unsupported-architecture";
+    case SLLM_GFX950_ERR_KV_MISSING:     return "missing-metadata";
     case SLLM_GFX950_ERR_TENSOR_SHAPE:   return "wrong-tensor-shape";
     case SLLM_GFX950_ERR_TOO_LARGE:      return "exceeds-limit";
     case SLLM_GFX950_ERR_NO_DEVICE:      return "no-gfx950-device";
@@ -431,6 +442,12 @@ int sllm_shim_decode_function(const char *name, hipFunction_t *f) {
 int sllm_shim_launch(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t block, uint32_t lds, void **args) {
     if (gx == 0 || gy == 0) return SLLM_GFX950_OK;
     HIP_TRY(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, lds, g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
+int sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, void **args) {
+    if (gx == 0 || gy == 0 || gz == 0) return SLLM_GFX950_OK;
+    HIP_TRY(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, 0, g.stream, args, NULL));
     return SLLM_GFX950_OK;
 }
 

@@ -1,0 +1,169 @@
+"""Chunks of tokens on the GPU (sllm_gfx950_forward_chunk,
+sllm_gfx950_forward_prefill_chunked) against the oracle.
+
+The reference's chunk path gives every position the logits of its one-token
+path bit for bit (tests/test_oracle_fwd.py runs its own
+sllm_forward_prefill_chunked to show it), and the oracle's token-by-token
+logits are those bits; so every row of a device chunk must equal the
+oracle's logits at that position, bit for bit. Shapes: chunk sizes from 2
+to 64 over a 70-token sequence (later chunks attend to keys earlier ones
+wrote), chunks over a restored 1024-position cache at tiny and BitNet-2B
+widths, the full 30-block 2B model in one 100-token chunk (the MFMA GEMM's
+LDS tile), and decode / greedy generation carrying on after a chunk.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_rot=64, n_vocab=1000,
+            eps=1e-5, rope_base=500000.0)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _tokens(n, vocab, seed):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, vocab, n)]
+
+
+def _oracle_logits(orc, model, n_ctx, toks, base=0, caches=None):
+    o = orc.Decoder(model, n_ctx)
+    try:
+        if caches is not None:
+            ok, ov = o.caches()
+            k, v = caches
+            ok[:, :, :k.shape[2]] = k
+            ov[:, :, :v.shape[2]] = v
+        return np.stack([o.forward(t, base + p) for p, t in enumerate(toks)])
+    finally:
+        o.close()
+
+
+def _first_diff(got, want):
+    bad = np.argwhere(bits(got) != bits(want))
+    return f"first differing (position, row) {tuple(bad[0])} of {len(bad)}" if len(bad) else ""
+
+
+@pytest.fixture(scope="module")
+def tiny(amd, orc):
+    model = amd.synth_model(TINY, 71)
+    toks = _tokens(70, TINY["n_vocab"], 72)
+    emb = np.asarray(model["tok_embd"]).reshape(TINY["n_vocab"], TINY["n_embd"])
+    for i, t in enumerate(toks[::5]):                 # binary16 subnormals in the lookup
+        emb[t, (11 * i) % TINY["n_embd"]] = (0x0001, 0x03FF, 0x8200, 0x0155)[i % 4]
+    return model, toks, _oracle_logits(orc, model, 80, toks)
+
+
+@pytest.mark.parametrize("chunk", [2, 3, 7, 16, 64])
+def test_chunked_prefill_matches_token_by_token(amd, dev, tiny, chunk):
+    model, toks, want = tiny
+    print(f"[chunk] prefill 70 tokens in chunks of {chunk}", flush=True)
+    g = amd.DeviceDecoder(dev, model, 80)
+    try:
+        got = g.prefill_chunked(toks, chunk)
+        assert g.n_past() == len(toks)
+    finally:
+        g.close()
+    assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
+def test_chunks_at_uneven_positions_then_decode(amd, dev, tiny):
+    """forward_chunk at base 0 (5 tokens), a single token, a chunk of 30, then
+    one token at a time; the graph-replayed decode step carries on from the
+    cache the chunks wrote."""
+    model, toks, want = tiny
+    g = amd.DeviceDecoder(dev, model, 80)
+    g.set_graph(True)
+    try:
+        rows = [g.forward_chunk(toks[:5], 0), g.forward_chunk(toks[5:6], 5), g.forward_chunk(toks[6:36], 6)]
+        rows += [g.forward(t, p)[None] for p, t in enumerate(toks[36:45], 36)]
+        rows.append(g.forward_chunk(toks[45:70], 45))
+        got = np.concatenate(rows)
+    finally:
+        g.close()
+    assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
+def test_chunk_without_logits_keeps_the_last_and_greedy_continues(amd, orc, dev, tiny):
+    """logits = NULL: the output head runs for the last token only; its
+    argmax starts a greedy continuation, as after a one-token forward."""
+    model, toks, want = tiny
+    g = amd.DeviceDecoder(dev, model, 80)
+    u = amd.DeviceDecoder(dev, model, 80)
+    try:
+        assert g.forward_chunk(toks[:40], 0, logits=False) is None
+        assert g.argmax() == int(np.argmax(want[39]))
+        for p, t in enumerate(toks[:40]):
+            u.forward(t, p, logits=False)
+        assert np.array_equal(g.generate([], 12), u.generate([], 12))
+    finally:
+        g.close()
+        u.close()
+
+
+@pytest.mark.parametrize("widths", ["tiny", "2b"])
+def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
+    """40 tokens at positions 1024..1063 over a restored cache: every query's
+    softmax spans its own KV rows past the prefix."""
+    cfg = dict(TINY) if widths == "tiny" else dict(amd.BITNET_2B, n_layer=2, n_vocab=512)
+    model = amd.synth_model(cfg, 73)
+    n_pos, n_ctx = 1024, 1072
+    hd = cfg["n_embd"] // cfg["n_head"]
+    rng = np.random.default_rng(74)
+    shape = (cfg["n_layer"], cfg["n_head_kv"], n_pos, hd)
+    k = rng.standard_normal(shape).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal(shape).astype(np.float16).astype(np.float32)
+    toks = _tokens(40, cfg["n_vocab"], 75)
+    want = _oracle_logits(orc, model, n_ctx, toks, n_pos, (k, v))
+    print(f"[chunk] {widths}: 40 tokens after a {n_pos}-position prefix", flush=True)
+    g = amd.DeviceDecoder(dev, model, n_ctx)
+    try:
+        g.kv_load(k, v, n_pos)
+        got = np.concatenate([g.forward_chunk(toks[:24], n_pos), g.forward_chunk(toks[24:], n_pos + 24)])
+    finally:
+        g.close()
+    assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
+def test_full_2b_chunk_is_bit_exact(amd, orc, dev):
+    """All 30 blocks at BitNet-2B shape, 100 tokens in one chunk (every GEMM
+    on the LDS tile), logits of every position against the oracle."""
+    cfg = dict(amd.BITNET_2B)
+    print("[chunk] building the 2B model", flush=True)
+    model = amd.synth_model(cfg, 5)
+    toks = _tokens(100, cfg["n_vocab"], 76)
+    print("[chunk] oracle, 100 tokens", flush=True)
+    want = _oracle_logits(orc, model, 128, toks)
+    g = amd.DeviceDecoder(dev, model, 128)
+    try:
+        print("[chunk] device chunk of 100", flush=True)
+        got = g.forward_chunk(toks, 0)
+    finally:
+        g.close()
+    assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
+def test_chunk_refuses_what_the_reference_refuses(amd, dev):
+    cfg = dict(TINY, n_layer=1)
+    model = amd.synth_model(cfg, 77)
+    g = amd.DeviceDecoder(dev, model, 600)
+    try:
+        assert g.status_chunk([], 0) == -1                           # n < 1
+        assert g.status_chunk([1] * 513, 0) == -1                    # n above the limit
+        assert g.status_chunk([1, cfg["n_vocab"]], 0) == -1          # token out of range
+        assert g.status_chunk([1, -1], 0) == -1
+        assert g.status_chunk([1, 2], 599) == -1                     # past n_ctx
+        assert g.status_chunk([1, 2, 3], 4) == 0                     # a gap is allowed
+        assert g.n_past() == 7
+        assert g.status_chunk([1, 2], 6) == -1                       # rewinding is not
+        assert g.status_prefill([1, 2], 2) == -1                     # prefill starts at 0: rewinds
+        g.reset()
+        assert g.status_prefill([1, 2], 0) == -1                     # chunk 0
+        assert g.status_prefill([1, 2], 513) == -1                   # chunk above the limit
+        assert g.status_prefill([1] * 601, 4) == -36                 # more tokens than n_ctx
+        assert g.status_prefill([1] * 512, 512) == 0
+        assert g.n_past() == 512
+    finally:
+        g.close()

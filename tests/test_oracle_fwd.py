@@ -279,3 +279,35 @@ def test_state_file_restores_the_reference_cache(amd, orc, tmp_path):
     finally:
         r.close()
         d.close()
+
+
+@needs_ref
+def test_reference_chunks_equal_its_token_path_and_the_oracle(amd, orc):
+    """sllm_forward_chunk / sllm_forward_prefill_chunked of the reference
+    (src/forward.c:589-868) give every position's logits bit for bit as its
+    one-token forward does (the property tests/test_phase5.c:85-150 of the
+    reference asserts), and those are the oracle's token-by-token logits: the
+    target a device chunk is checked against. Chunk sizes below, at and above
+    the sequence; a later chunk attends to keys an earlier one wrote."""
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 17)
+    toks = _tokens(19, cfg["n_vocab"], 18)
+    d = orc.Decoder(model, 32)
+    try:
+        want = np.stack([d.forward(t, p) for p, t in enumerate(toks)])
+    finally:
+        d.close()
+    for chunk in (1, 2, 5, 19, 32):
+        r = orc.RefDecoder(model, 32, threads=2)
+        try:
+            got = r.prefill_chunked(toks, chunk)
+        finally:
+            r.close()
+        assert np.array_equal(bits(got), bits(want)), f"chunk {chunk}"
+    r = orc.RefDecoder(model, 32, threads=2)
+    try:
+        a = r.forward_chunk(toks[:7], 0)
+        b = r.forward_chunk(toks[7:], 7)
+    finally:
+        r.close()
+    assert np.array_equal(bits(np.concatenate([a, b])), bits(want))
