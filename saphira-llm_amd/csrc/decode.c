@@ -799,7 +799,6 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
     const chunk_bufs *B = &c->chk;
     const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
     const uint32_t pos_blocks = (uint32_t) ((base + n + ATT_POS - 1) / ATT_POS);
-    const uint32_t slices = (uint32_t) (m->hd / PV_SLICE);
     int st = SLLM_GFX950_OK;
     for (int32_t il = 0; il < m->n_layer && st == SLLM_GFX950_OK; ++il) {
         const dev_layer *L = &m->layers[il];
@@ -816,10 +815,11 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_kvs, (uint32_t) n, 1, ATT_THREADS, 0, aargs);
         if (st == SLLM_GFX950_OK) {
             st = sllm_shim_launch_3d(c->f_cscores, (uint32_t) m->n_head_kv, pos_blocks, (uint32_t) n,
-                                     ATT_THREADS, aargs);
+                                     ATT_THREADS, 0, aargs);
         }
         if (st == SLLM_GFX950_OK) {
-            st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, slices, (uint32_t) n, ATT_THREADS, aargs);
+            st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, 1, (uint32_t) n, ATT_THREADS,
+                                     (uint32_t) (m->n_head / m->n_head_kv) * c->sc_stride * 4, aargs);
         }
         /* attn_sub_norm, O */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_PLAIN, B->attn, NULL, NULL, L->attn_sub_norm, (uint32_t) e, 1, NULL);

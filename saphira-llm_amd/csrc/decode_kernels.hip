@@ -739,10 +739,6 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_dec_pv(dec_attn A) { pv_body<false>(A); }
 
-// The chunk's softmax and p . V: grid (KV head, 16-dimension slices, token).
-extern "C" __global__ void __launch_bounds__(ATT_THREADS)
-sllm_k_chk_pv(dec_attn A) { pv_body<true>(A); }
-
 // ---------------------------------------------------------------------------
 // output: x = a + b, RMSNorm with output_norm, the F16 rows
 // (src/forward.c:800-827), then the argmax (src/forward.c:876-883) and the
@@ -1123,6 +1119,162 @@ sllm_k_chk_lm_head(chk_lm L) {
             const float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
             L.logits[(size_t) (t0 + (uint32_t) u) * L.n_vocab + row] = (s0 + s1) + (s2 + s3);
         }
+    }
+}
+
+// The chunk's softmax and p . V: workgroup (KV head, token t at position
+// chunk_base + t), wave w = query head w of the KV head.
+//  - Softmax of the head's scores into LDS (src/ops.c:386-422), the same
+//    operations as the decode step's: the max; ggml_v_expf over whole groups
+//    of eight, the C library's expf over the rest; the double sum of the
+//    groups (((e0+e4) + (e1+e5)) + (e2+e6)) + (e3+e7) in any order, checked,
+//    in the reference's order when the check cannot decide; p = e * (1/sum).
+//  - Lane l then owns head dimensions 2l and 2l + 1 and adds p_s * v_s to
+//    each in order of s (src/forward.c:706-726), V rows streaming from L2
+//    two blocks of sixteen positions ahead. Many workgroups share a CU, so
+//    the other waves fill a wave's load latency.
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_chk_pv(dec_attn A) {
+    extern __shared__ __attribute__((aligned(16))) float Pd[];      // [grp][sc_stride]
+    __shared__ uint64_t tab[32];
+    const uint32_t kvh = blockIdx.x, t = blockIdx.z, tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t npast = A.chunk_base + t + 1;
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
+    const uint32_t nb = npast / 8, nt = nb * 8;
+    if (tid < 32) tab[tid] = c_expf_tab[tid];
+    __syncthreads();
+
+    if (wave < grp) {
+        const float *sc = A.scores + (size_t) t * A.n_head * ss + (size_t) (kvh * grp + wave) * ss;
+        float *ph = Pd + (size_t) wave * ss;
+        auto group_sum = [](const float (&e)[8]) {
+            const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
+            const double t2 = (double) e[2] + (double) e[6], t3 = (double) e[3] + (double) e[7];
+            return ((t0 + t1) + t2) + t3;
+        };
+        auto load8 = [&](uint32_t s, float (&v)[8]) {
+            const uint32_t at = min(s, ss - 8);
+            const f32x4 a = *G_CAST(const f32x4, sc + at), b = *G_CAST(const f32x4, sc + at + 4);
+            v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+            v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+        };
+        auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = v[i] - m;
+                v[i] = s + (uint32_t) i < nt ? ggml_v_expf(x) : sllm_libm_expf(x, tab);
+            }
+        };
+        float m = -INFINITY;
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            load8(s, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
+        }
+        m = wave_max(m);
+        double part = 0.0;
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            load8(s, v);
+            exps8(v, s, m);
+            if (s + 8 <= npast) {
+                part += group_sum(v);
+                *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
+                *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
+            } else if (s < npast) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (s + (uint32_t) i < npast) ph[s + (uint32_t) i] = v[i];
+                }
+            }
+        }
+        if (lane < npast - nt) part += (double) sllm_libm_expf(sc[nt + lane] - m, tab);
+        const double sum = wave_sum_d(part);
+        const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
+        float inv = (float) (1.0 / (sum - bound));
+        if (inv != (float) (1.0 / (sum + bound))) {   // uniform over the wave
+            if (lane == 0) {
+                double seq = 0.0;
+                for (uint32_t s = 0; s < nt; s += 8) {
+                    float v[8];
+                    load8(s, v);
+                    exps8(v, s, m);
+                    seq += group_sum(v);
+                }
+                for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
+                inv = (float) (1.0 / seq);
+            }
+            inv = __shfl(inv, 0, 64);
+        }
+        for (uint32_t i = lane; i < npast; i += 64) ph[i] = ph[i] * inv;
+    }
+    __syncthreads();
+    if (wave >= grp) return;
+
+    // p . V: lane l owns dimensions 2l, 2l + 1 (lanes past the head idle)
+    const float *ph = Pd + (size_t) wave * ss;
+    const uint32_t d = min(2 * lane, hd - 2);
+    const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d;
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    f32x2 va[16], vb[16];
+    auto load16 = [&](uint32_t s, f32x2 (&v)[16]) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = *G_CAST(const f32x2, vc + (size_t) min(s + (uint32_t) j, npast - 1) * hd);
+    };
+    float acc0 = 0.0f, acc1 = 0.0f;
+    auto step16 = [&](uint32_t s, const f32x2 (&v)[16]) {
+        float p[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 p4 = *reinterpret_cast<const f32x4 *>(ph + s + 4 * q);
+            p[4 * q] = p4[0]; p[4 * q + 1] = p4[1]; p[4 * q + 2] = p4[2]; p[4 * q + 3] = p4[3];
+        }
+        float r0[16], r1[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            r0[j] = p[j] * v[j][0];
+            r1[j] = p[j] * v[j][1];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            acc0 = acc0 + r0[j];
+            acc1 = acc1 + r1[j];
+        }
+    };
+    auto tail = [&](uint32_t s, uint32_t r, const f32x2 (&v)[16]) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if ((uint32_t) j < r) {
+                const float p = ph[s + (uint32_t) j];
+                acc0 = acc0 + p * v[j][0];
+                acc1 = acc1 + p * v[j][1];
+            }
+        }
+    };
+    load16(0, va);
+    load16(16, vb);
+    uint32_t s = 0;
+    for (; s + 32 <= npast; s += 32) {
+        step16(s, va);
+        load16(s + 32, va);
+        step16(s + 16, vb);
+        load16(s + 48, vb);
+    }
+    const uint32_t r = npast - s;
+    if (r >= 16) {
+        step16(s, va);
+        tail(s + 16, r - 16, vb);
+    } else {
+        tail(s, r, va);
+    }
+    if (2 * lane < hd) {
+        float *out = A.out + (size_t) t * A.n_head * hd + (size_t) (kvh * grp + wave) * hd + 2 * lane;
+        out[0] = acc0;
+        out[1] = acc1;
     }
 }
 

@@ -445,9 +445,10 @@ int sllm_shim_launch(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t block, 
     return SLLM_GFX950_OK;
 }
 
-int sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, void **args) {
+int sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, uint32_t lds,
+                        void **args) {
     if (gx == 0 || gy == 0 || gz == 0) return SLLM_GFX950_OK;
-    HIP_TRY(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, 0, g.stream, args, NULL));
+    HIP_TRY(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, lds, g.stream, args, NULL));
     return SLLM_GFX950_OK;
 }
 

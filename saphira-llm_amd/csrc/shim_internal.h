@@ -65,6 +65,6 @@ SLLM_HIDDEN int         sllm_shim_decode_function(const char *name, hipFunction_
 SLLM_HIDDEN int         sllm_shim_launch(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t block,
                                          uint32_t lds, void **args);
 SLLM_HIDDEN int         sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz,
-                                            uint32_t block, void **args);
+                                            uint32_t block, uint32_t lds, void **args);
 
 #endif /* SLLM_SHIM_INTERNAL_H */
