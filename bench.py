@@ -257,6 +257,51 @@ def measure_decode(amd, dev, tokens=128, warm=8, graph=True):
     }
 
 
+PREFILL_TOKENS = 512
+PREFILL_CHECK = 16
+
+
+def measure_prefill(amd, dev, model, reps=5):
+    """The chunked forward at BitNet-2B shape: PREFILL_TOKENS tokens as one
+    chunk from position 0 (every projection one int8-MFMA GEMM over the
+    chunk), timed with HIP events on the library stream -- with the output
+    head for the last token only (a prompt's prefill), and for every token
+    (sllm_forward_chunk's full output, its copy to host memory included).
+    Rows 0..PREFILL_CHECK-1 of the full output go to the CPU leg's bit-exact
+    check."""
+    cfg = dict(amd.BITNET_2B)
+    n = PREFILL_TOKENS
+    toks = [int(t) for t in np.random.default_rng(90).integers(0, cfg["n_vocab"], n)]
+    g = amd.DeviceDecoder(dev, model, n + 8)
+    res = {}
+    for label, logits in (("last", False), ("all", True)):
+        best = None
+        for _ in range(reps):
+            g.reset()
+            dev.events(2)
+            dev.sync()
+            dev.record(0)
+            g.forward_chunk(toks, 0, logits=logits)
+            dev.record(1)
+            dev.sync()
+            ms = dev.elapsed(0, 1)
+            best = ms if best is None or ms < best else best
+        res[label] = best
+    g.reset()
+    full = g.forward_chunk(toks, 0, logits=True)
+    g.close()
+    check = {"model": model, "tokens": toks[:PREFILL_CHECK], "logits": full[:PREFILL_CHECK].copy()}
+    return check, {
+        "workload": (f"random-init BitNet-b1.58-2B, one chunk of {n} tokens at positions 0..{n - 1} "
+                     f"(sllm_gfx950_forward_chunk), batch 1"),
+        "tokens": n,
+        "ms_last_logits": round(res["last"], 3),
+        "tokens_per_s": round(n / (res["last"] * 1e-3), 1),
+        "ms_all_logits_incl_host_copy": round(res["all"], 3),
+        "all_logits_tokens_per_s": round(n / (res["all"] * 1e-3), 1),
+    }
+
+
 PEAK_INT8_TOPS = 5000.0
 GEMM_SETS = 64
 
@@ -393,6 +438,37 @@ def cpu_decode(dec_check, seconds=10.0, threads=16):
                                      "sample": f"sllm_forward greedy from position {DECODE_PREFIX} after the same prefix"}}
 
 
+def cpu_prefill(pre_check, seconds=10.0, threads=16):
+    """Checker: rows 0..15 of the chunk's logits against the oracle's
+    token-by-token logits, bit for bit. Baseline: the reference's own
+    sllm_forward_prefill_chunked (oracle/_ref) on the same model and tokens,
+    chunks of 16, as many chunks as fit in about `seconds` on `threads`
+    threads of this host."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    c = pre_check
+    model = c["model"]
+    o = orc.Decoder(model, PREFILL_CHECK + 8)
+    want = np.stack([o.forward(t, p) for p, t in enumerate(c["tokens"])])
+    o.close()
+    if not np.array_equal(want.view(np.uint32), np.ascontiguousarray(c["logits"], np.float32).view(np.uint32)):
+        raise SystemExit("bench: the GPU chunk's logits differ from the oracle")
+    log(f"prefill chunk: logits of positions 0..{PREFILL_CHECK - 1} match the oracle bit for bit")
+    if not orc.ref_available():
+        return {"checked": True, "cpu": None}
+    toks = np.asarray(c["tokens"] * (PREFILL_TOKENS // PREFILL_CHECK), np.int32)
+    r = orc.RefDecoder(model, PREFILL_TOKENS + 8, threads=threads)
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and done + 16 <= PREFILL_TOKENS:
+        r.forward_chunk(toks[done:done + 16], done)
+        done += 16
+    dt = time.perf_counter() - t0
+    r.close()
+    return {"checked": True, "cpu": {"tokens_per_s": round(done / dt, 2), "tokens": done, "seconds": round(dt, 1),
+                                     "threads": threads, "kind": "reference",
+                                     "sample": "sllm_forward_chunk, chunks of 16 from position 0, every token's logits"}}
+
+
 def cpu_gemm_check(checks):
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
@@ -506,8 +582,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="decode leg: enqueue each token's launches instead of replaying a HIP graph "
                          "(rocprofv3's kernel tracer does not survive graph replay)")
-    ap.add_argument("--legs", default="gemv,block,decode,gemm",
-                    help="comma-separated legs to run beside the headline GEMV (block, decode, gemm); "
+    ap.add_argument("--legs", default="gemv,block,decode,prefill,gemm",
+                    help="comma-separated legs to run beside the headline GEMV (block, decode, prefill, gemm); "
                          "for profiling one leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -557,6 +633,7 @@ def main():
     checks = wl.outputs([0, wl.sets - 1])
     legs = set(args.legs.split(","))
     block_checks, block30, dec_check, decode, gemm_checks, gemm = [], None, None, None, [], None
+    pre_check, prefill = None, None
     if "block" in legs:
         block_checks, block30 = measure_block_plan(amd, dev)
         log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
@@ -564,6 +641,11 @@ def main():
         dec_check, decode = measure_decode(amd, dev, graph=not args.no_graph)
         log(f"decode: {decode['tokens_per_s']} tokens/s ({decode['us_per_token']} us per token, "
             f"{decode['effective_GBps']} GB/s effective)")
+    if "prefill" in legs:
+        pre_model = dec_check["model"] if dec_check is not None else amd.synth_model(dict(amd.BITNET_2B), 0)
+        pre_check, prefill = measure_prefill(amd, dev, pre_model)
+        log(f"prefill: {prefill['tokens']}-token chunk {prefill['ms_last_logits']} ms "
+            f"({prefill['tokens_per_s']} tokens/s); with every token's logits {prefill['ms_all_logits_incl_host_copy']} ms")
     if "gemm" in legs:
         gemm_checks, gemm = measure_gemm(amd, dev)
 
@@ -590,6 +672,7 @@ def main():
         "calibration": calib,
         "block30": block30,
         "decode": decode,
+        "prefill": prefill,
         "gemm": gemm,
     }
     if not args.no_cpu:
@@ -600,6 +683,10 @@ def main():
             dec = cpu_decode(dec_check, seconds=args.cpu_seconds)
             out["decode"]["parity"] = "logits, int32 dots and activations of the first token bit-identical to the oracle"
             out["decode"]["cpu_baseline"] = dec["cpu"]
+        if pre_check is not None:
+            pre = cpu_prefill(pre_check, seconds=args.cpu_seconds)
+            out["prefill"]["parity"] = f"logits of positions 0..{PREFILL_CHECK - 1} bit-identical to the oracle"
+            out["prefill"]["cpu_baseline"] = pre["cpu"]
     print(json.dumps(out), flush=True)
 
 
