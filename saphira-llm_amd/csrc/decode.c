@@ -109,7 +109,7 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 /* kernel constants (decode_kernels.hip) */
 #define ATT_THREADS 256
 #define ATT_POS     64
-#define PV_SLICE    16
+#define PV_SLICE    8
 #define LM_THREADS  256
 #define LM_ROWS     64
 #define LM_MAX_E    8192

@@ -396,11 +396,18 @@ constexpr uint32_t ATT_MAX_HD = 128;
 constexpr uint32_t ATT_MAX_GRP = 4;     // query heads per KV head
 constexpr uint32_t KT_STRIDE = ATT_MAX_HD + 4;     // LDS key row: 16-byte aligned, rows 4 banks apart
 constexpr int KT_LOADS = ATT_POS * ATT_MAX_HD / 4 / ATT_THREADS;   // float4 per thread
-constexpr uint32_t PV_SLICE = 16;       // head dimensions per p.V workgroup
-constexpr uint32_t PV_RPOS = 1536;      // positions of p and V staged in LDS per round
-constexpr uint32_t PV_VSTRIDE = PV_RPOS + 4;
-constexpr int PV_VLOADS = (int) (PV_RPOS * PV_SLICE / 4 / ATT_THREADS);   // float4 of V per thread
+constexpr uint32_t PV_SLICE = 8;       // head dimensions per p.V workgroup
+constexpr uint32_t PV_RPOS = 1536;      // positions of p (LDS) and V (registers) per round
+constexpr uint32_t PV_SUB = 192;        // positions per product sub-round
+constexpr uint32_t PV_XSTRIDE = PV_SUB + 4;                // LDS product row: rows 4 banks apart
+constexpr int PV_PTHREADS = ATT_THREADS - 64;              // producer threads (waves 1..3)
+constexpr int PV_VLOADS = (int) (PV_RPOS * PV_SLICE / 4 / PV_PTHREADS);   // float4 of V per producer
+constexpr int PV_VSUB = (int) (PV_SUB * PV_SLICE / 4 / PV_PTHREADS);      // of them per sub-round
+constexpr uint32_t PV_G4 = PV_SLICE / 4;                   // float4 per position of a slice
 static_assert(ATT_MAX_GRP * PV_SLICE <= 64, "one chain wave");
+static_assert(PV_VLOADS * PV_PTHREADS * 4 == (int) (PV_RPOS * PV_SLICE), "whole float4 per producer");
+static_assert(PV_VSUB * PV_PTHREADS * 4 == (int) (PV_SUB * PV_SLICE) && PV_RPOS % PV_SUB == 0, "sub-rounds");
+static_assert(PV_PTHREADS % PV_G4 == 0, "a producer keeps its dimensions");
 
 // NeoX RoPE (src/ops.c:467-549) of element d of a head vector: pairs
 // (e, e + half) rotate by angle e, x[e] -> x[e] c - x[e+half] s and
@@ -554,13 +561,17 @@ sllm_k_chk_scores(dec_attn A) { scores_body<true>(A); }
 //    inv = 1/sum narrowed to f32; p = e * inv. Each lane holds groups of
 //    eight consecutive scores, so a group's sum never leaves its lane, and
 //    the first round's e go to LDS in the same pass.
-//  - Per round of 1536 positions, p and V (transposed) in LDS; wave 0, one
-//    lane per (head, dimension), adds p_s * v_s to its accumulator in order
-//    of s (src/forward.c:706-726), its LDS reads sixteen positions ahead.
+//  - Per round of 1536 positions, p in LDS and the slice of V in the
+//    registers of waves 1..3 (32 float4 per thread, issued before the
+//    softmax). In sub-rounds of 192 positions those waves form the products
+//    p_s * v_s of every (head, dimension) into one of two LDS buffers, while
+//    wave 0, one lane per (head, dimension), adds the previous sub-round's
+//    products to its accumulator in order of s (src/forward.c:706-726) --
+//    the chain wave issues adds and reads only.
 template <bool CHUNK>
 __device__ __forceinline__ void pv_body(const dec_attn &A) {
     __shared__ __attribute__((aligned(16))) float P[ATT_MAX_GRP][PV_RPOS];
-    __shared__ __attribute__((aligned(16))) float Vt[PV_SLICE][PV_VSTRIDE];
+    __shared__ __attribute__((aligned(16))) float X[2][ATT_MAX_GRP * PV_SLICE][PV_XSTRIDE];
     __shared__ float stat_inv[ATT_MAX_GRP], stat_m[ATT_MAX_GRP];
     __shared__ uint64_t tab[32];          // the expf table, next to the lanes that index it
     const uint32_t kvh = blockIdx.x, d0 = blockIdx.y * PV_SLICE, tid = threadIdx.x;
@@ -571,21 +582,6 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
     const float *scores = A.scores + (size_t) t * A.n_head * ss;
     const uint32_t nb = npast / 8, nt = nb * 8;
     const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d0;
-
-    // thread t holds float4 f = t + 256 u of a round: position f / 4,
-    // dimensions 4 (f % 4) .. + 3 of the slice
-    f32x4 vr[PV_VLOADS];
-    auto load_v = [&](uint32_t base) {
-#pragma unroll
-        for (int u = 0; u < PV_VLOADS; ++u) {
-            const uint32_t f = tid + (uint32_t) u * ATT_THREADS;
-            const uint32_t sp = min(base + f / 4, npast - 1);
-            vr[u] = *G_CAST(const f32x4, vc + (size_t) sp * hd + 4 * (f % 4));
-        }
-    };
-    load_v(0);
-    if (tid < 32) tab[tid] = c_expf_tab[tid];
-    __syncthreads();
 
     auto group_sum = [](const float (&e)[8]) {
         const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
@@ -600,39 +596,92 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
         v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
         v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
     };
-    // e of the group at s (lanes whose group reaches into the tail take the
-    // C library's expf there)
+    // e of the group at s: ggml_v_expf for a whole group, the C library's
+    // expf for the tail group (s and nt are multiples of eight, so a group
+    // lies wholly on one side; a branch, so that only the tail's lane runs
+    // the double-precision path)
     auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
+        if (s < nt) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float x = v[i] - m;
-            v[i] = s + (uint32_t) i < nt ? ggml_v_expf(x) : sllm_libm_expf(x, tab);
+            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
         }
     };
+    // one round (npast <= 1536): each softmax wave's scores are loaded
+    // first, all at once, ahead of V, and stay in registers
+    constexpr int RG = (int) (PV_RPOS / 512);
+    const bool one_round = npast <= PV_RPOS;
+    float sv[RG][8];
+    if (one_round && wave < grp) {
+        const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
+#pragma unroll
+        for (int g = 0; g < RG; ++g) load8(sc, 512u * (uint32_t) g + 8 * lane, sv[g]);
+    }
+
+    // producer pt = tid - 64 holds float4 f = pt + 192 u of a round:
+    // position f / G4, dimensions 4 (pt % G4) .. + 3 of the slice (G4 =
+    // float4 per position); its float4 G4 j .. G4 j + G4 - 1 are sub-round j
+    const uint32_t pt = tid - 64u;
+    f32x4 vr[PV_VLOADS];
+    auto load_v = [&](uint32_t base) {
+#pragma unroll
+        for (int u = 0; u < PV_VLOADS; ++u) {
+            const uint32_t f = pt + (uint32_t) u * PV_PTHREADS;
+            const uint32_t sp = min(base + f / PV_G4, npast - 1);
+            vr[u] = *G_CAST(const f32x4, vc + (size_t) sp * hd + 4 * (f % PV_G4));
+        }
+    };
+    if (wave > 0) load_v(0);
+    if (tid < 32) tab[tid] = c_expf_tab[tid];
+    __syncthreads();
+
     if (wave < grp) {
         const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
         float *ph = P[wave];
         float m = -INFINITY;
-        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
-            float v[8];
-            const uint32_t s = b0 + 8 * lane;
-            load8(sc, s, v);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
-        }
-        m = wave_max(m);
-        // e (of the first round into LDS) and the sum of whole groups; the
-        // tail positions, one lane each
         double part = 0.0;
-        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
-            float v[8];
-            const uint32_t s = b0 + 8 * lane;
-            load8(sc, s, v);
-            exps8(v, s, m);
-            if (s + 8 <= npast) part += group_sum(v);
-            if (s < PV_RPOS) {
-                *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
-                *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
+        if (one_round) {
+            float (&v)[RG][8] = sv;
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                const uint32_t s = 512u * (uint32_t) g + 8 * lane;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[g][i] : -INFINITY);
+            }
+            m = wave_max(m);
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                const uint32_t s = 512u * (uint32_t) g + 8 * lane;
+                if (s < npast) {
+                    exps8(v[g], s, m);
+                    if (s + 8 <= npast) part += group_sum(v[g]);
+                    *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[g][0], v[g][1], v[g][2], v[g][3] };
+                    *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[g][4], v[g][5], v[g][6], v[g][7] };
+                }
+            }
+        } else {
+            for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+                float v[8];
+                const uint32_t s = b0 + 8 * lane;
+                load8(sc, s, v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
+            }
+            m = wave_max(m);
+            // e (of the first round into LDS) and the sum of whole groups; the
+            // tail positions, one lane each
+            for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+                float v[8];
+                const uint32_t s = b0 + 8 * lane;
+                load8(sc, s, v);
+                exps8(v, s, m);
+                if (s + 8 <= npast) part += group_sum(v);
+                if (s < PV_RPOS) {
+                    *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
+                    *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
+                }
             }
         }
         if (lane < npast - nt) part += (double) sllm_libm_expf(sc[nt + lane] - m, tab);
@@ -666,16 +715,37 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
         }
     }
 
-    // rounds of 1536 positions
+    // rounds of 1536 positions, sub-rounds of 192
     const bool chain = wave == 0 && lane < grp * PV_SLICE;
-    const float *ph = P[lane / PV_SLICE];
-    const float *vt = Vt[lane % PV_SLICE];
+    const uint32_t d4 = 4u * (pt % PV_G4);
+    // products of sub-round j (positions 192 j ..) into X[buf]
+    auto produce = [&](uint32_t j, int buf) {
+        float pw[PV_VSUB][ATT_MAX_GRP];           // every p read first, then the products
+#pragma unroll
+        for (int u = 0; u < PV_VSUB; ++u) {
+            const uint32_t sl = (pt + (uint32_t) u * PV_PTHREADS) / PV_G4;
+#pragma unroll
+            for (int h = 0; h < (int) ATT_MAX_GRP; ++h) pw[u][h] = P[min((uint32_t) h, grp - 1)][PV_SUB * j + sl];
+        }
+#pragma unroll
+        for (int u = 0; u < PV_VSUB; ++u) {
+            const f32x4 v = vr[(int) (PV_VSUB * j) + u];     // j is a constant after unrolling
+            const uint32_t sl = (pt + (uint32_t) u * PV_PTHREADS) / PV_G4;
+#pragma unroll
+            for (int h = 0; h < (int) ATT_MAX_GRP; ++h) {
+                if ((uint32_t) h < grp) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) X[buf][(uint32_t) h * PV_SLICE + d4 + (uint32_t) e][sl] = pw[u][h] * v[e];
+                }
+            }
+        }
+    };
     float acc = 0.0f;
     for (uint32_t base = 0; base < npast; base += PV_RPOS) {
         const uint32_t n = min(PV_RPOS, npast - base);
         if (base > 0) {
-            __syncthreads();                      // stat_* visible; the last round's reads done
-            load_v(base);
+            __syncthreads();                      // stat_* visible; the last round's products read
+            if (wave > 0) load_v(base);
             if (wave < grp) {                     // p of this round, recomputed (the same bits)
                 const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
                 const float m = stat_m[wave], inv = stat_inv[wave];
@@ -691,46 +761,58 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 }
             }
         }
-#pragma unroll
-        for (int u = 0; u < PV_VLOADS; ++u) {
-            const uint32_t f = tid + (uint32_t) u * ATT_THREADS, r = f / 4, c4 = f % 4;
-            if (r < n) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) Vt[4 * c4 + (uint32_t) e][r] = vr[u][e];
-            }
-        }
+        __syncthreads();                          // this round's p in LDS
+        const uint32_t n_sub = (n + PV_SUB - 1) / PV_SUB;
+        if (wave > 0) produce(0, 0);
         __syncthreads();
-        if (chain) {
-            // sixteen positions per step, the next step's reads in flight
-            f32x4 pa[4], va[4], pb[4], vb[4];
-            auto rd = [&](uint32_t at, f32x4 (&pp)[4], f32x4 (&vv)[4]) {
-                const uint32_t c = min(at, PV_RPOS - 16);
+        // unrolled whole, so that the producers' register indices are constants
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    pp[t] = *reinterpret_cast<const f32x4 *>(ph + c + 4 * t);
-                    vv[t] = *reinterpret_cast<const f32x4 *>(vt + c + 4 * t);
+        for (uint32_t j = 0; j < PV_RPOS / PV_SUB; ++j) {
+            if (j >= n_sub) break;                // uniform
+            if (wave == 0) {
+                if (chain) {
+                    const float *x = X[j & 1u][lane];
+                    const uint32_t cnt = min(PV_SUB, n - PV_SUB * j);
+                    // sixteen products per block, three blocks in a ring: the
+                    // reads for block s + 32 are in flight while block s is added
+                    f32x4 qa[4], qb[4], qc[4];
+                    auto rd = [&](uint32_t at, f32x4 (&q)[4]) {
+                        const uint32_t c = min(at, PV_SUB - 16);
+#pragma unroll
+                        for (int t4 = 0; t4 < 4; ++t4) q[t4] = *reinterpret_cast<const f32x4 *>(x + c + 4 * t4);
+                    };
+                    auto add16 = [&](const f32x4 (&q)[4]) {
+#pragma unroll
+                        for (int t4 = 0; t4 < 4; ++t4) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc = acc + q[t4][e];
+                        }
+                    };
+                    uint32_t s = 0;
+                    rd(0, qa);
+                    rd(16, qb);
+                    for (; s + 48 <= cnt; s += 48) {
+                        rd(s + 32, qc);
+                        add16(qa);
+                        rd(s + 48, qa);
+                        add16(qb);
+                        rd(s + 64, qb);
+                        add16(qc);
+                    }
+                    if (s + 16 <= cnt) {
+                        add16(qa);
+                        s += 16;
+                        if (s + 16 <= cnt) {
+                            add16(qb);
+                            s += 16;
+                        }
+                    }
+                    for (; s < cnt; ++s) acc = acc + x[s];
                 }
-            };
-            auto add16 = [&](const f32x4 (&pp)[4], const f32x4 (&vv)[4]) {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc = acc + pp[t][e] * vv[t][e];
-                }
-            };
-            uint32_t s = 0;
-            rd(0, pa, va);
-            for (; s + 32 <= n; s += 32) {
-                rd(s + 16, pb, vb);
-                add16(pa, va);
-                rd(s + 32, pa, va);
-                add16(pb, vb);
+            } else if (j + 1 < n_sub) {
+                produce(j + 1, (int) ((j + 1) & 1u));
             }
-            if (s + 16 <= n) {
-                add16(pa, va);
-                s += 16;
-            }
-            for (; s < n; ++s) acc = acc + ph[s] * vt[s];
+            __syncthreads();
         }
     }
     if (chain) A.out[(size_t) t * A.n_head * hd + (size_t) (kvh * grp + lane / PV_SLICE) * hd + d0 + lane % PV_SLICE] = acc;
@@ -1159,11 +1241,13 @@ sllm_k_chk_pv(dec_attn A) {
             v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
             v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
         };
-        auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
+        auto exps8 = [&](float (&v)[8], uint32_t s, float m) {   // as in the decode kernel
+            if (s < nt) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = v[i] - m;
-                v[i] = s + (uint32_t) i < nt ? ggml_v_expf(x) : sllm_libm_expf(x, tab);
+                for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
             }
         };
         float m = -INFINITY;
