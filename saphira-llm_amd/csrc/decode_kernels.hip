@@ -76,12 +76,12 @@ __device__ __forceinline__ float ggml_v_expf(float x) {
     const float j = fmaf(fmaf(fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u,
                               fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
                          u, 0x1.ffffecp-1f * b);
-    if (!(fabsf(n) > 126.0f)) return fmaf(j, k, k);
+    // the three results, then a select: no branch per element
     const uint32_t g = n <= 0.0f ? 0x82000000u : 0u;
     const float s1 = __uint_as_float(g + 0x7f000000u);
     const float s2 = __uint_as_float(e - g);
-    if (fabsf(n) > 192.0f) return s1 * s1;
-    return fmaf(s2, j, s2) * s1;
+    const float in_range = fmaf(j, k, k), scaled = fmaf(s2, j, s2) * s1, extreme = s1 * s1;
+    return !(fabsf(n) > 126.0f) ? in_range : (fabsf(n) > 192.0f ? extreme : scaled);
 }
 
 __constant__ uint64_t c_expf_tab[32] = SLLM_EXPF_TAB_INIT;
@@ -656,7 +656,14 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 const uint32_t s = 512u * (uint32_t) g + 8 * lane;
                 if (s < npast) {
                     exps8(v[g], s, m);
-                    if (s + 8 <= npast) part += group_sum(v[g]);
+                    if (s + 8 <= npast) {
+                        part += group_sum(v[g]);
+                    } else {                      // the tail, from the lane's own registers
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            if (s + (uint32_t) i < npast) part += (double) v[g][i];
+                        }
+                    }
                     *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[g][0], v[g][1], v[g][2], v[g][3] };
                     *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[g][4], v[g][5], v[g][6], v[g][7] };
                 }
@@ -677,14 +684,20 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 const uint32_t s = b0 + 8 * lane;
                 load8(sc, s, v);
                 exps8(v, s, m);
-                if (s + 8 <= npast) part += group_sum(v);
+                if (s + 8 <= npast) {
+                    part += group_sum(v);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        if (s + (uint32_t) i < npast) part += (double) v[i];
+                    }
+                }
                 if (s < PV_RPOS) {
                     *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
                     *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
                 }
             }
         }
-        if (lane < npast - nt) part += (double) sllm_libm_expf(sc[nt + lane] - m, tab);
         const double sum = wave_sum_d(part);
         const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
         float inv = (float) (1.0 / (sum - bound));
@@ -791,12 +804,17 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                     uint32_t s = 0;
                     rd(0, qa);
                     rd(16, qb);
+                    // (sched_barrier: the reads stay where they are issued, ahead
+                    // of the adds they overlap)
                     for (; s + 48 <= cnt; s += 48) {
                         rd(s + 32, qc);
+                        __builtin_amdgcn_sched_barrier(0);
                         add16(qa);
                         rd(s + 48, qa);
+                        __builtin_amdgcn_sched_barrier(0);
                         add16(qb);
                         rd(s + 64, qb);
+                        __builtin_amdgcn_sched_barrier(0);
                         add16(qc);
                     }
                     if (s + 16 <= cnt) {
@@ -1269,14 +1287,16 @@ sllm_k_chk_pv(dec_attn A) {
                 part += group_sum(v);
                 *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
                 *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
-            } else if (s < npast) {
+            } else if (s < npast) {                   // the tail: stored and added one by one
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    if (s + (uint32_t) i < npast) ph[s + (uint32_t) i] = v[i];
+                    if (s + (uint32_t) i < npast) {
+                        ph[s + (uint32_t) i] = v[i];
+                        part += (double) v[i];
+                    }
                 }
             }
         }
-        if (lane < npast - nt) part += (double) sllm_libm_expf(sc[nt + lane] - m, tab);
         const double sum = wave_sum_d(part);
         const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
         float inv = (float) (1.0 / (sum - bound));
