@@ -210,14 +210,31 @@ void sllm_gfx950_plan_destroy(sllm_gfx950_plan *plan);
 int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
                      const sllm_gfx950_act *act, size_t m, float *out, int32_t *rows_out);
 
+/* One tensor of sllm_gfx950_gemm_multi: its packed weights and outputs, as
+ * the arguments of sllm_gfx950_gemm. */
+typedef struct sllm_gfx950_gemm_job {
+    const uint8_t *w;
+    size_t         n_rows;
+    float         *out;        /* [m][n_rows] epilogue, or NULL */
+    int32_t       *rows_out;   /* [m][n_rows] raw dots, or NULL (not both) */
+} sllm_gfx950_gemm_job;
+
+/* Up to three tensors of width n against the same m quantised rows in one
+ * launch -- the reference's Q / K / V, or gate / up, of every token of a
+ * chunk over one quantised activation (src/forward.c:645-665, :756-773).
+ * Each job's outputs are what sllm_gfx950_gemm writes for it. */
+int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t n, const int8_t *q,
+                           const sllm_gfx950_act *act, size_t m);
+
 /* Quantise m rows of x (m x n f32, one scale/sum per row, as
  * sllm_gfx950_quant_act) into q / act, then sllm_gfx950_gemm: two launches. */
 int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const float *x, size_t m,
                              int8_t *q, sllm_gfx950_act *act, float *out, int32_t *rows_out);
 
-/* GEMM tile override for tuning and tests: 0 automatic (by m), 1: 16 tokens
- * x 16 rows per workgroup (K split over its waves), 2: 32 x 128, 3: 64 x 128,
- * 4: 128 x 128 staged through LDS (K % 256 == 0; tile 3 otherwise). */
+/* GEMM tile override for tuning and tests: 0 automatic (by m and the grid),
+ * 1: 16 tokens x 16 rows per workgroup (K split over its waves), 2: 32 x 128,
+ * 3: 64 x 128, 4: 128 x 128 staged through two LDS buffers, 5: the same
+ * through one buffer (4 and 5 need K % 256 == 0; tile 3 otherwise). */
 int sllm_gfx950_set_gemm_tile(int tile);
 
 /* Launch-geometry override for tuning sweeps and tests; affects launches

@@ -57,6 +57,11 @@ class LayerDesc(ctypes.Structure):
                                         "attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm")]
 
 
+class GemmJob(ctypes.Structure):
+    """sllm_gfx950_gemm_job: one tensor of a multi-tensor GEMM."""
+    _fields_ = [("w", c_void_p), ("n_rows", c_size_t), ("out", c_void_p), ("rows_out", c_void_p)]
+
+
 class ModelDesc(ctypes.Structure):
     """sllm_gfx950_model_desc."""
     _fields_ = [("n_layer", c_int32), ("n_embd", c_int32), ("n_ff", c_int32), ("n_head", c_int32),
@@ -115,6 +120,7 @@ PROTOTYPES = {
     "sllm_gfx950_linear_batch": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p, c_void_p,
                                          c_void_p, c_void_p]),
     "sllm_gfx950_set_gemm_tile": (c_int, [c_int]),
+    "sllm_gfx950_gemm_multi": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t]),
     "sllm_gfx950_model_upload": (c_int, [POINTER(ModelDesc), POINTER(c_void_p)]),
     "sllm_gfx950_model_free": (None, [c_void_p]),
     "sllm_gfx950_model_load_gguf": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),
@@ -315,6 +321,11 @@ class Device:
 
     def gemm(self, w, n_rows, n, q, act, m, out, rows_out=None):
         check(self.lib.sllm_gfx950_gemm(w, n_rows, n, q, act, m, out, rows_out), "gemm")
+
+    def gemm_multi(self, jobs, n, q, act, m):
+        """jobs: (w, n_rows, out, rows_out) device pointers per tensor (1 to 3)."""
+        arr = (GemmJob * len(jobs))(*[GemmJob(w, n_rows, out, ro) for w, n_rows, out, ro in jobs])
+        check(self.lib.sllm_gfx950_gemm_multi(arr, len(jobs), n, q, act, m), "gemm_multi")
 
     def linear_batch(self, w, n_rows, n, x, m, q, act, out, rows_out=None):
         check(self.lib.sllm_gfx950_linear_batch(w, n_rows, n, x, m, q, act, out, rows_out), "linear_batch")

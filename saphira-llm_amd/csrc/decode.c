@@ -793,7 +793,8 @@ static int prep(sllm_gfx950_ctx *c, int32_t n, uint32_t mode, const void *a, con
  * projection one MFMA GEMM over the n quantised rows. all_logits: the output
  * head for every token into chk.logits (and the last row into c->logits);
  * otherwise for the last token only, straight into c->logits. Either way the
- * last row's argmax lands in the step record. */
+ * last row's argmax lands in the step record. Q, K and V are one launch,
+ * gate and up another (sllm_gfx950_gemm_multi). */
 static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_logits) {
     const struct sllm_gfx950_model *m = c->m;
     const chunk_bufs *B = &c->chk;
@@ -805,9 +806,11 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         /* l_out of the layer below (cproj + cffn_inp), or the embedding; attn_norm */
         st = il == 0 ? prep(c, n, IN_EMBED, m->tok_embd, NULL, B->x, L->attn_norm, (uint32_t) e, 1, NULL)
                      : prep(c, n, IN_RESID, B->proj, B->fi, B->x, L->attn_norm, (uint32_t) e, 1, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_Q], e, e, B->q8, B->act, (size_t) n, B->q, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_K], g, e, B->q8, B->act, (size_t) n, B->k, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_V], g, e, B->q8, B->act, (size_t) n, B->v, NULL);
+        if (st == SLLM_GFX950_OK) {
+            const sllm_gfx950_gemm_job qkv[3] = { { L->w[P_Q], e, B->q, NULL }, { L->w[P_K], g, B->k, NULL },
+                                                  { L->w[P_V], g, B->v, NULL } };
+            st = sllm_gfx950_gemm_multi(qkv, 3, e, B->q8, B->act, (size_t) n);
+        }
         k_dec_attn A = c->attn_args[il];
         A.q = B->q; A.k = B->k; A.v = B->v; A.scores = B->scores; A.out = B->attn;
         A.chunk_base = (uint32_t) base;
@@ -826,8 +829,10 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_O], e, e, B->q8, B->act, (size_t) n, B->proj, NULL);
         /* ffn_inp = attn_out + inpSA; ffn_norm; gate, up */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_RESID, B->proj, B->x, B->fi, L->ffn_norm, (uint32_t) e, 1, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_GATE], f, e, B->q8, B->act, (size_t) n, B->g, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_UP], f, e, B->q8, B->act, (size_t) n, B->u, NULL);
+        if (st == SLLM_GFX950_OK) {
+            const sllm_gfx950_gemm_job gu[2] = { { L->w[P_GATE], f, B->g, NULL }, { L->w[P_UP], f, B->u, NULL } };
+            st = sllm_gfx950_gemm_multi(gu, 2, e, B->q8, B->act, (size_t) n);
+        }
         /* silu(gate) * up, ffn_sub_norm, down */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_SILU, B->g, B->u, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL);
         if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_DOWN], e, f, B->q8, B->act, (size_t) n, B->proj, NULL);

@@ -118,7 +118,7 @@ static struct {
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
-    hipFunction_t  k_gemm[4];
+    hipFunction_t  k_gemm[5];
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -200,6 +200,7 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[1], g.mod, "sllm_k_gemm_mfma_2x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[2], g.mod, "sllm_k_gemm_mfma_4x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[3], g.mod, "sllm_k_gemm_mfma_l128"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[4], g.mod, "sllm_k_gemm_mfma_l128s"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
@@ -922,24 +923,79 @@ int sllm_gfx950_gemv_epilogue(const uint8_t *w, size_t n_rows, size_t n, const i
 /* ------------------------------------------------------------------ */
 
 typedef struct k_gemm_args {
-    const uint8_t         *w;
     const int8_t          *q;
     const sllm_gfx950_act *act;
-    float                 *out;
-    int32_t               *out_i;
-    uint32_t               n_rows, k, m, pad;
+    const uint8_t         *w[3];
+    float                 *out[3];
+    int32_t               *out_i[3];
+    uint32_t               n_rows[3];
+    uint32_t               tiles[3];
+    uint32_t               k, m, n_jobs, pad;
 } k_gemm_args;
 
-_Static_assert(sizeof(k_gemm_args) == 56, "k_gemm_args must match gemm_args in i2s_kernels.hip");
+_Static_assert(sizeof(k_gemm_args) == 128, "k_gemm_args must match gemm_args in i2s_kernels.hip");
 
 /* tile shapes per workgroup: tokens x rows (shape 0 splits K over its four
- * waves instead of spreading them along the rows; shape 3 stages its tile
- * through LDS and needs K % 256 == 0) */
-static const uint32_t k_gemm_tokens[4] = { 16, 32, 64, 128 }, k_gemm_rows[4] = { 16, 128, 128, 128 };
+ * waves instead of spreading them along the rows; shapes 3 and 4 stage their
+ * tile through LDS and need K % 256 == 0 -- 3 with two buffers, one
+ * workgroup per CU; 4 with one, two per CU) */
+#define N_GEMM_TILES 5
+static const uint32_t k_gemm_tokens[N_GEMM_TILES] = { 16, 32, 64, 128, 128 };
+static const uint32_t k_gemm_rows[N_GEMM_TILES] = { 16, 128, 128, 128, 128 };
 
 int sllm_gfx950_set_gemm_tile(int tile) {
-    if (tile < 0 || tile > 4) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. 4");
+    if (tile < 0 || tile > N_GEMM_TILES) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. %d", N_GEMM_TILES);
     g.force_gemm_tile = tile;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t n, const int8_t *q,
+                           const sllm_gfx950_act *act, size_t m) {
+    NEED_OPEN();
+    if (jobs == NULL || n_jobs < 1 || n_jobs > 3) return fail(SLLM_GFX950_ERR_ARG, "gemm: 1 to 3 jobs");
+    if (m == 0) return SLLM_GFX950_OK;
+    if (q == NULL || ((uintptr_t) q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemm: q must be given and 16-byte aligned");
+    if (m > (size_t) UINT32_MAX / 2) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m = %zu too large", m);
+    size_t rows_all = 0;
+    for (size_t j = 0; j < n_jobs; ++j) {
+        const int st = check_weights(jobs[j].w, jobs[j].n_rows, n);
+        if (st != SLLM_GFX950_OK) return st;
+        if (jobs[j].out == NULL && jobs[j].rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: job %zu has no output", j);
+        if (jobs[j].out != NULL && act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: the epilogue needs act");
+        if ((uint64_t) m * jobs[j].n_rows > (uint64_t) 1 << 40) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m x rows too large");
+        rows_all += jobs[j].n_rows;
+    }
+    int tile = g.force_gemm_tile - 1;
+    if (tile < 0) {
+        /* measured on MI355X: split-K tiles win up to 32 tokens, and up to 64
+         * when the LDS tile's grid would be small (under 4096 rows); above,
+         * the LDS tile -- one buffer once the grid holds more than one
+         * workgroup per CU, two buffers below */
+        const uint64_t lds_grid = ((rows_all + 127) / 128) * ((m + 127) / 128);
+        if (m <= 32 || (m <= 64 && rows_all < 4096)) tile = 0;
+        else if (n % 256 != 0) tile = 2;
+        else tile = lds_grid > (uint64_t) (g.cu > 0 ? g.cu : 256) ? 4 : 3;
+    }
+    if (tile >= 3 && n % 256 != 0) tile = 2;
+    const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];
+    k_gemm_args a;
+    memset(&a, 0, sizeof a);
+    uint64_t gx = 0;
+    for (size_t j = 0; j < 3; ++j) {
+        const size_t jj = j < n_jobs ? j : n_jobs - 1;      /* unused slots repeat the last job, no tiles */
+        a.w[j] = jobs[jj].w;
+        a.out[j] = jobs[jj].out;
+        a.out_i[j] = jobs[jj].rows_out;
+        a.n_rows[j] = (uint32_t) jobs[jj].n_rows;
+        a.tiles[j] = j < n_jobs ? (uint32_t) ((jobs[j].n_rows + rows_per_wg - 1) / rows_per_wg) : 0u;
+        gx += a.tiles[j];
+    }
+    a.q = q; a.act = act; a.k = (uint32_t) n; a.m = (uint32_t) m; a.n_jobs = (uint32_t) n_jobs;
+    const uint64_t gy = (m + tok_per_wg - 1) / tok_per_wg;
+    if (gx == 0) return SLLM_GFX950_OK;
+    if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");
+    void *args[] = { &a };
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm[tile], (uint32_t) gx, (uint32_t) gy, 1, 256, 1, 1, 0, g.stream, args, NULL));
     return SLLM_GFX950_OK;
 }
 
@@ -947,30 +1003,8 @@ int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
                      const sllm_gfx950_act *act, size_t m, float *out, int32_t *rows_out) {
     NEED_OPEN();
     if (m == 0) return SLLM_GFX950_OK;
-    int st = check_weights(w, n_rows, n);
-    if (st != SLLM_GFX950_OK) return st;
-    if (q == NULL || ((uintptr_t) q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemm: q must be given and 16-byte aligned");
-    if (out == NULL && rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: no output");
-    if (out != NULL && act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: the epilogue needs act");
-    if (m > (size_t) UINT32_MAX / 2 || (uint64_t) m * n_rows > (uint64_t) 1 << 40) {
-        return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m = %zu too large", m);
-    }
-    int tile = g.force_gemm_tile - 1;
-    if (tile < 0) {
-        /* measured on MI355X: split-K tiles win up to 32 tokens, and up to 64
-         * when the LDS tile's grid would be small (n_rows < 4096); the LDS
-         * tile wins above */
-        if (m <= 32 || (m <= 64 && n_rows < 4096)) tile = 0;
-        else tile = n % 256 == 0 ? 3 : 2;
-    }
-    if (tile == 3 && n % 256 != 0) tile = 2;
-    const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];
-    const uint64_t gx = (n_rows + rows_per_wg - 1) / rows_per_wg, gy = (m + tok_per_wg - 1) / tok_per_wg;
-    if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");
-    k_gemm_args a = { w, q, act, out, rows_out, (uint32_t) n_rows, (uint32_t) n, (uint32_t) m, 0 };
-    void *args[] = { &a };
-    HIP_TRY(hipModuleLaunchKernel(g.k_gemm[tile], (uint32_t) gx, (uint32_t) gy, 1, 256, 1, 1, 0, g.stream, args, NULL));
-    return SLLM_GFX950_OK;
+    const sllm_gfx950_gemm_job job = { w, n_rows, out, rows_out };
+    return sllm_gfx950_gemm_multi(&job, 1, n, q, act, m);
 }
 
 int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const float *x, size_t m,

@@ -304,18 +304,41 @@ __device__ __forceinline__ bool stream_share(const gemv_job *__restrict__ jobs,
 
 typedef int32_t i32x4v __attribute__((ext_vector_type(4)));
 
+// Up to three tensors of the same K against the same quantised rows (Q, K
+// and V; gate and up): the grid's row tiles are job 0's, then job 1's, then
+// job 2's.
 struct gemm_args {
-    const uint8_t   *w;          // packed tensor with its tail
     const int8_t    *q;          // [m][k] int8
     const act_t     *act;        // [m]
-    float           *out;        // [m][n_rows] epilogue, or null
-    int32_t         *out_i;      // [m][n_rows] raw dots, or null
-    uint32_t         n_rows, k, m, pad;
+    const uint8_t   *w[3];       // packed tensors with their tails
+    float           *out[3];     // [m][n_rows] epilogue, or null
+    int32_t         *out_i[3];   // [m][n_rows] raw dots, or null
+    uint32_t         n_rows[3];
+    uint32_t         tiles[3];   // row tiles (workgroups along x) of each job
+    uint32_t         k, m, n_jobs, pad;
 };
 
+// the job of this workgroup's row tile, and the tile's index within it
+struct gemm_view {
+    const uint8_t *w;
+    float         *out;
+    int32_t       *out_i;
+    uint32_t       n_rows, tile;
+};
+
+__device__ __forceinline__ gemm_view gemm_pick(const gemm_args &G) {
+    const uint32_t b = blockIdx.x, t0 = G.tiles[0], t01 = t0 + G.tiles[1];
+    const uint32_t j = b < t0 ? 0u : (b < t01 ? 1u : 2u);       // uniform; selects, no indexing
+    return { j == 0 ? G.w[0] : (j == 1 ? G.w[1] : G.w[2]),
+             j == 0 ? G.out[0] : (j == 1 ? G.out[1] : G.out[2]),
+             j == 0 ? G.out_i[0] : (j == 1 ? G.out_i[1] : G.out_i[2]),
+             j == 0 ? G.n_rows[0] : (j == 1 ? G.n_rows[1] : G.n_rows[2]),
+             b - (j == 0 ? 0u : (j == 1 ? t0 : t01)) };
+}
+
 template <int TM, int TN>
-__device__ __forceinline__ void gemm_load(const gemm_args &G, uint32_t t0, uint32_t n0, uint32_t step,
-                                          i32x4v (&a)[TM], u32x4 (&b)[TN]) {
+__device__ __forceinline__ void gemm_load(const gemm_args &G, const gemm_view &V, uint32_t t0, uint32_t n0,
+                                          uint32_t step, i32x4v (&a)[TM], u32x4 (&b)[TN]) {
     const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
     const uint32_t blk = step >> 1, h = step & 1u;
     const uint32_t kq = 128u * blk + 32u * (uint32_t) g + 16u * h;        // A: k offset of this lane group
@@ -327,8 +350,8 @@ __device__ __forceinline__ void gemm_load(const gemm_args &G, uint32_t t0, uint3
     }
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
-        const uint32_t n = min(n0 + 16u * (uint32_t) tn + (uint32_t) li, G.n_rows - 1);
-        b[tn] = __builtin_nontemporal_load(G_CAST(const u32x4, G.w + (size_t) n * (G.k >> 2) + kw));
+        const uint32_t n = min(n0 + 16u * (uint32_t) tn + (uint32_t) li, V.n_rows - 1);
+        b[tn] = __builtin_nontemporal_load(G_CAST(const u32x4, V.w + (size_t) n * (G.k >> 2) + kw));
     }
 }
 
@@ -358,8 +381,9 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
     __shared__ i32x4v part[SPLIT > 1 ? SPLIT - 1 : 1][TM][TN][64];
     const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) threadIdx.x >> 6);
+    const gemm_view V = gemm_pick(G);
     const uint32_t t0 = blockIdx.y * 16u * TM;
-    const uint32_t n0 = (SPLIT > 1 ? blockIdx.x : blockIdx.x * 4u + wave) * 16u * TN;
+    const uint32_t n0 = (SPLIT > 1 ? V.tile : V.tile * 4u + wave) * 16u * TN;
     const uint32_t steps_all = G.k / 64u;
     const uint32_t s_begin = SPLIT > 1 ? steps_all * wave / SPLIT : 0u;
     const uint32_t s_end = SPLIT > 1 ? steps_all * (wave + 1) / SPLIT : steps_all;
@@ -375,12 +399,12 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
     u32x4 bw[GEMM_DEPTH][TN];
     const uint32_t last = s_end > s_begin ? s_end - 1 : s_begin;
 #pragma unroll
-    for (int i = 0; i < GEMM_DEPTH; ++i) gemm_load<TM, TN>(G, t0, n0, min(s_begin + (uint32_t) i, last), a[i], bw[i]);
+    for (int i = 0; i < GEMM_DEPTH; ++i) gemm_load<TM, TN>(G, V, t0, n0, min(s_begin + (uint32_t) i, last), a[i], bw[i]);
     for (uint32_t s = s_begin; s < s_end; s += GEMM_DEPTH) {
 #pragma unroll
         for (int i = 0; i < GEMM_DEPTH; ++i) {
             if (s + (uint32_t) i < s_end) gemm_mma<TM, TN>(a[i], bw[i], c);
-            gemm_load<TM, TN>(G, t0, n0, min(s + (uint32_t) i + GEMM_DEPTH, last), a[i], bw[i]);
+            gemm_load<TM, TN>(G, V, t0, n0, min(s + (uint32_t) i + GEMM_DEPTH, last), a[i], bw[i]);
         }
     }
     if (SPLIT > 1) {
@@ -405,7 +429,7 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
 
     // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
     // token, (float)(dot - sum) * post
-    const float ws = *G_CAST(const float, G.w + (size_t) G.n_rows * (G.k >> 2));
+    const float ws = *G_CAST(const float, V.w + (size_t) V.n_rows * (G.k >> 2));
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
@@ -417,10 +441,10 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
                 const uint32_t n = n0 + 16u * (uint32_t) tn + (uint32_t) li;
-                if (n < G.n_rows) {
+                if (n < V.n_rows) {
                     const int32_t d = c[tm][tn][r];
-                    if (G.out_i != nullptr) G_CAST(int32_t, G.out_i)[(size_t) t * G.n_rows + n] = d;
-                    if (G.out != nullptr) G_CAST(float, G.out)[(size_t) t * G.n_rows + n] = (float) (d - at.sum) * post;
+                    if (V.out_i != nullptr) G_CAST(int32_t, V.out_i)[(size_t) t * V.n_rows + n] = d;
+                    if (V.out != nullptr) G_CAST(float, V.out)[(size_t) t * V.n_rows + n] = (float) (d - at.sum) * post;
                 }
             }
         }
@@ -431,27 +455,40 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
 // Large token counts (the prefill chunk): the workgroup stages its tile
 // through LDS so that each byte of the token rows and of the packed weights
 // enters it once, not once per wave. 128 tokens x 128 rows per workgroup,
-// four waves of 64 x 64 (16 MFMAs per k step); K moves in chunks of 256,
-// double-buffered in LDS, with the global loads two chunks ahead in
-// registers. LDS rows are padded (272 bytes per token, 80 per weight row)
-// so that the 16-byte operand reads of a lane group spread over the banks.
-// K must be a multiple of 256.
+// four waves of 64 x 64 (16 MFMAs per k step); K moves in chunks of 256
+// through one LDS buffer, the next chunk's global loads in registers while
+// the current one is multiplied. One buffer (45 KB) and about 160 registers
+// let three workgroups share a CU, so that one workgroup's barriers and
+// LDS stores overlap the others' MFMAs. LDS rows are padded (272 bytes per
+// token, 80 per weight row) so that the 16-byte operand reads of a lane
+// group spread over the banks. K must be a multiple of 256.
 constexpr uint32_t GL_BM = 128, GL_BN = 128, GL_BK = 256;
 constexpr uint32_t GL_QS = GL_BK + 16, GL_WS = GL_BK / 4 + 16;
 constexpr int GL_QLOADS = (int) (GL_BM * GL_BK / 16 / 256);
 constexpr int GL_WLOADS = (int) (GL_BN * GL_BK / 4 / 16 / 256);
 
+template <int NB>
 struct gl_shared {
-    uint8_t q[2][GL_BM * GL_QS];
-    uint8_t w[2][GL_BN * GL_WS];
+    uint8_t q[NB][GL_BM * GL_QS];
+    uint8_t w[NB][GL_BN * GL_WS];
 };
 
+// SINGLE: one LDS buffer (45 KB, about 250 registers: two workgroups per
+// CU), the next chunk in registers while the current one is multiplied,
+// then the buffer rewritten between two barriers -- for grids of more than
+// one workgroup per CU, where the workgroups sharing a CU overlap each
+// other's barriers. Otherwise two LDS buffers (90 KB, one workgroup per
+// CU) and the global loads two chunks ahead, so that a lone workgroup's
+// loads overlap its own MFMAs.
+template <bool SINGLE>
 __device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
-    __shared__ __attribute__((aligned(16))) gl_shared S;
+    constexpr int NB = SINGLE ? 1 : 2;
+    __shared__ __attribute__((aligned(16))) gl_shared<NB> S;
+    const gemm_view V = gemm_pick(G);
     const uint32_t tid = threadIdx.x;
     const int lane = (int) (tid & 63), g = lane >> 4, li = lane & 15;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t t0 = blockIdx.y * GL_BM, n0 = blockIdx.x * GL_BN;
+    const uint32_t t0 = blockIdx.y * GL_BM, n0 = V.tile * GL_BN;
     const uint32_t wt = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;
     const uint32_t chunks = G.k / GL_BK, kb = G.k >> 2;
     auto gload = [&](uint32_t c, u32x4 (&q)[GL_QLOADS], u32x4 (&w)[GL_WLOADS]) {
@@ -465,8 +502,8 @@ __device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
 #pragma unroll
         for (int u = 0; u < GL_WLOADS; ++u) {
             const uint32_t p = tid + 256u * (uint32_t) u, row = p / 4u, off = (p % 4u) * 16u;
-            const uint32_t n = min(n0 + row, G.n_rows - 1);
-            w[u] = __builtin_nontemporal_load(G_CAST(const u32x4, G.w + (size_t) n * kb + cc * (GL_BK / 4) + off));
+            const uint32_t n = min(n0 + row, V.n_rows - 1);
+            w[u] = __builtin_nontemporal_load(G_CAST(const u32x4, V.w + (size_t) n * kb + cc * (GL_BK / 4) + off));
         }
     };
     auto lstore = [&](int buf, const u32x4 (&q)[GL_QLOADS], const u32x4 (&w)[GL_WLOADS]) {
@@ -512,26 +549,43 @@ __device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
             }
         }
     };
-    u32x4 q0[GL_QLOADS], w0[GL_WLOADS], q1[GL_QLOADS], w1[GL_WLOADS];
-    gload(0, q0, w0);
-    gload(1, q1, w1);
-    lstore(0, q0, w0);
-    __syncthreads();
-    // chunk ch computes from LDS buffer ch & 1; register set ch & 1 is
-    // refilled with chunk ch + 2 while it runs
-    for (uint32_t ch = 0; ch < chunks; ch += 2) {
-        gload(ch + 2, q0, w0);
-        compute(0);
-        lstore(1, q1, w1);
+    if (SINGLE) {
+        u32x4 qn[GL_QLOADS], wn_[GL_WLOADS];
+        gload(0, qn, wn_);
+        lstore(0, qn, wn_);
         __syncthreads();
-        if (ch + 1 >= chunks) break;
-        gload(ch + 3, q1, w1);
-        compute(1);
+        // chunk ch is multiplied from LDS while chunk ch + 1 arrives in
+        // registers; then the buffer is rewritten between two barriers
+        for (uint32_t ch = 0; ch < chunks; ++ch) {
+            gload(ch + 1, qn, wn_);
+            compute(0);
+            if (ch + 1 >= chunks) break;          // uniform
+            __syncthreads();
+            lstore(0, qn, wn_);
+            __syncthreads();
+        }
+    } else {
+        u32x4 q0[GL_QLOADS], w0[GL_WLOADS], q1[GL_QLOADS], w1[GL_WLOADS];
+        gload(0, q0, w0);
+        gload(1, q1, w1);
         lstore(0, q0, w0);
         __syncthreads();
+        // chunk ch computes from LDS buffer ch & 1; register set ch & 1 is
+        // refilled with chunk ch + 2 while it runs
+        for (uint32_t ch = 0; ch < chunks; ch += 2) {
+            gload(ch + 2, q0, w0);
+            compute(0);
+            lstore(1, q1, w1);
+            __syncthreads();
+            if (ch + 1 >= chunks) break;
+            gload(ch + 3, q1, w1);
+            compute(1);
+            lstore(0, q0, w0);
+            __syncthreads();
+        }
     }
 
-    const float ws = *G_CAST(const float, G.w + (size_t) G.n_rows * kb);
+    const float ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
 #pragma unroll
@@ -543,10 +597,10 @@ __device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
 #pragma unroll
             for (int tn = 0; tn < 4; ++tn) {
                 const uint32_t n = n0 + wn + 16u * (uint32_t) tn + (uint32_t) li;
-                if (n < G.n_rows) {
+                if (n < V.n_rows) {
                     const int32_t d = c[tm][tn][r];
-                    if (G.out_i != nullptr) G_CAST(int32_t, G.out_i)[(size_t) t * G.n_rows + n] = d;
-                    if (G.out != nullptr) G_CAST(float, G.out)[(size_t) t * G.n_rows + n] = (float) (d - at.sum) * post;
+                    if (V.out_i != nullptr) G_CAST(int32_t, V.out_i)[(size_t) t * V.n_rows + n] = d;
+                    if (V.out != nullptr) G_CAST(float, V.out)[(size_t) t * V.n_rows + n] = (float) (d - at.sum) * post;
                 }
             }
         }
@@ -646,7 +700,9 @@ sllm_k_gemm_mfma_2x2(gemm_args G) { gemm_block<2, 2, 1>(G); }
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_4x2(gemm_args G) { gemm_block<4, 2, 1>(G); }
 extern "C" __global__ void __launch_bounds__(256)
-sllm_k_gemm_mfma_l128(gemm_args G) { gemm_lds_block(G); }
+sllm_k_gemm_mfma_l128(gemm_args G) { gemm_lds_block<false>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_mfma_l128s(gemm_args G) { gemm_lds_block<true>(G); }
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

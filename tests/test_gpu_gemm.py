@@ -65,7 +65,7 @@ def test_gemm_matches_the_oracle_token_by_token(amd, orc, dev, n_rows, n, m):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"{n_rows}x{n} m={m}")
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
 def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     n_rows, n, m = 640, 2560, 37
     w, x = _case(amd, 2, n_rows, n, m)
@@ -75,6 +75,41 @@ def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     finally:
         dev.set_gemm_tile(0)
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"tile {tile}")
+
+
+@pytest.mark.parametrize("tile", [0, 1, 4, 5])
+@pytest.mark.parametrize("m", [37, 512])
+def test_several_tensors_in_one_launch(amd, orc, dev, tile, m):
+    """Q, K and V (2560, 640, 640 rows) against the same quantised rows in
+    one sllm_gfx950_gemm_multi launch: each job's outputs are the single
+    GEMM's, and the oracle's token by token on the first and last token."""
+    n = 2560
+    rows = (2560, 640, 640)
+    ws = [amd.synth_i2s(amd.synth_seed(3, 9, r, j), r, n) for j, r in enumerate(rows)]
+    x = np.concatenate([amd.synth_normal(amd.synth_seed(3, 9, t, 2000), n) for t in range(m)]).astype(np.float32)
+    bw = [dev.put(w) for w in ws]
+    bx, bq, ba = dev.put(x), dev.alloc(m * n), dev.alloc(8 * m)
+    outs = [(dev.alloc(4 * m * r), dev.alloc(4 * m * r)) for r in rows]
+    ref = [(dev.alloc(4 * m * r), dev.alloc(4 * m * r)) for r in rows]
+    dev.set_gemm_tile(tile)
+    try:
+        dev.quant_act(bx.vp, n, m, bq.vp, ba.vp)
+        dev.gemm_multi([(bw[j].vp, rows[j], outs[j][0].vp, outs[j][1].vp) for j in range(3)], n, bq.vp, ba.vp, m)
+        for j in range(3):
+            dev.gemm(bw[j].vp, rows[j], n, bq.vp, ba.vp, m, ref[j][0].vp, ref[j][1].vp)
+        dev.sync()
+        for j, r in enumerate(rows):
+            y = outs[j][0].download(np.float32, m * r).reshape(m, r)
+            d = outs[j][1].download(np.int32, m * r).reshape(m, r)
+            assert np.array_equal(bits(y), bits(ref[j][0].download(np.float32, m * r).reshape(m, r))), f"job {j}"
+            assert np.array_equal(d, ref[j][1].download(np.int32, m * r).reshape(m, r)), f"job {j}"
+            for t in (0, m - 1):
+                yo, qo, do, so, su = orc.linear(ws[j], r, n, x[t * n:(t + 1) * n])
+                assert np.array_equal(d[t], do) and np.array_equal(bits(y[t]), bits(yo)), f"job {j} token {t}"
+    finally:
+        dev.set_gemm_tile(0)
+        for b in bw + [bx, bq, ba] + [b for p in outs + ref for b in p]:
+            b.free()
 
 
 @pytest.mark.parametrize("n_rows,n", [(6912, 2560), (2560, 6912)], ids=["gate_up", "down"])
@@ -106,7 +141,7 @@ def test_gemm_refuses_bad_arguments(amd, dev):
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, None, 2, o.vp, None) == -1     # epilogue without act
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 2, None, None) == -1     # no output
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 0, o.vp, None) == 0      # nothing to do
-        assert lib.sllm_gfx950_set_gemm_tile(5) == -1
+        assert lib.sllm_gfx950_set_gemm_tile(6) == -1
     finally:
         for b in (w, q, a, o):
             b.free()
