@@ -103,6 +103,24 @@ def test_chunk_without_logits_keeps_the_last_and_greedy_continues(amd, orc, dev,
         u.close()
 
 
+def test_chunks_with_a_narrow_rotary_width_and_four_query_heads_per_kv_head(amd, orc, dev):
+    """n_rot 48 of a 64-wide head (dimensions 48..63 pass through RoPE),
+    eight query heads over two KV heads: prefill in chunks of 5 and 23,
+    every position's logits against the oracle."""
+    cfg = dict(TINY, n_layer=3, n_embd=512, n_ff=1024, n_head=8, n_head_kv=2, n_rot=48, n_vocab=777)
+    model = amd.synth_model(cfg, 78)
+    toks = _tokens(51, cfg["n_vocab"], 79)
+    want = _oracle_logits(orc, model, 64, toks)
+    print("[chunk] narrow rotary width, 4 query heads per KV head", flush=True)
+    for chunk in (5, 23):
+        g = amd.DeviceDecoder(dev, model, 64)
+        try:
+            got = g.prefill_chunked(toks, chunk)
+        finally:
+            g.close()
+        assert np.array_equal(bits(got), bits(want)), f"chunk {chunk}: " + _first_diff(got, want)
+
+
 @pytest.mark.parametrize("widths", ["tiny", "2b"])
 def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
     """40 tokens at positions 1024..1063 over a restored cache: every query's
