@@ -117,6 +117,8 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define CHK_THREADS  256
 #define CLM_THREADS  256
 #define CLM_TOK      4    /* tokens per chunk output-head workgroup */
+#define CS_TOK       4    /* tokens per chunk scores workgroup */
+#define CP_TOK       4    /* tokens per chunk p.V workgroup */
 
 /* projections of a block, in the reference's order (src/forward.c:642-793) */
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, N_PROJ };
@@ -817,12 +819,16 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         void *aargs[] = { &A };
         if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_kvs, (uint32_t) n, 1, ATT_THREADS, 0, aargs);
         if (st == SLLM_GFX950_OK) {
-            st = sllm_shim_launch_3d(c->f_cscores, (uint32_t) m->n_head_kv, pos_blocks, (uint32_t) n,
-                                     ATT_THREADS, 0, aargs);
+            uint32_t n_tok = (uint32_t) n;
+            void *sargs[] = { &A, &n_tok };
+            st = sllm_shim_launch_3d(c->f_cscores, (uint32_t) m->n_head_kv, pos_blocks,
+                                     (uint32_t) ((n + CS_TOK - 1) / CS_TOK), ATT_THREADS, 0, sargs);
         }
         if (st == SLLM_GFX950_OK) {
-            st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, 1, (uint32_t) n, ATT_THREADS,
-                                     (uint32_t) (m->n_head / m->n_head_kv) * c->sc_stride * 4, aargs);
+            uint32_t n_tok = (uint32_t) n;
+            void *pargs[] = { &A, &n_tok };
+            st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, 1, (uint32_t) ((n + CP_TOK - 1) / CP_TOK),
+                                     ATT_THREADS, 0, pargs);
         }
         /* attn_sub_norm, O */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_PLAIN, B->attn, NULL, NULL, L->attn_sub_norm, (uint32_t) e, 1, NULL);
