@@ -234,7 +234,9 @@ int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const fl
 /* GEMM tile override for tuning and tests: 0 automatic (by m and the grid),
  * 1: 16 tokens x 16 rows per workgroup (K split over its waves), 2: 32 x 128,
  * 3: 64 x 128, 4: 128 x 128 staged through two LDS buffers, 5: the same
- * through one buffer (4 and 5 need K % 256 == 0; tile 3 otherwise). */
+ * through one buffer, 6..9: 16 x 64, 32 x 64, 32 x 128 and 64 x 256 copied
+ * straight into a ring of LDS stages (4..9 need K % 256 == 0; tile 3
+ * otherwise). */
 int sllm_gfx950_set_gemm_tile(int tile);
 
 /* Launch-geometry override for tuning sweeps and tests; affects launches

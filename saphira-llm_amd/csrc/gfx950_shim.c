@@ -118,7 +118,7 @@ static struct {
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
-    hipFunction_t  k_gemm[5];
+    hipFunction_t  k_gemm[9];
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -201,6 +201,10 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[2], g.mod, "sllm_k_gemm_mfma_4x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[3], g.mod, "sllm_k_gemm_mfma_l128"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[4], g.mod, "sllm_k_gemm_mfma_l128s"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[5], g.mod, "sllm_k_gemm_dl1x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[6], g.mod, "sllm_k_gemm_dl2x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[7], g.mod, "sllm_k_gemm_dl2x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[8], g.mod, "sllm_k_gemm_dl4x4"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
@@ -937,11 +941,20 @@ _Static_assert(sizeof(k_gemm_args) == 128, "k_gemm_args must match gemm_args in 
 
 /* tile shapes per workgroup: tokens x rows (shape 0 splits K over its four
  * waves instead of spreading them along the rows; shapes 3 and 4 stage their
- * tile through LDS and need K % 256 == 0 -- 3 with two buffers, one
- * workgroup per CU; 4 with one, two per CU) */
-#define N_GEMM_TILES 5
-static const uint32_t k_gemm_tokens[N_GEMM_TILES] = { 16, 32, 64, 128, 128 };
-static const uint32_t k_gemm_rows[N_GEMM_TILES] = { 16, 128, 128, 128, 128 };
+ * tile through LDS -- 3 with two buffers, one workgroup per CU; 4 with one,
+ * two per CU; shapes 5..8 copy it straight into an LDS ring). Shapes 3 and
+ * up need K % 256 == 0. */
+#define N_GEMM_TILES 9
+#define GEMM_DL_FIRST 5
+static const uint32_t k_gemm_tokens[N_GEMM_TILES] = { 16, 32, 64, 128, 128, 16, 32, 32, 64 };
+static const uint32_t k_gemm_rows[N_GEMM_TILES] = { 16, 128, 128, 128, 128, 64, 64, 128, 256 };
+
+/* workgroups of tile shape t for these jobs and tokens */
+static uint64_t gemm_grid(int t, const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t m) {
+    uint64_t gx = 0;
+    for (size_t j = 0; j < n_jobs; ++j) gx += (jobs[j].n_rows + k_gemm_rows[t] - 1) / k_gemm_rows[t];
+    return gx * ((m + k_gemm_tokens[t] - 1) / k_gemm_tokens[t]);
+}
 
 int sllm_gfx950_set_gemm_tile(int tile) {
     if (tile < 0 || tile > N_GEMM_TILES) return fail(SLLM_GFX950_ERR_ARG, "set_gemm_tile: 0 (auto) .. %d", N_GEMM_TILES);
@@ -956,25 +969,29 @@ int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size
     if (m == 0) return SLLM_GFX950_OK;
     if (q == NULL || ((uintptr_t) q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemm: q must be given and 16-byte aligned");
     if (m > (size_t) UINT32_MAX / 2) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m = %zu too large", m);
-    size_t rows_all = 0;
     for (size_t j = 0; j < n_jobs; ++j) {
         const int st = check_weights(jobs[j].w, jobs[j].n_rows, n);
         if (st != SLLM_GFX950_OK) return st;
         if (jobs[j].out == NULL && jobs[j].rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: job %zu has no output", j);
         if (jobs[j].out != NULL && act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm: the epilogue needs act");
         if ((uint64_t) m * jobs[j].n_rows > (uint64_t) 1 << 40) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: m x rows too large");
-        rows_all += jobs[j].n_rows;
     }
     int tile = g.force_gemm_tile - 1;
-    if (tile < 0) {
-        /* measured on MI355X: split-K tiles win up to 32 tokens, and up to 64
-         * when the LDS tile's grid would be small (under 4096 rows); above,
-         * the LDS tile -- one buffer once the grid holds more than one
-         * workgroup per CU, two buffers below */
-        const uint64_t lds_grid = ((rows_all + 127) / 128) * ((m + 127) / 128);
-        if (m <= 32 || (m <= 64 && rows_all < 4096)) tile = 0;
-        else if (n % 256 != 0) tile = 2;
-        else tile = lds_grid > (uint64_t) (g.cu > 0 ? g.cu : 256) ? 4 : 3;
+    if (tile < 0 && n % 256 == 0) {
+        /* measured on MI355X (K = 2560 and 6912, 16 to 512 tokens): the
+         * direct-load tiles win everywhere. Pick the largest whose grid still
+         * gives every CU work: 64 x 256 from 1.5 workgroups per CU, 32 x 128
+         * from 1.9, else 32 x 64, and 16 x 64 for up to 32 tokens or when
+         * 32 x 64 would leave CUs idle. */
+        const uint64_t cu = (uint64_t) (g.cu > 0 ? g.cu : 256);
+        if (m <= 32) tile = 5;
+        else if (m > 128 && gemm_grid(8, jobs, n_jobs, m) * 2 >= cu * 3) tile = 8;
+        else if (m > 128 && gemm_grid(7, jobs, n_jobs, m) * 8 >= cu * 15) tile = 7;
+        else if (gemm_grid(6, jobs, n_jobs, m) * 2 >= cu * 3) tile = 6;
+        else tile = 5;
+    } else if (tile < 0) {
+        /* K % 256 != 0: split-K tiles up to 64 tokens, else 64 x 128 */
+        tile = m <= 64 ? 0 : 2;
     }
     if (tile >= 3 && n % 256 != 0) tile = 2;
     const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];

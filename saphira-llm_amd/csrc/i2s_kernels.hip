@@ -607,6 +607,175 @@ __device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
     }
 }
 
+// Direct-load tiles (K % 256 == 0). K moves in super-steps of 256: two I2_S
+// blocks, 256 bytes of each token row and 64 packed bytes of each weight row.
+// global_load_lds_dwordx4 copies both straight from global memory into a
+// ring of STAGES LDS stages, STAGES - 1 super-steps ahead, with no registers
+// or LDS stores in between; each wave waits on its own copies (vmcnt) and one
+// barrier per super-step makes every wave's copies visible.
+//
+// Operand layout. Lane group g of a wave takes chunk g of its row's 64 packed
+// bytes (block 2s + g/2, half g%2) and feeds fields f = 0..3 of it to four
+// MFMA steps; its int8 operand for step f is the 16 token bytes at
+// k = 256 s + 128 (g/2) + 32 f + 16 (g%2) -- the elements the field holds
+// (block layout in the file header). So one 16-byte weight read serves four
+// steps, and every dot still sums the same products as the reference's.
+//
+// LDS layout: a token row is 16 granules of 16 bytes, granule G of token t at
+// slot G ^ (t % 16); a weight row is 4 chunks, chunk c of row r at slot
+// c ^ ((r / 4) % 4). The 16 lanes of a lane group then read 16 distinct banks
+// groups. The copies fill LDS in lane order, so each lane fetches the global
+// granule that belongs at its slot.
+//
+// A workgroup is 16 TM tokens x 64 TN rows: four waves side by side along the
+// rows, each 16 TM tokens x 16 TN rows (TM x TN MFMA tiles). Within a super-
+// step the next step's operand reads and weight unpacking are interleaved
+// with the current step's MFMAs, which keep the matrix unit busy while the
+// SIMD issues them.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {   // s_waitcnt vmcnt(N), the other counters untouched
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *) (p))
+
+template <int TM, int TN, int STAGES>
+__device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
+    constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
+    constexpr uint32_t A_BYTES = BM * 256u, STAGE = A_BYTES + BN * 64u;
+    constexpr int VM = TM + TN;                     // copies per wave per super-step
+    static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 2) * VM < 64, "stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t S[STAGES * STAGE];
+    const gemm_view V = gemm_pick(G);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 4, li = lane & 15u;
+    const uint32_t t0 = blockIdx.y * BM, n0 = V.tile * BN;
+    const uint32_t nsup = G.k / 256u, kb = G.k >> 2;
+    // copy sources: instruction j of this wave fills LDS granules
+    // (4 j + wave) * 64 + lane of the token and the weight block
+    const int8_t *asrc[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
+        const uint32_t t = p >> 4, gr = (p & 15u) ^ (t & 15u);
+        asrc[j] = G.q + (size_t) min(t0 + t, G.m - 1) * G.k + gr * 16u;
+    }
+    const uint8_t *bsrc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
+        const uint32_t r = p >> 2, ch = (p & 3u) ^ ((r >> 2) & 3u);
+        bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb + ch * 16u;
+    }
+    auto issue = [&](uint32_t s, uint32_t slot) {   // super-steps past the end re-copy the last (never read)
+        const uint32_t sc = min(s, nsup - 1);
+        uint8_t *base = S + slot * STAGE;
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+            __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + sc * 256u),
+                                             LDS_PTR(base + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            __builtin_amdgcn_global_load_lds((const void *) (bsrc[j] + sc * 64u),
+                                             LDS_PTR(base + A_BYTES + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+    };
+    uint32_t aoff[4];                               // token 16 tm + li (tm * 4096 added), granule of step f
+#pragma unroll
+    for (int f = 0; f < 4; ++f) aoff[f] = li * 256u + (((8u * (g >> 1) + 2u * (uint32_t) f + (g & 1u)) ^ li) * 16u);
+    const uint32_t wr = wave * (16u * TN);          // this wave's first row in the tile
+    const uint32_t boff = A_BYTES + (wr + li) * 64u + ((g ^ ((li >> 2) & 3u)) * 16u);
+    i32x4v c[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
+    }
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) issue((uint32_t) s, (uint32_t) s);
+    for (uint32_t s = 0; s < nsup; ++s) {
+        // this super-step's copies done (later ones may stay in flight), then everyone's
+        const uint32_t ahead = min(nsup - 1u - s, (uint32_t) STAGES - 2u);
+        if (ahead == 0) wait_vmem<0>();
+        else if (ahead == 1) wait_vmem<VM>();
+        else wait_vmem<(STAGES - 2) * VM>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's reads of the stage being refilled done
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(s + STAGES - 1, (s + STAGES - 1) % STAGES);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *st = S + (s % STAGES) * STAGE;
+        u32x4 raw[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) raw[tn] = *reinterpret_cast<const u32x4 *>(st + boff + (uint32_t) tn * 1024u);
+        i32x4v a[2][TM], b[2][TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) a[0][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[0] + (uint32_t) tm * 4096u);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) b[0][tn][d] = (int32_t) ((raw[tn][d] >> 6u) & 0x03030303u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const int cu = f & 1, nx = cu ^ 1;
+            if (f < 3) {
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm)
+                    a[nx][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[f + 1] + (uint32_t) tm * 4096u);
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) b[nx][tn][d] = (int32_t) ((raw[tn][d] >> (4u - 2u * (uint32_t) f)) & 0x03030303u);
+                }
+            }
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm)
+                    c[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[cu][tm], b[cu][tn], c[tm][tn], 0, 0, 0);
+            }
+            if (f < 3) {
+                // each MFMA, then one of the next step's reads and its share of the unpacking
+                constexpr int VPM = (8 * TN + TM * TN - 1) / (TM * TN);
+#pragma unroll
+                for (int i = 0; i < TM * TN; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (i < TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wait_vmem<0>();                                 // no copy may land after the workgroup leaves
+
+    // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
+    // token, (float)(dot - sum) * post
+    const float ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t t = t0 + 16u * (uint32_t) tm + 4u * g + (uint32_t) r;
+            if (t >= G.m) continue;
+            const act_t at = G.act != nullptr ? G.act[t] : act_t { 1.0f, 0 };
+            const float post = ws / at.scale;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const uint32_t n = n0 + wr + 16u * (uint32_t) tn + li;
+                if (n < V.n_rows) {
+                    const int32_t d = c[tm][tn][r];
+                    if (V.out_i != nullptr) G_CAST(int32_t, V.out_i)[(size_t) t * V.n_rows + n] = d;
+                    if (V.out != nullptr) G_CAST(float, V.out)[(size_t) t * V.n_rows + n] = (float) (d - at.sum) * post;
+                }
+            }
+        }
+    }
+}
+
 } // namespace
 
 // ---------------------------------------------------------------------------
@@ -693,6 +862,7 @@ SLLM_STREAM_ENTRY(16)
 //   _s1x1  16 tokens x 16 rows, K split over the four waves
 //   _2x2   32 tokens x 128 rows      _4x2   64 tokens x 128 rows
 //   _l128  128 tokens x 128 rows staged through LDS (K % 256 == 0)
+//   _dl<TM>x<TN>  16 TM tokens x 64 TN rows, direct-load ring (K % 256 == 0)
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_s1x1(gemm_args G) { gemm_block<1, 1, 4>(G); }
 extern "C" __global__ void __launch_bounds__(256)
@@ -703,6 +873,14 @@ extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_l128(gemm_args G) { gemm_lds_block<false>(G); }
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_mfma_l128s(gemm_args G) { gemm_lds_block<true>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_dl1x1(gemm_args G) { gemm_dl_block<1, 1, 4>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_dl2x1(gemm_args G) { gemm_dl_block<2, 1, 4>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_dl2x2(gemm_args G) { gemm_dl_block<2, 2, 4>(G); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_dl4x4(gemm_args G) { gemm_dl_block<4, 4, 2>(G); }
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

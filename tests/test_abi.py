@@ -54,7 +54,8 @@ def test_library_embeds_a_gfx950_code_object():
     for k in (b"sllm_k_quant_act", b"sllm_k_quant_list", b"sllm_k_gemv_slab", b"sllm_k_gemv_stream_l4",
               b"sllm_k_gemv_stream_l8", b"sllm_k_gemv_stream_l16", b"sllm_k_gemm_mfma_s1x1",
               b"sllm_k_gemm_mfma_2x2", b"sllm_k_gemm_mfma_4x2", b"sllm_k_gemm_mfma_l128",
-              b"sllm_k_gemm_mfma_l128s"):
+              b"sllm_k_gemm_mfma_l128s", b"sllm_k_gemm_dl1x1", b"sllm_k_gemm_dl2x1", b"sllm_k_gemm_dl2x2",
+              b"sllm_k_gemm_dl4x4"):
         assert k in blob
 
 

@@ -65,7 +65,7 @@ def test_gemm_matches_the_oracle_token_by_token(amd, orc, dev, n_rows, n, m):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"{n_rows}x{n} m={m}")
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9])
 def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     n_rows, n, m = 640, 2560, 37
     w, x = _case(amd, 2, n_rows, n, m)
@@ -77,7 +77,7 @@ def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"tile {tile}")
 
 
-@pytest.mark.parametrize("tile", [0, 1, 4, 5])
+@pytest.mark.parametrize("tile", [0, 1, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("m", [37, 512])
 def test_several_tensors_in_one_launch(amd, orc, dev, tile, m):
     """Q, K and V (2560, 640, 640 rows) against the same quantised rows in
@@ -141,7 +141,7 @@ def test_gemm_refuses_bad_arguments(amd, dev):
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, None, 2, o.vp, None) == -1     # epilogue without act
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 2, None, None) == -1     # no output
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 0, o.vp, None) == 0      # nothing to do
-        assert lib.sllm_gfx950_set_gemm_tile(6) == -1
+        assert lib.sllm_gfx950_set_gemm_tile(10) == -1
     finally:
         for b in (w, q, a, o):
             b.free()
