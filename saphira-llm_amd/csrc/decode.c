@@ -117,8 +117,12 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define CHK_THREADS  256
 #define CLM_THREADS  256
 #define CLM_TOK      4    /* tokens per chunk output-head workgroup */
-#define CS_TOK       4    /* tokens per chunk scores workgroup */
+#define CS_TOK       8    /* tokens per chunk scores workgroup */
 #define CP_TOK       4    /* tokens per chunk p.V workgroup */
+#define CP_THREADS   512  /* threads per chunk p.V workgroup: two waves per query head */
+#define CSM_ROWS     4    /* softmax rows (one wave each) per chunk softmax workgroup */
+/* sllm_k_chk_kv_store stages a token's query row (n_head * hd = n_embd floats) in 7168 floats of LDS */
+_Static_assert(SLLM_GFX950_DEC_MAX_WIDTH <= 7168, "query row of the chunk KV store");
 
 /* projections of a block, in the reference's order (src/forward.c:642-793) */
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN, N_PROJ };
@@ -301,7 +305,7 @@ struct sllm_gfx950_ctx {
     k_dec_lm      lm_args;
     size_t        kv_per_layer;    /* floats */
     hipFunction_t f_gemv, f_scores, f_pv, f_lm, f_argmax;
-    hipFunction_t f_prep, f_kvs, f_cscores, f_cpv, f_clm, f_keys;
+    hipFunction_t f_prep, f_kvs, f_cscores, f_csoft, f_cpv, f_clm, f_keys;
     uint32_t      sc_stride;
     chunk_bufs    chk;
     int           graph_on, graph_ready;
@@ -486,6 +490,7 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
             (st = sllm_shim_decode_function("sllm_k_chk_prep", &c->f_prep)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_kv_store", &c->f_kvs)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_scores", &c->f_cscores)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_softmax", &c->f_csoft)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_pv", &c->f_cpv)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_lm_head", &c->f_clm)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_keys", &c->f_keys)) == SLLM_GFX950_OK) {
@@ -826,9 +831,15 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         }
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;
+            void *margs[] = { &A, &n_tok };
+            st = sllm_shim_launch(c->f_csoft, (uint32_t) ((n * m->n_head + CSM_ROWS - 1) / CSM_ROWS), 1, CSM_ROWS * 64, 0,
+                                  margs);
+        }
+        if (st == SLLM_GFX950_OK) {
+            uint32_t n_tok = (uint32_t) n;
             void *pargs[] = { &A, &n_tok };
             st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, 1, (uint32_t) ((n + CP_TOK - 1) / CP_TOK),
-                                     ATT_THREADS, 0, pargs);
+                                     CP_THREADS, 0, pargs);
         }
         /* attn_sub_norm, O */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_PLAIN, B->attn, NULL, NULL, L->attn_sub_norm, (uint32_t) e, 1, NULL);

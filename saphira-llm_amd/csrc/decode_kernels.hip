@@ -545,28 +545,29 @@ __device__ __forceinline__ void scores_body(const dec_attn &A) {
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_dec_scores(dec_attn A) { scores_body<false>(A); }
 
-// The chunk's scores: workgroup (KV head, 64 positions, 4 tokens), so that
-// a block of cached keys, loaded once into LDS, serves four tokens. Each
-// token's queries are roped at its own position (chunk_base + t); its keys
-// are already in the cache (the chunk's own included). Thread (h, r) holds
-// four dot chains -- token by token the q . k of the decode kernel, in
-// order of d, times 1/sqrt(hd) -- and writes the positions at or before
-// each token's own.
-constexpr uint32_t CS_TOK = 4;
+// The chunk's scores: workgroup (KV head, 64 positions, 8 tokens), so that
+// a block of cached keys, loaded once into LDS, serves eight tokens. Thread
+// (h, r) -- wave h is query head h of the KV head, lane r a position --
+// holds eight dot chains: token by token the q . k of the decode kernel, in
+// order of d, times 1/sqrt(hd), written for the positions at or before each
+// token's own. The queries were roped at their positions by
+// sllm_k_chk_kv_store; they are the same for every lane of a wave and come
+// through the scalar unit (8 dimensions of a token per load), so the LDS
+// serves only the keys.
+constexpr uint32_t CS_TOK = 8;
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_chk_scores(dec_attn A, uint32_t n_tok) {
-    __shared__ __attribute__((aligned(16))) float qr[CS_TOK][ATT_MAX_GRP][ATT_MAX_HD];
     __shared__ __attribute__((aligned(16))) float kt[ATT_POS][KT_STRIDE];
     const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tb = blockIdx.z * CS_TOK, tid = threadIdx.x;
     const uint32_t last_tok = min(tb + CS_TOK, n_tok) - 1;
     const uint32_t npast_max = A.chunk_base + last_tok + 1;
     if (s0 >= npast_max) return;
-    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, half = A.half, hd4 = hd / 4;
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, hd4 = hd / 4;
     const float *kc = A.k_cache + (size_t) kvh * A.n_ctx * hd;
 
-    // (1) the block's keys (rows past the last token's position re-read a
-    // valid row), then the tokens' queries, roped
+    // the block's keys (rows past the last token's position re-read a valid row)
     const uint32_t n_f4 = ATT_POS * hd4, last_cached = npast_max - 1;
     f32x4 kv[KT_LOADS];
 #pragma unroll
@@ -574,14 +575,6 @@ sllm_k_chk_scores(dec_attn A, uint32_t n_tok) {
         const uint32_t f = min(tid + (uint32_t) u * ATT_THREADS, n_f4 - 1);
         const uint32_t r = f / hd4, c4 = f % hd4;
         kv[u] = *G_CAST(const f32x4, kc + (size_t) min(s0 + r, last_cached) * hd + 4 * c4);
-    }
-    const uint32_t per_tok = grp * hd;
-    for (uint32_t idx = tid; idx < CS_TOK * per_tok; idx += ATT_THREADS) {
-        const uint32_t tok = idx / per_tok, h = (idx % per_tok) / hd, d = idx % hd;
-        const uint32_t t = min(tb + tok, last_tok), pos = A.chunk_base + t;
-        const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
-        const rope_in qi = rope_load(A.q + (size_t) t * A.n_head * hd + (size_t) (kvh * grp + h) * hd, d, half, cs);
-        qr[tok][h][d] = rope_apply(qi, d, half);
     }
 #pragma unroll
     for (int u = 0; u < KT_LOADS; ++u) {
@@ -591,25 +584,34 @@ sllm_k_chk_scores(dec_attn A, uint32_t n_tok) {
     }
     __syncthreads();
 
-    // (2) thread (h, r): four chains over d, one per token
-    const uint32_t r = tid % ATT_POS, hh = tid / ATT_POS;
-    if (hh < grp && s0 + r < npast_max) {
-        float acc[CS_TOK];
+    const uint32_t r = tid % ATT_POS, hh = __builtin_amdgcn_readfirstlane(tid / ATT_POS);
+    if (hh >= grp) return;                           // uniform
+    const float *qrow[CS_TOK];
 #pragma unroll
-        for (int tk = 0; tk < (int) CS_TOK; ++tk) acc[tk] = 0.0f;
-        for (uint32_t d4 = 0; d4 < hd4; ++d4) {
-            const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&kt[r][4 * d4]);
+    for (int tk = 0; tk < (int) CS_TOK; ++tk)
+        qrow[tk] = A.q + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + hh) * hd;
+    float acc[CS_TOK];
 #pragma unroll
-            for (int tk = 0; tk < (int) CS_TOK; ++tk) {
-                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&qr[tk][hh][4 * d4]);
-                float a = acc[tk];
-                a = a + q4[0] * k4[0];
-                a = a + q4[1] * k4[1];
-                a = a + q4[2] * k4[2];
-                a = a + q4[3] * k4[3];
-                acc[tk] = a;
+    for (int tk = 0; tk < (int) CS_TOK; ++tk) acc[tk] = 0.0f;
+    for (uint32_t d0 = 0; d0 < hd; d0 += 8) {       // hd % 8 == 0
+        f32x4 k4[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) k4[j] = *reinterpret_cast<const f32x4 *>(&kt[r][d0 + 4 * j]);
+#pragma unroll
+        for (int tk = 0; tk < (int) CS_TOK; ++tk) {
+            const f32x8 q = *reinterpret_cast<const f32x8 *>(qrow[tk] + d0);
+            float a = acc[tk];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                a = a + q[4 * j] * k4[j][0];
+                a = a + q[4 * j + 1] * k4[j][1];
+                a = a + q[4 * j + 2] * k4[j][2];
+                a = a + q[4 * j + 3] * k4[j][3];
             }
+            acc[tk] = a;
         }
+    }
+    if (s0 + r < npast_max) {
 #pragma unroll
         for (int tk = 0; tk < (int) CS_TOK; ++tk) {
             const uint32_t t = tb + (uint32_t) tk;
@@ -1202,19 +1204,32 @@ sllm_k_chk_prep(chk_prep P) {
 
 // Workgroup t: token t's key roped at its position (NeoX, src/ops.c:467-549)
 // and stored with its value into the caches (src/forward.c:668-690), so that
-// every query of the chunk finds the keys at or before its position.
+// every query of the chunk finds the keys at or before its position; and the
+// token's queries roped in place (read whole into LDS first: each output
+// needs its pair's input), so that the scores read them as they are.
+constexpr uint32_t KVS_MAX_Q = 7168;    // a query row: n_head * hd <= the decoder's widest row
+
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_chk_kv_store(dec_attn A) {
+    __shared__ float qs[KVS_MAX_Q];
     const uint32_t t = blockIdx.x, pos = A.chunk_base + t, hd = A.hd, half = A.half;
-    const uint32_t gqa = A.n_kv * hd;
+    const uint32_t gqa = A.n_kv * hd, nq = A.n_head * hd;
     const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
     const float *k = A.k + (size_t) t * gqa, *v = A.v + (size_t) t * gqa;
+    float *q = const_cast<float *>(A.q) + (size_t) t * nq;
+    for (uint32_t i = threadIdx.x; i < nq; i += ATT_THREADS) qs[i] = q[i];
     for (uint32_t i = threadIdx.x; i < gqa; i += ATT_THREADS) {
         const uint32_t kvh = i / hd, d = i % hd;
         const rope_in r = rope_load(k + (size_t) kvh * hd, d, half, cs);
         const size_t at = ((size_t) kvh * A.n_ctx + pos) * hd + d;
         A.k_cache[at] = rope_apply(r, d, half);
         A.v_cache[at] = v[i];
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nq; i += ATT_THREADS) {
+        const uint32_t hh = i / hd, d = i % hd;
+        const rope_in r = rope_load(qs + (size_t) hh * hd, d, half, cs);
+        q[i] = rope_apply(r, d, half);
     }
 }
 
@@ -1293,56 +1308,44 @@ sllm_k_chk_lm_head(chk_lm L) {
     }
 }
 
-// The chunk's softmax and p . V: workgroup (KV head, 4 tokens), wave w =
-// query head w of the KV head, so that each V row, read once, serves four
-// tokens.
-//  - Per token, the softmax statistics of the head's scores (src/ops.c:
-//    386-422), the same operations as the decode step's: the max;
-//    ggml_v_expf over whole groups of eight, the C library's expf over the
-//    rest; the double sum of the groups (((e0+e4) + (e1+e5)) + (e2+e6)) +
-//    (e3+e7) and of the tail terms in any order, checked, in the
-//    reference's order when the check cannot decide; inv = 1/sum.
-//  - In rounds of 512 positions, p = e * inv of the four tokens into LDS
-//    (e recomputed: the same bits), then lane l adds p_s * v_s to each of
-//    its eight chains -- dimensions 2l and 2l + 1 of the four tokens -- in
-//    order of s (src/forward.c:706-726), a token's chain left alone past
-//    its own position. V rows stream from L2 two blocks of sixteen
-//    positions ahead.
-constexpr uint32_t CP_TOK = 4;
-constexpr uint32_t CP_ROUND = 512;
+// The chunk's softmax rows: one wave per (token, query head) row, the
+// decode step's operations (src/ops.c:386-422) -- the max; ggml_v_expf over
+// whole groups of eight, the C library's expf over the rest; the double sum
+// of the groups (((e0+e4) + (e1+e5)) + (e2+e6)) + (e3+e7) and of the tail
+// terms in any order, checked, in the reference's order when the check
+// cannot decide; inv = 1/sum -- then p_s = e_s * inv written back over the
+// row for s < npast (e recomputed for rows past 512 positions: the same
+// bits).
+constexpr int CSM_THREADS = 256;        // four rows per workgroup
 
-extern "C" __global__ void __launch_bounds__(ATT_THREADS)
-sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
-    __shared__ __attribute__((aligned(16))) float P[ATT_MAX_GRP][CP_TOK][CP_ROUND];
+extern "C" __global__ void __launch_bounds__(CSM_THREADS)
+sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
     __shared__ uint64_t tab[32];
-    // the last token blocks (the longest rows) first
-    const uint32_t kvh = blockIdx.x, tb = (gridDim.z - 1 - blockIdx.z) * CP_TOK, tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
-    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
-    const uint32_t last_tok = min(tb + CP_TOK, n_tok) - 1;
-    const uint32_t npast_max = A.chunk_base + last_tok + 1, npast_min = A.chunk_base + tb + 1;
-    if (tid < 32) tab[tid] = c_expf_tab[tid];
+    if (threadIdx.x < 32) tab[threadIdx.x] = c_expf_tab[threadIdx.x];
     __syncthreads();
-    if (wave >= grp) return;                       // (no block barrier below this point)
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t row_i = blockIdx.x * (CSM_THREADS / 64) + wave;
+    if (row_i >= n_tok * A.n_head) return;          // uniform
+    const uint32_t t = row_i / A.n_head, hh = row_i % A.n_head, ss = A.sc_stride;
+    const uint32_t npast = A.chunk_base + t + 1, nb = npast / 8, nt = nb * 8;
+    float *sc = A.scores + (size_t) t * A.n_head * ss + (size_t) hh * ss;
 
     auto group_sum = [](const float (&e)[8]) {
         const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
         const double t2 = (double) e[2] + (double) e[6], t3 = (double) e[3] + (double) e[7];
         return ((t0 + t1) + t2) + t3;
     };
-    // the scores row of token tk for this wave's head, and its length
-    auto row = [&](uint32_t tk) {
-        const uint32_t t = min(tb + tk, last_tok);
-        return A.scores + (size_t) t * A.n_head * ss + (size_t) (kvh * grp + wave) * ss;
-    };
-    auto row_npast = [&](uint32_t tk) { return A.chunk_base + min(tb + tk, last_tok) + 1; };
-    auto load8 = [&](const float *sc, uint32_t s, float (&v)[8]) {
+    auto load8 = [&](uint32_t s, float (&v)[8]) {
         const uint32_t at = min(s, ss - 8);
         const f32x4 a = *G_CAST(const f32x4, sc + at), b = *G_CAST(const f32x4, sc + at + 4);
         v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
         v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
     };
-    auto exps8 = [&](float (&v)[8], uint32_t s, uint32_t nt, float m) {   // as in the decode kernel
+    auto store8 = [&](uint32_t s, const float (&v)[8], float inv) {
+        *G_CAST(f32x4, sc + s) = (f32x4) { v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv };
+        *G_CAST(f32x4, sc + s + 4) = (f32x4) { v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv };
+    };
+    auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
         if (s < nt) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
@@ -1351,7 +1354,7 @@ sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
             for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
         }
     };
-    auto add_group = [&](double &part, const float (&v)[8], uint32_t s, uint32_t npast) {
+    auto add_group = [&](double &part, const float (&v)[8], uint32_t s) {
         if (s + 8 <= npast) {
             part += group_sum(v);
         } else {                                   // the tail, term by term
@@ -1361,207 +1364,190 @@ sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
             }
         }
     };
-    // inv = 1/sum from the lanes' partial sums: checked, else the
-    // reference's order by one lane
-    auto inverse = [&](double part, const float *sc, uint32_t npast, float m) {
-        const uint32_t nb = npast / 8, nt = nb * 8;
-        const double sum = wave_sum_d(part);
-        const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
-        float inv = (float) (1.0 / (sum - bound));
-        if (inv != (float) (1.0 / (sum + bound))) {   // uniform over the wave
-            if (lane == 0) {
-                double seq = 0.0;
-                for (uint32_t s = 0; s < nt; s += 8) {
-                    float v[8];
-                    load8(sc, s, v);
-                    exps8(v, s, nt, m);
-                    seq += group_sum(v);
-                }
-                for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
-                inv = (float) (1.0 / seq);
-            }
-            inv = __shfl(inv, 0, 64);
-        }
-        return inv;
-    };
-    auto wave_sync = [&]() {                       // this wave's LDS writes seen by its lanes
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    };
 
-    // (1) the softmax statistics of the four rows. Rows of at most 512
-    // positions (one round): all four loaded at once and kept in registers,
-    // e into LDS in the same pass, then scaled by inv in place.
-    float st_m[CP_TOK], st_inv[CP_TOK];
-    const bool one_round = npast_max <= CP_ROUND;
-    if (one_round) {
-        float v[CP_TOK][8];
+    float m = -INFINITY;
+    double part = 0.0;
+    float v1[8];                                    // a row of one round stays in registers
+    if (npast <= 512) {
         const uint32_t s = 8 * lane;
+        load8(s, v1);
 #pragma unroll
-        for (int tk = 0; tk < (int) CP_TOK; ++tk) load8(row((uint32_t) tk), s, v[tk]);
-#pragma unroll
-        for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-            const uint32_t npast = row_npast((uint32_t) tk), nt = npast / 8 * 8;
-            float m = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[tk][i] : -INFINITY);
-            m = wave_max(m);
-            double part = 0.0;
-            if (s < npast) {
-                exps8(v[tk], s, nt, m);
-                add_group(part, v[tk], s, npast);
-                *reinterpret_cast<f32x4 *>(&P[wave][tk][s]) = (f32x4) { v[tk][0], v[tk][1], v[tk][2], v[tk][3] };
-                *reinterpret_cast<f32x4 *>(&P[wave][tk][s + 4]) = (f32x4) { v[tk][4], v[tk][5], v[tk][6], v[tk][7] };
-            }
-            st_m[tk] = m;
-            st_inv[tk] = inverse(part, row((uint32_t) tk), npast, m);
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v1[i] : -INFINITY);
+        m = wave_max(m);
+        if (s < npast) {
+            exps8(v1, s, m);
+            add_group(part, v1, s);
         }
-        wave_sync();
-#pragma unroll
-        for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-            const uint32_t npast = row_npast((uint32_t) tk);
-            for (uint32_t i = lane; i < npast; i += 64) P[wave][tk][i] = P[wave][tk][i] * st_inv[tk];
-        }
-        wave_sync();
     } else {
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            load8(s, v);
 #pragma unroll
-        for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-            const uint32_t npast = row_npast((uint32_t) tk), nt = npast / 8 * 8;
-            const float *sc = row((uint32_t) tk);
-            float m = -INFINITY;
-            for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
-                float v[8];
-                const uint32_t s = b0 + 8 * lane;
-                load8(sc, s, v);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
+        }
+        m = wave_max(m);
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            if (s < npast) {
+                load8(s, v);
+                exps8(v, s, m);
+                add_group(part, v, s);
             }
-            m = wave_max(m);
-            double part = 0.0;
-            for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
-                float v[8];
-                const uint32_t s = b0 + 8 * lane;
-                if (s < npast) {
-                    load8(sc, s, v);
-                    exps8(v, s, nt, m);
-                    add_group(part, v, s, npast);
-                }
-            }
-            st_m[tk] = m;
-            st_inv[tk] = inverse(part, sc, npast, m);
         }
     }
+    // inv = 1/sum from the lanes' partial sums: checked, else the reference's
+    // order by one lane
+    const double sum = wave_sum_d(part);
+    const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
+    float inv = (float) (1.0 / (sum - bound));
+    if (inv != (float) (1.0 / (sum + bound))) {     // uniform over the wave
+        if (lane == 0) {
+            double seq = 0.0;
+            for (uint32_t s = 0; s < nt; s += 8) {
+                float v[8];
+                load8(s, v);
+                exps8(v, s, m);
+                seq += group_sum(v);
+            }
+            for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
+            inv = (float) (1.0 / seq);
+        }
+        inv = __shfl(inv, 0, 64);
+    }
+    // every lane's reads of the row are done (the wave reduced them above)
+    if (npast <= 512) {
+        const uint32_t s = 8 * lane;
+        if (s < npast) store8(s, v1, inv);
+    } else {
+        for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            float v[8];
+            const uint32_t s = b0 + 8 * lane;
+            if (s < npast) {
+                load8(s, v);
+                exps8(v, s, m);
+                store8(s, v, inv);
+            }
+        }
+    }
+}
 
-    // (2) rounds of 512 positions: p of the round into LDS (already there in
-    // the one-round case), then the chains
-    const uint32_t d = min(2 * lane, hd - 2);
+// The chunk's p . V: workgroup (KV head, 4 tokens) of eight waves; wave w
+// is query head h = w % 4 of the KV head and half w / 4 of the head
+// dimensions, one dimension per lane. Each lane adds p_s * v_s to four
+// chains -- its dimension for the four tokens -- in order of s
+// (src/forward.c:706-726), a token's chain left alone past its own
+// position. p (written over the scores rows by sllm_k_chk_softmax) is the
+// same for every lane of a wave and comes through the scalar unit, eight
+// positions of a token per load; V rows stream from L2 two blocks of sixteen
+// positions ahead. The two waves of a SIMD hide each other's waits.
+constexpr uint32_t CP_TOK = 4;
+constexpr int CP_THREADS = 512;
+
+extern "C" __global__ void __launch_bounds__(CP_THREADS)
+sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
+    // the last token blocks (the longest rows) first
+    const uint32_t kvh = blockIdx.x, tb = (gridDim.z - 1 - blockIdx.z) * CP_TOK, tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = wave & 3u, half_id = wave >> 2;
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
+    if (h >= grp || 64u * half_id >= hd) return;   // uniform; no barriers in this kernel
+    const uint32_t last_tok = min(tb + CP_TOK, n_tok) - 1;
+    const uint32_t npast_max = A.chunk_base + last_tok + 1, npast_min = A.chunk_base + tb + 1;
+    const uint32_t d = min(64u * half_id + lane, hd - 1);
     const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d;
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    float acc[CP_TOK][2];
-    uint32_t npast_t[CP_TOK];                     // each token's own (past n_tok: never written out)
+    const float *prow[CP_TOK];                     // token rows past n_tok read the last one's
+    float acc[CP_TOK];
+    uint32_t npast_t[CP_TOK];                      // each token's own (past n_tok: never written out)
 #pragma unroll
     for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-        acc[tk][0] = acc[tk][1] = 0.0f;
+        prow[tk] = A.scores + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + h) * ss;
+        acc[tk] = 0.0f;
         npast_t[tk] = A.chunk_base + tb + (uint32_t) tk + 1;
     }
-    for (uint32_t base = 0; base < npast_max; base += CP_ROUND) {
-        const uint32_t n = min(CP_ROUND, npast_max - base);
-        if (!one_round) {
-            wave_sync();                            // the last round's reads of P done
+    // p of positions s..s+7 of token tk (within the row: sc_stride >= n_ctx, a multiple of 8)
+    auto p8 = [&](int tk, uint32_t s) { return *reinterpret_cast<const f32x8 *>(prow[tk] + min(s, ss - 8)); };
+    float va[16], vb[16];
+    auto load16 = [&](uint32_t s, float (&v)[16]) {
 #pragma unroll
-            for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-                const uint32_t npast = row_npast((uint32_t) tk), nt = npast / 8 * 8;
-                const uint32_t i = 8 * lane;        // one group of eight per lane per round
-                if (i < n && base + i < npast) {
-                    float v[8];
-                    load8(row((uint32_t) tk), base + i, v);
-                    exps8(v, base + i, nt, st_m[tk]);
-                    const float inv = st_inv[tk];
-                    *reinterpret_cast<f32x4 *>(&P[wave][tk][i]) = (f32x4) { v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv };
-                    *reinterpret_cast<f32x4 *>(&P[wave][tk][i + 4]) = (f32x4) { v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv };
-                }
-            }
-            wave_sync();
+        for (int q = 0; q < 16; ++q) v[q] = *G_CAST(const float, vc + (size_t) min(s + (uint32_t) q, npast_max - 1) * hd);
+    };
+    // eight positions at which every token of the block is live, with p of
+    // them in pc; the next eight's p go to pn. Scalar loads return out of
+    // order, so a wait covers all of them: the next loads are issued only
+    // after the first use of pc has waited for it.
+    auto step8 = [&](uint32_t s, const float *v, const f32x8 (&pc)[CP_TOK], f32x8 (&pn)[CP_TOK]) {
+#pragma unroll
+        for (int tk = 0; tk < (int) CP_TOK; ++tk) acc[tk] = acc[tk] + pc[tk][0] * v[0];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int tk = 0; tk < (int) CP_TOK; ++tk) pn[tk] = p8(tk, s + 8);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 1; q < 8; ++q) {
+#pragma unroll
+            for (int tk = 0; tk < (int) CP_TOK; ++tk) acc[tk] = acc[tk] + pc[tk][q] * v[q];
         }
-
-        f32x2 va[16], vb[16];
-        auto load16 = [&](uint32_t s, f32x2 (&v)[16]) {
+    };
+    f32x8 pa[CP_TOK], pb[CP_TOK];
 #pragma unroll
-            for (int q = 0; q < 16; ++q) v[q] = *G_CAST(const f32x2, vc + (size_t) min(s + (uint32_t) q, npast_max - 1) * hd);
-        };
-        // sixteen positions at which every token of the block is live: the
-        // products, then the ordered adds
-        auto step16 = [&](uint32_t s, const f32x2 (&v)[16]) {
+    for (int tk = 0; tk < (int) CP_TOK; ++tk) pa[tk] = p8(tk, 0);
+    // sixteen positions: p of the first eight in pa on entry, of the next
+    // sixteen's first eight in pa on exit
+    auto step16 = [&](uint32_t s, const float (&v)[16]) {
+        step8(s, v, pa, pb);
+        step8(s + 8, v + 8, pb, pa);
+    };
+    // the last positions: a token's chain left alone past its own
+    auto tail = [&](uint32_t s, uint32_t r, const float (&v)[16]) {
 #pragma unroll
-            for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-                float pr[16];
+        for (int hb = 0; hb < 2; ++hb) {
+            if (8u * (uint32_t) hb < r) {
+                f32x8 p[CP_TOK];
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&P[wave][tk][s - base + 4 * q4]);
-                    pr[4 * q4] = p4[0]; pr[4 * q4 + 1] = p4[1]; pr[4 * q4 + 2] = p4[2]; pr[4 * q4 + 3] = p4[3];
-                }
-                float x0[16], x1[16];
+                for (int tk = 0; tk < (int) CP_TOK; ++tk) p[tk] = p8(tk, s + 8u * (uint32_t) hb);
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    x0[q] = pr[q] * v[q][0];
-                    x1[q] = pr[q] * v[q][1];
-                }
+                for (int q = 0; q < 8; ++q) {
+                    const uint32_t at = s + 8u * (uint32_t) hb + (uint32_t) q;
+                    if (8u * (uint32_t) hb + (uint32_t) q < r) {
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    acc[tk][0] = acc[tk][0] + x0[q];
-                    acc[tk][1] = acc[tk][1] + x1[q];
-                }
-            }
-        };
-        // the last positions: a token's chains left alone past its own
-        auto tail = [&](uint32_t s, uint32_t r, const f32x2 (&v)[16]) {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                if ((uint32_t) q < r) {
-#pragma unroll
-                    for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-                        const float p = P[wave][tk][s - base + (uint32_t) q];
-                        const bool live = s + (uint32_t) q < npast_t[tk];
-                        const float x0 = p * v[q][0], x1 = p * v[q][1];
-                        acc[tk][0] = live ? acc[tk][0] + x0 : acc[tk][0];
-                        acc[tk][1] = live ? acc[tk][1] + x1 : acc[tk][1];
+                        for (int tk = 0; tk < (int) CP_TOK; ++tk) {
+                            const float x = p[tk][q] * v[8 * hb + q];
+                            acc[tk] = at < npast_t[tk] ? acc[tk] + x : acc[tk];
+                        }
                     }
                 }
             }
-        };
-        load16(base, va);
-        load16(base + 16, vb);
-        uint32_t s = base;
-        const uint32_t end = base + n;
-        const uint32_t bulk = max(base, min(end, npast_min));   // every token live before this
-        for (; s + 32 <= bulk; s += 32) {
-            step16(s, va);
-            load16(s + 32, va);
-            step16(s + 16, vb);
-            load16(s + 48, vb);
         }
-        // at most 15 + 3 positions remain, in va then vb
-        if (s + 16 <= bulk) {
-            step16(s, va);
-            s += 16;
-            load16(s + 16, va);
-            tail(s, min(end - s, 16u), vb);
-            if (end - s > 16) tail(s + 16, end - s - 16, va);
-        } else {
-            tail(s, min(end - s, 16u), va);
-            if (end - s > 16) tail(s + 16, end - s - 16, vb);
-        }
+    };
+    load16(0, va);
+    load16(16, vb);
+    uint32_t s = 0;
+    const uint32_t end = npast_max;
+    const uint32_t bulk = min(end, npast_min);      // every token live before this
+    for (; s + 32 <= bulk; s += 32) {
+        step16(s, va);
+        load16(s + 32, va);
+        step16(s + 16, vb);
+        load16(s + 48, vb);
     }
-    if (2 * lane < hd) {
+    // at most 15 + 3 positions remain, in va then vb
+    if (s + 16 <= bulk) {
+        step16(s, va);
+        s += 16;
+        load16(s + 16, va);
+        tail(s, min(end - s, 16u), vb);
+        if (end - s > 16) tail(s + 16, end - s - 16, va);
+    } else {
+        tail(s, min(end - s, 16u), va);
+        if (end - s > 16) tail(s + 16, end - s - 16, vb);
+    }
+    if (64u * half_id + lane < hd) {
 #pragma unroll
         for (int tk = 0; tk < (int) CP_TOK; ++tk) {
             const uint32_t t = tb + (uint32_t) tk;
-            if (t < n_tok) {
-                float *out = A.out + (size_t) t * A.n_head * hd + (size_t) (kvh * grp + wave) * hd + 2 * lane;
-                out[0] = acc[tk][0];
-                out[1] = acc[tk][1];
-            }
+            if (t < n_tok) A.out[(size_t) t * A.n_head * hd + (size_t) (kvh * grp + h) * hd + 64u * half_id + lane] = acc[tk];
         }
     }
 }
