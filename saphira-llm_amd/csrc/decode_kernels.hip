@@ -1137,6 +1137,14 @@ sllm_k_chk_prep(chk_prep P) {
     const size_t row = (size_t) t * k;
     const int32_t token = P.mode == IN_EMBED ? P.tokens[t] : 0;
     double part = 0.0;
+    // the norm weights of this thread's elements, loaded beside the vector
+    // rather than after the mean (CHK_MAX_K / 4 / CHK_THREADS float4 at most)
+    f32x4 wv[CHK_MAX_K / 4 / CHK_THREADS];
+#pragma unroll
+    for (int u = 0; u < (int) (CHK_MAX_K / 4 / CHK_THREADS); ++u) {
+        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        wv[u] = i < k ? *G_CAST(const f32x4, P.norm_w + i) : (f32x4) { 0.0f, 0.0f, 0.0f, 0.0f };
+    }
     for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
         f32x4 v;
         if (P.mode == IN_EMBED) {
@@ -1161,9 +1169,12 @@ sllm_k_chk_prep(chk_prep P) {
     const float mean = rms_mean(part, k, red_d, lane_d, [&](uint32_t j) { return xs[j]; });
     const float scale = 1.0f / sqrtf(mean + P.eps);
     float m = 0.0f;
-    for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
+#pragma unroll
+    for (int u = 0; u < (int) (CHK_MAX_K / 4 / CHK_THREADS); ++u) {
+        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        if (i >= k) break;
         f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
-        const f32x4 w = *G_CAST(const f32x4, P.norm_w + i);
+        const f32x4 w = wv[u];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             v[c] = (scale * v[c]) * w[c];
@@ -1205,13 +1216,14 @@ sllm_k_chk_prep(chk_prep P) {
 // Workgroup t: token t's key roped at its position (NeoX, src/ops.c:467-549)
 // and stored with its value into the caches (src/forward.c:668-690), so that
 // every query of the chunk finds the keys at or before its position; and the
-// token's queries roped in place (read whole into LDS first: each output
-// needs its pair's input), so that the scores read them as they are.
+// token's queries roped in place, so that the scores read them as they are.
+// The query and key rows and the position's cos / sin are read into LDS
+// first, in one round of loads (each output needs its pair's input).
 constexpr uint32_t KVS_MAX_Q = 7168;    // a query row: n_head * hd <= the decoder's widest row
 
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_chk_kv_store(dec_attn A) {
-    __shared__ float qs[KVS_MAX_Q];
+    __shared__ float qs[KVS_MAX_Q], ks[KVS_MAX_Q], cst[ATT_MAX_HD];
     const uint32_t t = blockIdx.x, pos = A.chunk_base + t, hd = A.hd, half = A.half;
     const uint32_t gqa = A.n_kv * hd, nq = A.n_head * hd;
     const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
@@ -1219,16 +1231,19 @@ sllm_k_chk_kv_store(dec_attn A) {
     float *q = const_cast<float *>(A.q) + (size_t) t * nq;
     for (uint32_t i = threadIdx.x; i < nq; i += ATT_THREADS) qs[i] = q[i];
     for (uint32_t i = threadIdx.x; i < gqa; i += ATT_THREADS) {
-        const uint32_t kvh = i / hd, d = i % hd;
-        const rope_in r = rope_load(k + (size_t) kvh * hd, d, half, cs);
-        const size_t at = ((size_t) kvh * A.n_ctx + pos) * hd + d;
-        A.k_cache[at] = rope_apply(r, d, half);
-        A.v_cache[at] = v[i];
+        ks[i] = k[i];
+        A.v_cache[((size_t) (i / hd) * A.n_ctx + pos) * hd + i % hd] = v[i];
     }
+    for (uint32_t i = threadIdx.x; i < 2 * half; i += ATT_THREADS) cst[i] = cs[i];
     __syncthreads();
+    for (uint32_t i = threadIdx.x; i < gqa; i += ATT_THREADS) {
+        const uint32_t kvh = i / hd, d = i % hd;
+        const rope_in r = rope_load(ks + (size_t) kvh * hd, d, half, cst);
+        A.k_cache[((size_t) kvh * A.n_ctx + pos) * hd + d] = rope_apply(r, d, half);
+    }
     for (uint32_t i = threadIdx.x; i < nq; i += ATT_THREADS) {
         const uint32_t hh = i / hd, d = i % hd;
-        const rope_in r = rope_load(qs + (size_t) hh * hd, d, half, cs);
+        const rope_in r = rope_load(qs + (size_t) hh * hd, d, half, cst);
         q[i] = rope_apply(r, d, half);
     }
 }
