@@ -117,7 +117,8 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define CHK_THREADS  256
 #define CLM_THREADS  256
 #define CLM_TOK      4    /* tokens per chunk output-head workgroup */
-#define CS_TOK       8    /* tokens per chunk scores workgroup */
+#define CS_TOK       8    /* tokens per chunk scores workgroup (half that up to CS_SMALL tokens) */
+#define CS_SMALL     128
 #define CP_TOK       4    /* tokens per chunk p.V workgroup */
 #define CP_THREADS   512  /* threads per chunk p.V workgroup: two waves per query head */
 #define CSM_ROWS     4    /* softmax rows (one wave each) per chunk softmax workgroup */
@@ -305,7 +306,7 @@ struct sllm_gfx950_ctx {
     k_dec_lm      lm_args;
     size_t        kv_per_layer;    /* floats */
     hipFunction_t f_gemv, f_scores, f_pv, f_lm, f_argmax;
-    hipFunction_t f_prep, f_kvs, f_cscores, f_csoft, f_cpv, f_clm, f_keys;
+    hipFunction_t f_prep, f_kvs, f_cscores, f_cscores4, f_csoft, f_cpv, f_clm, f_keys;
     uint32_t      sc_stride;
     chunk_bufs    chk;
     int           graph_on, graph_ready;
@@ -490,6 +491,7 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
             (st = sllm_shim_decode_function("sllm_k_chk_prep", &c->f_prep)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_kv_store", &c->f_kvs)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_scores", &c->f_cscores)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_scores4", &c->f_cscores4)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_softmax", &c->f_csoft)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_pv", &c->f_cpv)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_lm_head", &c->f_clm)) == SLLM_GFX950_OK &&
@@ -826,8 +828,11 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;
             void *sargs[] = { &A, &n_tok };
-            st = sllm_shim_launch_3d(c->f_cscores, (uint32_t) m->n_head_kv, pos_blocks,
-                                     (uint32_t) ((n + CS_TOK - 1) / CS_TOK), ATT_THREADS, 0, sargs);
+            /* eight tokens per workgroup, four for small chunks (measured: the grid
+             * of a 64-token chunk is too small at eight) */
+            const int tok = n > CS_SMALL ? CS_TOK : CS_TOK / 2;
+            st = sllm_shim_launch_3d(n > CS_SMALL ? c->f_cscores : c->f_cscores4, (uint32_t) m->n_head_kv, pos_blocks,
+                                     (uint32_t) ((n + tok - 1) / tok), ATT_THREADS, 0, sargs);
         }
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;

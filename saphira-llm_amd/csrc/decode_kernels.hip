@@ -545,20 +545,20 @@ __device__ __forceinline__ void scores_body(const dec_attn &A) {
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_dec_scores(dec_attn A) { scores_body<false>(A); }
 
-// The chunk's scores: workgroup (KV head, 64 positions, 8 tokens), so that
-// a block of cached keys, loaded once into LDS, serves eight tokens. Thread
+// The chunk's scores: workgroup (KV head, 64 positions, TOK tokens), so
+// that a block of cached keys, loaded once into LDS, serves TOK tokens (8;
+// 4 for small chunks, whose grid would otherwise be a few dozen). Thread
 // (h, r) -- wave h is query head h of the KV head, lane r a position --
-// holds eight dot chains: token by token the q . k of the decode kernel, in
+// holds TOK dot chains: token by token the q . k of the decode kernel, in
 // order of d, times 1/sqrt(hd), written for the positions at or before each
 // token's own. The queries were roped at their positions by
 // sllm_k_chk_kv_store; they are the same for every lane of a wave and come
 // through the scalar unit (8 dimensions of a token per load), so the LDS
 // serves only the keys.
-constexpr uint32_t CS_TOK = 8;
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
-extern "C" __global__ void __launch_bounds__(ATT_THREADS)
-sllm_k_chk_scores(dec_attn A, uint32_t n_tok) {
+template <uint32_t CS_TOK>
+__device__ __forceinline__ void chk_scores_body(const dec_attn &A, uint32_t n_tok) {
     __shared__ __attribute__((aligned(16))) float kt[ATT_POS][KT_STRIDE];
     const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tb = blockIdx.z * CS_TOK, tid = threadIdx.x;
     const uint32_t last_tok = min(tb + CS_TOK, n_tok) - 1;
@@ -622,6 +622,11 @@ sllm_k_chk_scores(dec_attn A, uint32_t n_tok) {
         }
     }
 }
+
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_chk_scores(dec_attn A, uint32_t n_tok) { chk_scores_body<8>(A, n_tok); }
+extern "C" __global__ void __launch_bounds__(ATT_THREADS)
+sllm_k_chk_scores4(dec_attn A, uint32_t n_tok) { chk_scores_body<4>(A, n_tok); }
 
 // Softmax and p . V: workgroup (KV head, 16 head dimensions), four waves.
 //  - The slice of V for the first 1536 positions is loaded first, all of it

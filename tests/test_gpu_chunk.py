@@ -8,8 +8,9 @@ logits are those bits; so every row of a device chunk must equal the
 oracle's logits at that position, bit for bit. Shapes: chunk sizes from 2
 to 64 over a 70-token sequence (later chunks attend to keys earlier ones
 wrote), chunks over a restored 1024-position cache at tiny and BitNet-2B
-widths, the full 30-block 2B model in one 100-token chunk (the MFMA GEMM's
-LDS tile), and decode / greedy generation carrying on after a chunk.
+widths, chunks of 200 and 150 tokens (the scores' eight-token workgroups),
+the full 30-block 2B model in one 100-token chunk, and decode / greedy
+generation carrying on after a chunk.
 """
 import numpy as np
 import pytest
@@ -121,6 +122,24 @@ def test_chunks_with_a_narrow_rotary_width_and_four_query_heads_per_kv_head(amd,
         assert np.array_equal(bits(got), bits(want)), f"chunk {chunk}: " + _first_diff(got, want)
 
 
+def test_chunks_above_128_tokens(amd, orc, dev):
+    """A chunk of 200 tokens, then one of 150 at positions 200..349: above
+    128 tokens the scores take eight tokens per workgroup, and the second
+    chunk's rows run past 256 positions; every position's logits against
+    the oracle."""
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 81)
+    toks = _tokens(350, cfg["n_vocab"], 82)
+    want = _oracle_logits(orc, model, 360, toks)
+    print("[chunk] 200 + 150 tokens", flush=True)
+    g = amd.DeviceDecoder(dev, model, 360)
+    try:
+        got = np.concatenate([g.forward_chunk(toks[:200], 0), g.forward_chunk(toks[200:], 200)])
+    finally:
+        g.close()
+    assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
 @pytest.mark.parametrize("widths", ["tiny", "2b"])
 def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
     """40 tokens at positions 1024..1063 over a restored cache: every query's
@@ -147,7 +166,7 @@ def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
 
 def test_full_2b_chunk_is_bit_exact(amd, orc, dev):
     """All 30 blocks at BitNet-2B shape, 100 tokens in one chunk (every GEMM
-    on the LDS tile), logits of every position against the oracle."""
+    on a direct-load MFMA tile), logits of every position against the oracle."""
     cfg = dict(amd.BITNET_2B)
     print("[chunk] building the 2B model", flush=True)
     model = amd.synth_model(cfg, 5)
