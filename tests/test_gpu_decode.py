@@ -104,13 +104,15 @@ def _kv_prefix(cfg, n_pos, seed):
     return k, v
 
 
-@pytest.mark.parametrize("widths", ["tiny", "2b"])
-def test_decode_after_a_1024_position_prefix(amd, orc, dev, widths):
-    """Positions 1024.. over a restored cache: every softmax spans five V
-    chunks and seventeen score workgroups per KV head."""
+@pytest.mark.parametrize("widths,n_pos", [("tiny", 1024), ("2b", 1024), ("tiny", 4030)])
+def test_decode_after_a_restored_prefix(amd, orc, dev, widths, n_pos):
+    """Positions past a restored cache. At 1024 the softmax spans seventeen
+    score workgroups per KV head and p.V keeps p and V of the row in one
+    round (1536 positions); at 4030 .. 4034 p.V takes three rounds, e
+    recomputed for the second and third."""
     cfg = dict(TINY) if widths == "tiny" else dict(amd.BITNET_2B, n_layer=2, n_vocab=512)
     model = amd.synth_model(cfg, 12)
-    n_pos, n_ctx = 1024, 1032
+    n_ctx = n_pos + 8
     k, v = _kv_prefix(cfg, n_pos, 13)
     g, o = amd.DeviceDecoder(dev, model, n_ctx), orc.Decoder(model, n_ctx)
     ok, ov = o.caches()
