@@ -248,7 +248,7 @@ int sllm_gfx950_set_gemm_tile(int tile);
  *   lanes_per_row  streaming kernel: 4, 8 or 16
  *   waves          streaming kernel: waves per workgroup, 1..16
  *   rows_per_wg    streaming kernel: rows per workgroup
- *   slab_kib       slab kernel: KiB of packed weights per workgroup */
+ *   slab_kib       slab kernel: KiB of packed weights per workgroup (0: 136) */
 int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, int rows_per_wg,
                            int slab_kib);
 

@@ -520,7 +520,7 @@ int sllm_gfx950_quant_act(const float *x, size_t n, size_t n_tok, int8_t *q,
 #define SLAB_THREADS     256
 #define SLAB_MAX_K       7168
 #define SLAB_MAX_ROWS    1024
-#define SLAB_DEFAULT_KIB 128
+#define SLAB_DEFAULT_KIB 136     /* 32 slabs per BitNet-2B FFN matrix: 2-4 % faster than 34 (128 KiB) */
 
 typedef struct slab_geom { int lpr, cpl; } slab_geom;
 static const slab_geom k_slab_geom[2] = { { 8, 5 }, { 16, 7 } };
