@@ -388,8 +388,8 @@ def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
 
 
 def cpu_decode(dec_check, seconds=10.0, threads=16):
-    """The decode checker and baseline. Checker: the oracle's decode step on
-    the same model and prefix at the same position -- logits, every int32
+    """The decode parity check and baseline. Parity: the oracle's decode step
+    on the same model and prefix at the same position -- logits, every int32
     dot and every activation of the GPU's traced token, bit for bit. Baseline:
     the reference's own sllm_forward (oracle/_ref) restored to the same
     prefix through its state file (src/forward.c:963-1100), greedy decode
@@ -439,7 +439,7 @@ def cpu_decode(dec_check, seconds=10.0, threads=16):
 
 
 def cpu_prefill(pre_check, seconds=10.0, threads=16):
-    """Checker: rows 0..15 of the chunk's logits against the oracle's
+    """Parity: rows 0..15 of the chunk's logits against the oracle's
     token-by-token logits, bit for bit. Baseline: the reference's own
     sllm_forward_prefill_chunked (oracle/_ref) on the same model and tokens,
     chunks of 16, as many chunks as fit in about `seconds` on `threads`
@@ -483,7 +483,7 @@ def cpu_gemm_check(checks):
 
 
 def cpu_baseline(wl, checks, seconds=6.0):
-    """The CPU leg. First the checker: the GPU outputs kept in `checks`
+    """The CPU leg. First the parity check: the GPU outputs kept in `checks`
     against the oracle, bit for bit. Then the baseline: the reference's CPU
     path (or the oracle's restatement) over a bounded sample of the same
     workload -- passes over the 32 sets, each set quantise -> GEMV ->

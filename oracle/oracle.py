@@ -1,8 +1,8 @@
 """ctypes access to the oracle libraries -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this module, and only as the checker (or the CPU figure beside the
-GPU); the product path never does.
+import this module, and only to check GPU results (or for the CPU figure
+beside the GPU); the product path never does.
 
   liboracle.so          the C restatement (sllm_oracle.c), always built
   _ref/libsllm_ref.so   the reference's own hot-path sources compiled where

@@ -2,8 +2,8 @@
  * sllm_oracle.h -- CPU restatement of saphira-llm's I2_S ternary path.
  *
  * TEST INFRASTRUCTURE, NOT PRODUCT. Only tests/, __graft_entry__.smoke() and
- * the cpu_baseline leg of bench.py may load this library, and only as the
- * checker (or, for bench.py, as the CPU figure reported beside the GPU). The
+ * the cpu_baseline leg of bench.py may load this library, and only to check
+ * GPU results (or, for bench.py, for the CPU figure reported beside the GPU). The
  * product path (saphira-llm_amd/) never links, loads or calls it.
  *
  * Every function restates the reference behaviour at the file:line given
