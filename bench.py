@@ -588,7 +588,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the I2_S GEMV path runs on a single MI355X and "
-              "this build has no multi-GPU path (--gpus must be 1).", file=sys.stderr)
+              "the library has no multi-GPU path (--gpus must be 1).", file=sys.stderr)
         sys.exit(2)
 
     amd = load_package()
