@@ -729,11 +729,41 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[g][i] : -INFINITY);
             }
             m = wave_max(m);
+            // the tail group's C-library expf (npast - nt <= 7 terms): one
+            // term per lane, so that the wave evaluates it once rather than
+            // the tail's lane eight times over
+            if (npast > nt) {                     // uniform
+                const uint32_t gt = nt / 512u, lt = (nt % 512u) / 8u, cnt = npast - nt;
+                float xt = 0.0f;
+#pragma unroll
+                for (int g = 0; g < RG; ++g) {
+                    if ((uint32_t) g == gt) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const float xi = __shfl(v[g][i], (int) lt, 64);
+                            xt = lane == (uint32_t) i ? xi : xt;
+                        }
+                    }
+                }
+                float et = 0.0f;
+                if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float ei = __shfl(et, i, 64);
+#pragma unroll
+                    for (int g = 0; g < RG; ++g) {
+                        if ((uint32_t) g == gt && lane == lt && (uint32_t) i < cnt) v[g][i] = ei;
+                    }
+                }
+            }
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
                 const uint32_t s = 512u * (uint32_t) g + 8 * lane;
                 if (s < npast) {
-                    exps8(v[g], s, m);
+                    if (s < nt) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) v[g][i] = ggml_v_expf(v[g][i] - m);
+                    }
                     if (s + 8 <= npast) {
                         part += group_sum(v[g]);
                     } else {                      // the tail, from the lane's own registers
