@@ -1404,6 +1404,33 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
             for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
         }
     };
+    // e of whole groups (lanes whose group lies below nt)
+    auto ggml8 = [&](float (&v)[8], uint32_t s, float m) {
+        if (s < nt) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+        }
+    };
+    // e of the tail group (npast - nt <= 7 terms, the C library's expf),
+    // held by lane lt: one term per lane, so that the wave evaluates expf
+    // once rather than lane lt eight times over. Called by the whole wave.
+    auto tail8 = [&](float (&v)[8], uint32_t lt, float m) {
+        const uint32_t cnt = npast - nt;
+        float xt = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float xi = __shfl(v[i], (int) lt, 64);
+            xt = lane == (uint32_t) i ? xi : xt;
+        }
+        float et = 0.0f;
+        if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float ei = __shfl(et, i, 64);
+            if (lane == lt && (uint32_t) i < cnt) v[i] = ei;
+        }
+    };
+    const bool has_tail = npast > nt;
     auto add_group = [&](double &part, const float (&v)[8], uint32_t s) {
         if (s + 8 <= npast) {
             part += group_sum(v);
@@ -1424,8 +1451,9 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v1[i] : -INFINITY);
         m = wave_max(m);
+        if (has_tail) tail8(v1, nt / 8u, m);
         if (s < npast) {
-            exps8(v1, s, m);
+            ggml8(v1, s, m);
             add_group(part, v1, s);
         }
     } else {
@@ -1440,9 +1468,10 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
         for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
             float v[8];
             const uint32_t s = b0 + 8 * lane;
+            load8(s, v);
+            if (has_tail && nt - b0 < 512u) tail8(v, (nt - b0) / 8u, m);   // uniform
             if (s < npast) {
-                load8(s, v);
-                exps8(v, s, m);
+                ggml8(v, s, m);
                 add_group(part, v, s);
             }
         }
@@ -1474,9 +1503,10 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
         for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
             float v[8];
             const uint32_t s = b0 + 8 * lane;
+            load8(s, v);
+            if (has_tail && nt - b0 < 512u) tail8(v, (nt - b0) / 8u, m);   // uniform
             if (s < npast) {
-                load8(s, v);
-                exps8(v, s, m);
+                ggml8(v, s, m);
                 store8(s, v, inv);
             }
         }
