@@ -687,6 +687,25 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
             for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
         }
     };
+    // e of the tail group (npast - nt <= 7 terms, the C library's expf),
+    // held by lane lt: one term per lane, so that the wave evaluates expf
+    // once rather than lane lt eight times over. Called by the whole wave.
+    auto tail8 = [&](float (&v)[8], uint32_t lt, float m) {
+        const uint32_t cnt = npast - nt;
+        float xt = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float xi = __shfl(v[i], (int) lt, 64);
+            xt = lane == (uint32_t) i ? xi : xt;
+        }
+        float et = 0.0f;
+        if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float ei = __shfl(et, i, 64);
+            if (lane == lt && (uint32_t) i < cnt) v[i] = ei;
+        }
+    };
     // one round (npast <= 1536): each softmax wave's scores are loaded
     // first, all at once, ahead of V, and stay in registers
     constexpr int RG = (int) (PV_RPOS / 512);
@@ -791,7 +810,11 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 float v[8];
                 const uint32_t s = b0 + 8 * lane;
                 load8(sc, s, v);
-                exps8(v, s, m);
+                if (npast > nt && nt - b0 < 512u) tail8(v, (nt - b0) / 8u, m);   // uniform
+                if (s < nt) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+                }
                 if (s + 8 <= npast) {
                     part += group_sum(v);
                 } else {
@@ -874,7 +897,11 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                     float v[8];
                     const uint32_t i = i0 + 8 * lane;
                     load8(sc, base + i, v);
-                    exps8(v, base + i, m);
+                    if (npast > nt && nt - (base + i0) < 512u) tail8(v, (nt - base - i0) / 8u, m);   // uniform
+                    if (base + i < nt) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[e] = ggml_v_expf(v[e] - m);
+                    }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         if (i + (uint32_t) e < n) P[wave][i + (uint32_t) e] = v[e] * inv;
