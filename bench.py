@@ -180,6 +180,68 @@ def measure_block_plan(amd, dev, layers=30, steps=200):
             "frac_of_peak": round(total / (ev_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "steps": steps}
 
 
+CFG0_N = 2560
+CFG0_COPIES = 192      # 192 x 1.64 MB = 315 MB: more than the 256 MB Infinity Cache
+
+
+def measure_cfg0(amd, dev, calls=2000):
+    """One 2560 x 2560 I2_S GEMV at batch 1 (quantise -> GEMV -> epilogue,
+    one launch per call, sllm_gfx950_linear): hot (the same tensor every
+    call, resident in the caches) and rotated over CFG0_COPIES distinct
+    tensors (so HBM feeds them); and the rotated copies as one plan (every
+    GEMV of the set in one launch, each with its own activation), the
+    bandwidth-bound form. Returns the figures and two outputs for the oracle
+    check."""
+    n = CFG0_N
+    ws = [amd.synth_i2s(amd.synth_seed(0, s_, 0, 0), n, n) for s_ in range(CFG0_COPIES)]
+    xs = np.stack([amd.synth_normal(amd.synth_seed(0, s_, 0, 1), n) for s_ in range(CFG0_COPIES)])
+    bws = [dev.put(w) for w in ws]
+    bx = dev.put(xs)
+    bq, ba = dev.alloc(n), dev.alloc(8)
+    by = dev.alloc(4 * n * CFG0_COPIES)
+    per_call = n * n // 4 + 4 + 4 * n + 4 * n
+    res = {}
+    for label, rot in (("hot", 1), ("rotated", CFG0_COPIES)):
+        for i in range(64):
+            dev.linear(bws[i % rot].vp, n, n, bx.at(4 * n * (i % rot)), bq.vp, ba.vp, by.at(4 * n * (i % rot)))
+        dev.events(2)
+        dev.sync()
+        dev.record(0)
+        for i in range(calls):
+            dev.linear(bws[i % rot].vp, n, n, bx.at(4 * n * (i % rot)), bq.vp, ba.vp, by.at(4 * n * (i % rot)))
+        dev.record(1)
+        us = dev.elapsed(0, 1) * 1e3 / calls
+        res[label] = {"us_per_call": round(us, 2), "GBps": round(per_call / us / 1e3, 1)}
+        log(f"cfg0 2560x2560 {label}: {us:.2f} us per call, {per_call / us / 1e3:.1f} GB/s")
+    checks = []
+    for i in (0, CFG0_COPIES - 1):
+        checks.append((ws[i], n, n, xs[i], by.download(np.float32, n, 4 * n * i), f"cfg0 copy {i}"))
+    plan = dev.plan([amd.GemvJob(bws[i].ptr, n, n, bx.ptr + 4 * n * i, None, None, by.ptr + 4 * n * i, None)
+                     for i in range(CFG0_COPIES)])
+    for _ in range(20):
+        dev.plan_run(plan)
+    reps = 200
+    dev.sync()
+    dev.record(0)
+    for _ in range(reps):
+        dev.plan_run(plan)
+    dev.record(1)
+    us = dev.elapsed(0, 1) * 1e3 / reps
+    dev.plan_destroy(plan)
+    for b in bws + [bx, bq, ba, by]:
+        b.free()
+    total = per_call * CFG0_COPIES
+    res["batched"] = {"us_per_launch": round(us, 2), "GBps": round(total / us / 1e3, 1),
+                      "frac_of_peak": round(total / us / 1e3 / PEAK_HBM_GBS, 4), "gemvs_per_launch": CFG0_COPIES}
+    log(f"cfg0 2560x2560, {CFG0_COPIES} rotated GEMVs in one launch: {us:.2f} us, {total / us / 1e3:.1f} GB/s")
+    return checks, (ws, xs), dict(res, workload=(f"I2_S GEMV 2560x2560 batch 1, uniform ternary, per-tensor scale U(0.5,2), "
+                                       f"f32 N(0,1) activation int8-absmax quantised in-kernel, f32 output; one "
+                                       f"launch per call (sllm_gfx950_linear), hot and rotated over "
+                                       f"{CFG0_COPIES} tensors ({CFG0_COPIES * (n * n // 4 + 32) / 1e6:.0f} MB); "
+                                       f"and the {CFG0_COPIES} as one launch"),
+                        bytes_per_call=per_call, calls=calls)
+
+
 # the decode workload: random-init BitNet-b1.58-2B, a 1024-position KV prefix
 # of binary16 N(0,1) values (held as f32, as the reference's cache holds it)
 DECODE_PREFIX = 1024
@@ -209,11 +271,13 @@ def decode_bytes_per_token(cfg, npast):
     return i2s + lm + norms + kv, {"i2s": i2s, "lm_head": lm, "norms": norms, "kv": kv}
 
 
-def measure_decode(amd, dev, tokens=128, warm=8, graph=True):
+def measure_decode(amd, dev, tokens=128, warm=8, graph=True, inflight=None):
     """The decode step at BitNet-2B shape on the device's own greedy loop
     (one HIP graph per token, the output kernel feeding the next token): the
     first token after the prefix is traced for the CPU leg's bit-exact check,
-    then `warm` untimed and `tokens` timed tokens."""
+    then `warm` untimed and `tokens` timed tokens. Every generated id is kept
+    for the CPU leg's token witness. inflight: tokens the loop keeps enqueued
+    ahead of the host (the library's default when None)."""
     cfg = dict(amd.BITNET_2B)
     t0 = time.perf_counter()
     model = amd.synth_model(cfg, 0)
@@ -227,7 +291,9 @@ def measure_decode(amd, dev, tokens=128, warm=8, graph=True):
     dots0, acts0 = g.trace_read()
     g.trace_stop()
     g.set_graph(graph)
-    g.generate([], warm)
+    if inflight is not None:
+        g.set_inflight(inflight)
+    warm_ids = g.generate([], warm)
     dev.events(2)
     dev.sync()
     t0 = time.perf_counter()
@@ -242,12 +308,13 @@ def measure_decode(amd, dev, tokens=128, warm=8, graph=True):
     npast_mean = pos_first + 1 + (tokens - 1) / 2
     bpt, parts = decode_bytes_per_token(cfg, npast_mean)
     check = {"model": model, "k": k, "v": v, "token": tok0, "logits": logits0, "dots": dots0, "acts": acts0,
-             "ids": [int(x) for x in ids[:8]]}
+             "ids": [int(x) for x in warm_ids] + [int(x) for x in ids]}
     return check, {
         "workload": (f"random-init BitNet-b1.58-2B (30 blocks, 2560/6912, 20x128 heads, 5 KV heads, F16 128256 x 2560 "
                      f"output), KV cache of {DECODE_PREFIX} binary16 N(0,1) positions, greedy decode at positions "
                      f"{pos_first}..{pos_first + tokens - 1}, batch 1, "
-                     + ("one HIP graph per token" if graph else "the token's launches enqueued one by one")),
+                     + ("one HIP graph per token" if graph else "the token's launches enqueued one by one")
+                     + ("" if inflight is None else f", at most {inflight} token(s) enqueued ahead")),
         "tokens_per_s": round(tok_s, 1), "us_per_token": round(ms * 1e3 / tokens, 1),
         "wall_tokens_per_s": round(tokens / wall, 1), "tokens": tokens,
         "bytes_per_token": int(bpt), "bytes_parts": {a: int(b) for a, b in parts.items()},
@@ -387,13 +454,44 @@ def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
             "read_GBps": round(nbytes / read_ms / 1e6, 1), "bytes": nbytes}
 
 
-def cpu_decode(dec_check, seconds=10.0, threads=16):
-    """The decode parity check and baseline. Parity: the oracle's decode step
-    on the same model and prefix at the same position -- logits, every int32
-    dot and every activation of the GPU's traced token, bit for bit. Baseline:
-    the reference's own sllm_forward (oracle/_ref) restored to the same
-    prefix through its state file (src/forward.c:963-1100), greedy decode
-    timed for about `seconds` on `threads` threads of this host."""
+def host_cpu():
+    """The host's CPU model, the logical CPUs this process may run on and the
+    physical cores among them (distinct (package, core) pairs in
+    /proc/cpuinfo), and the thread counts the CPU baselines use: 1, 4 and
+    all (at most 16, the GPU box's CPU share)."""
+    try:
+        allowed = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = list(range(os.cpu_count() or 1))
+    model, cores = "", set()
+    try:
+        for block in open("/proc/cpuinfo").read().split("\n\n"):
+            d = {}
+            for line in block.splitlines():
+                if ":" in line:
+                    key, val = line.split(":", 1)
+                    d[key.strip()] = val.strip()
+            if "processor" not in d or int(d["processor"]) not in allowed:
+                continue
+            model = model or d.get("model name", "")
+            cores.add((d.get("physical id", "0"), d.get("core id", d["processor"])))
+    except OSError:
+        pass
+    top = min(16, len(allowed))
+    return {"cpu": model, "logical_cpus": len(allowed), "physical_cores": len(cores) or None,
+            "thread_counts": sorted({1, min(4, top), top})}
+
+
+def cpu_decode(dec_check, seconds=10.0, thread_counts=(16,)):
+    """The decode parity check, token witness and baseline. Parity: the
+    oracle's decode step on the same model and prefix at the same position --
+    logits, every int32 dot and every activation of the GPU's traced token,
+    bit for bit. Baseline: the reference's own sllm_forward (oracle/_ref)
+    restored to the same prefix through its state file (src/forward.c:963-1100),
+    greedy decode timed for about `seconds` at each thread count. Witness (as
+    the reference's tgbench checks its token stream, bench/tg_bench.c:300-321):
+    every run's greedy ids equal the GPU's ids position by position over the
+    positions both generated; a mismatch ends the bench."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     from oracle.gguf_synth import state_image
@@ -414,36 +512,51 @@ def cpu_decode(dec_check, seconds=10.0, threads=16):
     log(f"decode at position {DECODE_PREFIX}: logits, {wdots.size} int32 dots and {wacts.size} activations "
         f"match the oracle bit for bit")
     if not orc.ref_available():
-        return {"checked": True, "cpu": None}
+        return {"checked": True, "cpu": None, "witness": None}
     fd, path = tempfile.mkstemp(suffix=".slkv")
     os.close(fd)
+    runs, witnessed = [], 0
+    gpu_ids = c["ids"]
     try:
         with open(path, "wb") as f:
             f.write(state_image(cfg, n_ctx, c["k"], c["v"], want))
-        r = orc.RefDecoder(model, n_ctx, threads=threads)
-        r.state_load(path)
-        tok, pos, n = int(c["token"]), DECODE_PREFIX, 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < seconds and pos < n_ctx:
-            lg = r.forward(tok, pos)
-            tok = int(orc.ref().ref_argmax(orc._p(lg), lg.size))
-            pos += 1
-            n += 1
-        dt = time.perf_counter() - t0
-        r.close()
+        for threads in thread_counts:
+            r = orc.RefDecoder(model, n_ctx, threads=threads)
+            r.state_load(path)
+            tok, pos, ids = int(c["token"]), DECODE_PREFIX, []
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < seconds and pos < n_ctx:
+                lg = r.forward(tok, pos)
+                tok = int(orc.ref().ref_argmax(orc._p(lg), lg.size))
+                ids.append(tok)
+                pos += 1
+            dt = time.perf_counter() - t0
+            r.close()
+            n = min(len(ids), len(gpu_ids))
+            for i in range(n):
+                if ids[i] != gpu_ids[i]:
+                    raise SystemExit(f"bench: token witness: the reference's greedy id at position "
+                                     f"{DECODE_PREFIX + 1 + i} is {ids[i]}, the GPU's {gpu_ids[i]}")
+            witnessed = max(witnessed, n)
+            runs.append({"threads": threads, "tokens_per_s": round(len(ids) / dt, 2), "tokens": len(ids),
+                         "seconds": round(dt, 1)})
+            log(f"reference decode, {threads} threads: {len(ids) / dt:.2f} tokens/s; "
+                f"{n} greedy ids equal to the GPU's")
     finally:
         os.remove(path)
-    return {"checked": True, "cpu": {"tokens_per_s": round(n / dt, 2), "tokens": n, "seconds": round(dt, 1),
-                                     "threads": threads, "kind": "reference",
-                                     "sample": f"sllm_forward greedy from position {DECODE_PREFIX} after the same prefix"}}
+    best = max(runs, key=lambda r_: r_["tokens_per_s"])
+    return {"checked": True, "witness": witnessed,
+            "cpu": dict(best, kind="reference", runs=runs,
+                        sample=f"sllm_forward greedy from position {DECODE_PREFIX} after the same prefix, "
+                               f"at {', '.join(str(r_['threads']) for r_ in runs)} threads; the fastest")}
 
 
-def cpu_prefill(pre_check, seconds=10.0, threads=16):
+def cpu_prefill(pre_check, seconds=10.0, thread_counts=(16,)):
     """Parity: rows 0..15 of the chunk's logits against the oracle's
     token-by-token logits, bit for bit. Baseline: the reference's own
     sllm_forward_prefill_chunked (oracle/_ref) on the same model and tokens,
-    chunks of 16, as many chunks as fit in about `seconds` on `threads`
-    threads of this host."""
+    chunks of 16, as many chunks as fit in about `seconds`, at each thread
+    count of this host."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     c = pre_check
@@ -457,16 +570,22 @@ def cpu_prefill(pre_check, seconds=10.0, threads=16):
     if not orc.ref_available():
         return {"checked": True, "cpu": None}
     toks = np.asarray(c["tokens"] * (PREFILL_TOKENS // PREFILL_CHECK), np.int32)
-    r = orc.RefDecoder(model, PREFILL_TOKENS + 8, threads=threads)
-    done, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and done + 16 <= PREFILL_TOKENS:
-        r.forward_chunk(toks[done:done + 16], done)
-        done += 16
-    dt = time.perf_counter() - t0
-    r.close()
-    return {"checked": True, "cpu": {"tokens_per_s": round(done / dt, 2), "tokens": done, "seconds": round(dt, 1),
-                                     "threads": threads, "kind": "reference",
-                                     "sample": "sllm_forward_chunk, chunks of 16 from position 0, every token's logits"}}
+    runs = []
+    for threads in thread_counts:
+        r = orc.RefDecoder(model, PREFILL_TOKENS + 8, threads=threads)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds and done + 16 <= PREFILL_TOKENS:
+            r.forward_chunk(toks[done:done + 16], done)
+            done += 16
+        dt = time.perf_counter() - t0
+        r.close()
+        runs.append({"threads": threads, "tokens_per_s": round(done / dt, 2), "tokens": done, "seconds": round(dt, 1)})
+        log(f"reference chunked prefill, {threads} threads: {done / dt:.2f} tokens/s")
+    best = max(runs, key=lambda r_: r_["tokens_per_s"])
+    return {"checked": True, "cpu": dict(best, kind="reference", runs=runs,
+                                         sample="sllm_forward_chunk, chunks of 16 from position 0, every token's "
+                                                f"logits, at {', '.join(str(r_['threads']) for r_ in runs)} threads; "
+                                                "the fastest")}
 
 
 def cpu_gemm_check(checks):
@@ -482,7 +601,7 @@ def cpu_gemm_check(checks):
     log(f"{n} GEMM tokens (first, middle, last of every run) match the oracle bit for bit")
 
 
-def cpu_baseline(wl, checks, seconds=6.0):
+def cpu_baseline(wl, checks, seconds=6.0, cfg0=None, host=None):
     """The CPU leg. First the parity check: the GPU outputs kept in `checks`
     against the oracle, bit for bit. Then the baseline: the reference's CPU
     path (or the oracle's restatement) over a bounded sample of the same
@@ -491,27 +610,27 @@ def cpu_baseline(wl, checks, seconds=6.0):
     timed at 1 thread and at all threads; at all threads both with the
     reference's own split policy (src/forward.c:145-205, which keeps GEMVs
     below 512 rows per thread on one thread) and with every GEMV
-    distributed; the faster all-thread figure is the baseline."""
+    distributed; the faster all-thread figure is the baseline. cfg0: (the
+    2560 x 2560 tensors, their activations) timed the same way."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     for w, n_rows, n, x, got, what in checks:
         want = orc.linear(w, n_rows, n, x, orc.DOT_VNNI)[0]
         if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
             raise SystemExit(f"bench: output mismatch against the oracle ({what})")
-    log(f"{len(checks)} GPU outputs (sets 0 and 31, block layers 0 and 29) match the oracle bit for bit")
+    log(f"{len(checks)} GPU outputs (sets 0 and 31, block layers 0 and 29, cfg0 copies) match the oracle bit for bit")
     use_ref = orc.ref_available()
-    try:
-        threads = min(16, len(os.sched_getaffinity(0)))
-    except AttributeError:
-        threads = min(16, os.cpu_count() or 1)
+    host = host or host_cpu()
+    threads = host["thread_counts"][-1]
     Act = orc.Act
-    q_up, q_dn = np.empty(K_UP, np.int8), np.empty(N_FF, np.int8)
+    q_buf = np.empty(N_FF, np.int8)
     dots = np.empty(N_FF, np.int32)
     y = np.empty(N_FF, np.float32)
     P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
-    per_set = wl.step_bytes / wl.sets
 
-    def timed(nt, distribute_all):
+    def timed(nt, distribute_all, unit):
+        """unit(quant, run, i): the i-th unit of work (quantise + GEMVs);
+        returns the units done in about `seconds`."""
         if use_ref:
             r = orc.ref()
             r.sllm_i2s_select_auto()
@@ -526,18 +645,11 @@ def cpu_baseline(wl, checks, seconds=6.0):
             quant = o.orc_quant_act
             run = lambda w, n_rows, n, q, a: o.orc_gemv_epilogue_parallel(pool, P(w), n_rows, n, P(q), ctypes.byref(a),
                                                                           P(dots), P(y), path)
-        a_up, a_dn = Act(), Act()
-        sets_done = 0
+        done = 0
         t0 = time.perf_counter()
         while time.perf_counter() - t0 < seconds:
-            s = sets_done % wl.sets
-            ws = wl.host_w[s]
-            quant(P(wl.x_up[s]), K_UP, P(q_up), ctypes.byref(a_up))
-            run(ws[0], N_FF, K_UP, q_up, a_up)
-            run(ws[1], N_FF, K_UP, q_up, a_up)
-            quant(P(wl.x_dn[s]), N_FF, P(q_dn), ctypes.byref(a_dn))
-            run(ws[2], K_UP, N_FF, q_dn, a_dn)
-            sets_done += 1
+            unit(quant, run, done)
+            done += 1
         dt = time.perf_counter() - t0
         if use_ref:
             orc.ref().sllm_pool_destroy(pool)
@@ -545,31 +657,84 @@ def cpu_baseline(wl, checks, seconds=6.0):
         else:
             orc.orc().orc_pool_destroy(pool)
             isa = "vnni" if orc.orc().orc_vnni_supported() else "v3"
-        return {"GBps": sets_done * per_set / dt / 1e9, "sets": sets_done, "seconds": dt, "dot": isa}
+        return {"units": done, "seconds": dt, "dot": isa}
 
-    one = timed(1, 0)
-    policy = timed(threads, 0)
-    spread = timed(threads, 1) if use_ref else policy
-    best = max((policy, "reference split policy"), (spread, "every GEMV distributed"), key=lambda t: t[0]["GBps"])
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    def ffn_set(quant, run, i):
+        s = i % wl.sets
+        ws, a = wl.host_w[s], Act()
+        quant(P(wl.x_up[s]), K_UP, P(q_buf), ctypes.byref(a))
+        run(ws[0], N_FF, K_UP, q_buf, a)
+        run(ws[1], N_FF, K_UP, q_buf, a)
+        quant(P(wl.x_dn[s]), N_FF, P(q_buf), ctypes.byref(a))
+        run(ws[2], K_UP, N_FF, q_buf, a)
+
+    def sweep(unit, unit_bytes):
+        one = timed(1, 0, unit)
+        policy = timed(threads, 0, unit)
+        spread = timed(threads, 1, unit) if use_ref else policy
+        gbps = lambda t: t["units"] * unit_bytes / t["seconds"] / 1e9
+        best = max((policy, "reference split policy"), (spread, "every GEMV distributed"), key=lambda t: gbps(t[0]))
+        return one, policy, spread, best, gbps
+
+    one, policy, spread, best, gbps = sweep(ffn_set, wl.step_bytes / wl.sets)
     b = best[0]
-    return {
-        "value": round(b["GBps"], 3), "unit": "GB/s", "cores": threads,
+    out = {
+        "value": round(gbps(b), 3), "unit": "GB/s", "cores": threads,
         "kind": "reference" if use_ref else "port",
-        "sample": (f"{b['sets']} FFN sets (gate+up+down: quantise+GEMV+epilogue) cycling over the same "
+        "sample": (f"{b['units']} FFN sets (gate+up+down: quantise+GEMV+epilogue) cycling over the same "
                    f"{wl.sets} weight sets in {b['seconds']:.1f}s, {threads} threads, {best[1]}, dot={b['dot']}"),
-        "one_thread_GBps": round(one["GBps"], 3),
-        "policy_GBps": round(policy["GBps"], 3),
-        "all_distributed_GBps": round(spread["GBps"], 3),
-        "host": {"cpu": cpu_model, "nproc": os.cpu_count()},
+        "one_thread_GBps": round(gbps(one), 3),
+        "policy_GBps": round(gbps(policy), 3),
+        "all_distributed_GBps": round(gbps(spread), 3),
+        "host": host,
     }
+    if cfg0 is not None:
+        ws0, xs0 = cfg0
+        n = CFG0_N
+
+        def cfg0_call(quant, run, i):
+            a = Act()
+            quant(P(xs0[i % len(ws0)]), n, P(q_buf), ctypes.byref(a))
+            run(ws0[i % len(ws0)], n, n, q_buf, a)
+
+        one, policy, spread, best, gbps = sweep(cfg0_call, n * n // 4 + 4 + 8 * n)
+        out["cfg0"] = {"one_thread_GBps": round(gbps(one), 3), "policy_GBps": round(gbps(policy), 3),
+                       "all_distributed_GBps": round(gbps(spread), 3), "threads": threads,
+                       "best_us_per_call": round(best[0]["seconds"] / best[0]["units"] * 1e6, 1),
+                       "sample": f"quantise + GEMV + epilogue of the 2560x2560 tensors rotated over {len(ws0)}, "
+                                 f"{best[1]} at {threads} threads, dot={best[0]['dot']}"}
+        log(f"cfg0 reference CPU: {gbps(one):.2f} GB/s on 1 thread, {gbps(best[0]):.2f} GB/s on {threads}")
+    return out
+
+
+I2S_CODE_OBJECT = os.path.join(ROOT, "saphira-llm_amd", "build", "i2s_gfx950.hsaco")
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "gemv_slab_ffn32_traffic.json")
+
+
+def code_object_sha256():
+    """SHA-256 of the GEMV code object embedded in the library (the build's
+    i2s_gfx950.hsaco), or None when it is not on disk."""
+    import hashlib
+    try:
+        with open(I2S_CODE_OBJECT, "rb") as f:
+            return hashlib.sha256(f.read()).hexdigest()
+    except OSError:
+        return None
+
+
+def profiled_traffic():
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes over this same workload (scaled by the counters'
+    reading of a copy of known size) -- only when they were taken on the code
+    object this run uses (its SHA-256 is stored with them); else None."""
+    if not os.path.exists(TRAFFIC_JSON):
+        return None, "no traffic profile"
+    with open(TRAFFIC_JSON) as f:
+        t = json.load(f)
+    cur = code_object_sha256()
+    if cur is None or t.get("code_object_sha256") != cur:
+        return None, "traffic profile taken on another build of the GEMV code object"
+    return t.get("hbm_bytes_per_launch"), "rocprofv3 FETCH_SIZE / WRITE_SIZE of this code object (profiles/)"
 
 
 def main():
@@ -582,9 +747,12 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="decode leg: enqueue each token's launches instead of replaying a HIP graph "
                          "(rocprofv3's kernel tracer does not survive graph replay)")
-    ap.add_argument("--legs", default="gemv,block,decode,prefill,gemm",
-                    help="comma-separated legs to run beside the headline GEMV (block, decode, prefill, gemm); "
-                         "for profiling one leg")
+    ap.add_argument("--inflight", type=int, default=None,
+                    help="decode leg: tokens the device greedy loop keeps enqueued ahead of the host "
+                         "(default: the library's)")
+    ap.add_argument("--legs", default="cfg0,block,decode,prefill,gemm",
+                    help="comma-separated legs to run beside the headline GEMV (cfg0, block, decode, prefill, "
+                         "gemm); for profiling one leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the I2_S GEMV path runs on a single MI355X and "
@@ -621,24 +789,20 @@ def main():
     log(f"step {ms_per_step * 1e3:.1f} us wall, slab GEMV {gemv_avg * 1e3:.1f} us per launch "
         f"(events on the stream), {achieved:.0f} GB/s")
 
-    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # passes over this same command (scaled by the counters' reading of a copy
-    # of known size), or null when no such summary is present
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "gemv_slab_ffn32_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic, traffic_note = profiled_traffic()
 
     checks = wl.outputs([0, wl.sets - 1])
     legs = set(args.legs.split(","))
     block_checks, block30, dec_check, decode, gemm_checks, gemm = [], None, None, None, [], None
     pre_check, prefill = None, None
+    cfg0_checks, cfg0_host, cfg0 = [], None, None
+    if "cfg0" in legs:
+        cfg0_checks, cfg0_host, cfg0 = measure_cfg0(amd, dev)
     if "block" in legs:
         block_checks, block30 = measure_block_plan(amd, dev)
         log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
     if "decode" in legs:
-        dec_check, decode = measure_decode(amd, dev, graph=not args.no_graph)
+        dec_check, decode = measure_decode(amd, dev, graph=not args.no_graph, inflight=args.inflight)
         log(f"decode: {decode['tokens_per_s']} tokens/s ({decode['us_per_token']} us per token, "
             f"{decode['effective_GBps']} GB/s effective)")
     if "prefill" in legs:
@@ -665,11 +829,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": traffic_note,
             "kernel": "sllm_k_gemv_slab (96 GEMVs with in-kernel quantisation, one launch)",
             "avg_launch_us": round(gemv_avg * 1e3, 2), "bytes_per_launch": wl.gemv_bytes,
         },
         "calibration": calib,
+        "cfg0": cfg0,
         "block30": block30,
         "decode": decode,
         "prefill": prefill,
@@ -677,14 +842,18 @@ def main():
     }
     if not args.no_cpu:
         log("timing the CPU baseline")
-        out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks, args.cpu_seconds)
+        host = host_cpu()
+        out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks + cfg0_checks, args.cpu_seconds, cfg0_host, host)
         cpu_gemm_check(gemm_checks)
         if dec_check is not None:
-            dec = cpu_decode(dec_check, seconds=args.cpu_seconds)
-            out["decode"]["parity"] = "logits, int32 dots and activations of the first token bit-identical to the oracle"
+            dec = cpu_decode(dec_check, seconds=args.cpu_seconds, thread_counts=host["thread_counts"])
+            out["decode"]["parity"] = ("logits, int32 dots and activations of the first token bit-identical to the "
+                                       "oracle; greedy ids equal to the reference's own at every position both "
+                                       "generated")
+            out["decode"]["token_witness"] = dec["witness"]
             out["decode"]["cpu_baseline"] = dec["cpu"]
         if pre_check is not None:
-            pre = cpu_prefill(pre_check, seconds=args.cpu_seconds)
+            pre = cpu_prefill(pre_check, seconds=args.cpu_seconds, thread_counts=host["thread_counts"])
             out["prefill"]["parity"] = f"logits of positions 0..{PREFILL_CHECK - 1} bit-identical to the oracle"
             out["prefill"]["cpu_baseline"] = pre["cpu"]
     print(json.dumps(out), flush=True)

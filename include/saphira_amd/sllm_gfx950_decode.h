@@ -58,6 +58,10 @@ typedef struct sllm_gfx950_ctx   sllm_gfx950_ctx;
 /* Most tokens in one sllm_gfx950_forward_chunk (the reference's
  * SLLM_MAX_CHUNK, include/saphira_llm/forward.h:90, is 256). */
 #define SLLM_GFX950_DEC_MAX_CHUNK    512
+/* Tokens a greedy generation keeps enqueued ahead of the host
+ * (sllm_gfx950_ctx_set_inflight). */
+#define SLLM_GFX950_DEC_MAX_INFLIGHT     64
+#define SLLM_GFX950_DEC_DEFAULT_INFLIGHT 8
 
 /*
  * sllm_model_load (forward.h:33) for the device: copies every tensor of
@@ -157,12 +161,29 @@ const float *sllm_gfx950_ctx_logits(const sllm_gfx950_ctx *c);
 int  sllm_gfx950_ctx_argmax(sllm_gfx950_ctx *c, int32_t *token);
 
 /*
- * Fill positions [0, n_pos) of the cache from host memory -- k and v laid
- * out [layer][head_kv][pos][head_dim] with n_pos positions per head -- and
- * set n_past = n_pos: a restored context (the reference's sllm_state_load,
- * forward.h:162, without the file).
+ * sllm_state_load (forward.h:162, src/forward.c:1040-1121) without the file:
+ * fill positions [0, n_pos) of the cache from host memory -- k and v laid
+ * out [layer][head_kv][pos][head_dim] with n_pos positions per head --, clear
+ * positions [n_pos, n_ctx) of every (layer, KV head), restore the last
+ * position's logits (n_vocab floats, the state file's tail) and set n_past =
+ * n_pos. An empty-prompt sllm_gfx950_generate_greedy then continues from the
+ * restored logits' argmax, as the reference's does (src/forward.c:909-912).
+ * logits may be NULL: the context then has no last logits, and an
+ * empty-prompt generate is refused (SLLM_GFX950_ERR_ARG) until a forward.
  */
-int  sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos);
+int  sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos,
+                             const float *logits);
+
+/*
+ * How many tokens sllm_gfx950_generate_greedy keeps enqueued ahead of the
+ * host (1 .. SLLM_GFX950_DEC_MAX_INFLIGHT, default
+ * SLLM_GFX950_DEC_DEFAULT_INFLIGHT): before enqueueing token i it waits for
+ * token i - tokens to finish. Two or more keep the device busy; the bound
+ * keeps the number of dispatches outstanding at any time to tokens times a
+ * token's launches, where an unbounded loop would queue the whole
+ * generation at once.
+ */
+int  sllm_gfx950_ctx_set_inflight(sllm_gfx950_ctx *c, int32_t tokens);
 
 /*
  * Capture one token's launches in a HIP graph and replay it for every later

@@ -136,7 +136,8 @@ PROTOTYPES = {
     "sllm_gfx950_forward_prefill_chunked": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "sllm_gfx950_ctx_logits": (c_void_p, [c_void_p]),
     "sllm_gfx950_ctx_argmax": (c_int, [c_void_p, POINTER(c_int32)]),
-    "sllm_gfx950_ctx_kv_load": (c_int, [c_void_p, c_void_p, c_void_p, c_int32]),
+    "sllm_gfx950_ctx_kv_load": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "sllm_gfx950_ctx_set_inflight": (c_int, [c_void_p, c_int32]),
     "sllm_gfx950_ctx_set_graph": (c_int, [c_void_p, c_int]),
     "sllm_gfx950_trace_dots": (c_size_t, [c_void_p]),
     "sllm_gfx950_ctx_trace": (c_int, [c_void_p, c_void_p, c_void_p]),
@@ -549,10 +550,17 @@ class DeviceDecoder:
                                                 ptr(out)), "generate_greedy")
         return out[:n_new]
 
-    def kv_load(self, k, v, n_pos):
+    def kv_load(self, k, v, n_pos, logits=None):
+        """Restore a cache prefix of n_pos positions (k, v: [layer][head_kv]
+        [n_pos][head_dim]) and, given, the last position's logits."""
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
-        check(lib().sllm_gfx950_ctx_kv_load(self.c, ptr(k), ptr(v), n_pos), "ctx_kv_load")
+        lg = None if logits is None else np.ascontiguousarray(logits, np.float32)
+        check(lib().sllm_gfx950_ctx_kv_load(self.c, ptr(k), ptr(v), n_pos, None if lg is None else ptr(lg)),
+              "ctx_kv_load")
+
+    def set_inflight(self, tokens):
+        check(lib().sllm_gfx950_ctx_set_inflight(self.c, tokens), "ctx_set_inflight")
 
     def reset(self):
         check(lib().sllm_gfx950_ctx_reset(self.c), "ctx_reset")

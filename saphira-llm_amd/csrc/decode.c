@@ -312,6 +312,13 @@ struct sllm_gfx950_ctx {
     int           graph_on, graph_ready;
     hipGraph_t    graph;
     hipGraphExec_t graph_exec;
+    int           have_logits;     /* c->logits hold the last position's logits */
+    /* generate_greedy keeps at most `inflight` tokens enqueued ahead of the
+     * host: an event recorded after each token, waited on `inflight` tokens
+     * later */
+    int32_t       inflight;
+    hipEvent_t    inflight_ev[SLLM_GFX950_DEC_MAX_INFLIGHT];
+    int           n_inflight_ev;
 };
 
 /* Workgroups of a projection's GEMV: one row group each (decode GEMVs are a
@@ -423,6 +430,7 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
     if (c == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_new: host");
     c->m = m;
     c->n_ctx = n_ctx;
+    c->inflight = SLLM_GFX950_DEC_DEFAULT_INFLIGHT;
     const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
     const int32_t half = (m->n_rot - m->n_rot % 2) / 2;
     c->kv_per_layer = (size_t) m->n_head_kv * (size_t) n_ctx * (size_t) m->hd;
@@ -515,6 +523,9 @@ void sllm_gfx950_ctx_free(sllm_gfx950_ctx *c) {
         if (c->dev) hipFree(c->dev);
         if (c->chk.dev) hipFree(c->chk.dev);
     }
+    if (sllm_shim_is_open()) {
+        for (int i = 0; i < c->n_inflight_ev; ++i) hipEventDestroy(c->inflight_ev[i]);
+    }
     free(c->gargs);
     free(c->attn_args);
     free(c);
@@ -540,6 +551,7 @@ int sllm_gfx950_ctx_reset(sllm_gfx950_ctx *c) {
     if (he == hipSuccess) he = hipStreamSynchronize(s);
     if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_reset");
     c->n_past = 0;
+    c->have_logits = 0;
     return SLLM_GFX950_OK;
 }
 
@@ -635,6 +647,7 @@ int sllm_gfx950_forward(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, int32_t 
     if (st == SLLM_GFX950_OK) st = enqueue_token(c);
     if (st != SLLM_GFX950_OK) return st;
     c->n_past = pos + 1;
+    c->have_logits = 1;
     if (logits != NULL) {
         const hipStream_t s = sllm_shim_stream();
         hipError_t he = hipMemcpyAsync(logits, c->logits, (size_t) m->n_vocab * 4, hipMemcpyDeviceToHost, s);
@@ -671,6 +684,11 @@ int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, 
     }
     const int32_t base = c->n_past;
     const hipStream_t s = sllm_shim_stream();
+    while (c->n_inflight_ev < c->inflight) {
+        const hipError_t he = hipEventCreateWithFlags(&c->inflight_ev[c->n_inflight_ev], hipEventDisableTiming);
+        if (he != hipSuccess) return sllm_shim_hip_fail(he, "generate_greedy: events");
+        c->n_inflight_ev++;
+    }
     k_dec_step hs;
     memset(&hs, 0, sizeof hs);
     hs.pos = base;
@@ -694,6 +712,10 @@ int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, 
          * context (src/forward.c:909-920); out[0] is that token */
         if (n_new == 0) return SLLM_GFX950_OK;
         int32_t first = BOS_TOKEN;
+        if (base > 0 && !c->have_logits) {
+            return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "generate_greedy: no prompt and no last logits "
+                                  "(restore them with ctx_kv_load, or give a prompt)");
+        }
         if (base > 0) {
             const int st = sllm_gfx950_ctx_argmax(c, &first);
             if (st != SLLM_GFX950_OK) return st;
@@ -709,9 +731,22 @@ int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, 
         steps = n_new;
     }
     int st = set_step(c, &hs);
-    for (int32_t i = 0; i < steps && st == SLLM_GFX950_OK; ++i) st = enqueue_token(c);
+    for (int32_t i = 0; i < steps && st == SLLM_GFX950_OK; ++i) {
+        /* at most c->inflight tokens enqueued ahead: wait for token i - inflight */
+        hipEvent_t ev = c->inflight_ev[i % c->inflight];
+        if (i >= c->inflight) {
+            const hipError_t he = hipEventSynchronize(ev);
+            if (he != hipSuccess) return sllm_shim_hip_fail(he, "generate_greedy: in-flight wait");
+        }
+        st = enqueue_token(c);
+        if (st == SLLM_GFX950_OK) {
+            const hipError_t he = hipEventRecord(ev, s);
+            if (he != hipSuccess) return sllm_shim_hip_fail(he, "generate_greedy: in-flight event");
+        }
+    }
     if (st != SLLM_GFX950_OK) return st;
     c->n_past = base + steps;
+    c->have_logits = 1;
     const int32_t n_copy = n_new - gen_at;
     hipError_t he = hipSuccess;
     if (n_copy > 0) he = hipMemcpyAsync(out + gen_at, c->gen, (size_t) n_copy * 4, hipMemcpyDeviceToHost, s);
@@ -720,21 +755,63 @@ int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, 
     return SLLM_GFX950_OK;
 }
 
-int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos) {
+int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos,
+                            const float *logits) {
     if (c == NULL || k == NULL || v == NULL || n_pos < 0 || n_pos > c->n_ctx) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_kv_load: bad arguments");
     }
-    const size_t hd = (size_t) c->m->hd, rows = (size_t) c->m->n_layer * (size_t) c->m->n_head_kv;
+    const struct sllm_gfx950_model *m = c->m;
+    const size_t hd = (size_t) m->hd, rows = (size_t) m->n_layer * (size_t) m->n_head_kv;
+    const size_t dpitch = (size_t) c->n_ctx * hd * 4;
     const hipStream_t s = sllm_shim_stream();
     hipError_t he = hipSuccess;
     if (n_pos > 0) {
-        const size_t w = (size_t) n_pos * hd * 4, dpitch = (size_t) c->n_ctx * hd * 4;
+        const size_t w = (size_t) n_pos * hd * 4;
         he = hipMemcpy2DAsync(c->k_cache, dpitch, k, w, w, rows, hipMemcpyHostToDevice, s);
         if (he == hipSuccess) he = hipMemcpy2DAsync(c->v_cache, dpitch, v, w, w, rows, hipMemcpyHostToDevice, s);
     }
-    if (he == hipSuccess) he = hipStreamSynchronize(s);
+    /* positions past the restored prefix read as absent (zero) in every
+     * (layer, KV head), as src/forward.c:1098-1118 clears them */
+    if (he == hipSuccess && n_pos < c->n_ctx) {
+        const size_t from = (size_t) n_pos * hd * 4, w = dpitch - from;
+        he = hipMemset2DAsync((uint8_t *) c->k_cache + from, dpitch, 0, w, rows, s);
+        if (he == hipSuccess) he = hipMemset2DAsync((uint8_t *) c->v_cache + from, dpitch, 0, w, rows, s);
+    }
+    if (he == hipSuccess && logits != NULL) {
+        he = hipMemcpyAsync(c->logits, logits, (size_t) m->n_vocab * 4, hipMemcpyHostToDevice, s);
+    }
+    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_kv_load");
+    int st = SLLM_GFX950_OK;
+    if (logits != NULL) {
+        /* the restored logits' argmax becomes the step record's next token,
+         * what an empty-prompt generate continues from (src/forward.c:909-912) */
+        k_dec_step hs;
+        memset(&hs, 0, sizeof hs);
+        st = set_step(c, &hs);
+        uint64_t *partial = c->lm_partial;
+        const uint64_t *cpartial = c->lm_partial;
+        const float *lg = c->logits;
+        k_dec_step *step = c->step;
+        uint32_t nv = (uint32_t) m->n_vocab, nw = c->lm_wg;
+        void *kargs[] = { (void *) &lg, &nv, (void *) &partial };
+        void *aargs[] = { (void *) &cpartial, &nw, (void *) &lg, (void *) &step };
+        if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_keys, c->lm_wg, 1, 256, 0, kargs);
+        if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_argmax, 1, 1, 256, 0, aargs);
+    }
+    if (st != SLLM_GFX950_OK) return st;
+    he = hipStreamSynchronize(s);
     if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_kv_load");
     c->n_past = n_pos;
+    c->have_logits = logits != NULL;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_ctx_set_inflight(sllm_gfx950_ctx *c, int32_t tokens) {
+    if (c == NULL || tokens < 1 || tokens > SLLM_GFX950_DEC_MAX_INFLIGHT) {
+        return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_set_inflight: tokens must be 1..%d",
+                              SLLM_GFX950_DEC_MAX_INFLIGHT);
+    }
+    c->inflight = tokens;
     return SLLM_GFX950_OK;
 }
 
@@ -929,6 +1006,7 @@ int sllm_gfx950_forward_chunk(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, co
     if (st == SLLM_GFX950_OK) st = launch_chunk(c, n, base, logits != NULL);
     if (st != SLLM_GFX950_OK) return st;
     c->n_past = base + n;
+    c->have_logits = 1;
     if (logits != NULL) {
         he = hipMemcpyAsync(logits, c->chk.logits, (size_t) n * (size_t) m->n_vocab * 4, hipMemcpyDeviceToHost, s);
         if (he == hipSuccess) he = hipStreamSynchronize(s);

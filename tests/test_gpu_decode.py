@@ -283,3 +283,63 @@ def test_full_2b_decode_is_bit_exact(amd, orc, dev):
         g.trace_stop()
         g.close()
         o.close()
+
+
+def test_kv_load_restores_a_state_like_the_reference(amd, orc, dev):
+    """sllm_gfx950_ctx_kv_load against sllm_state_load (src/forward.c:1040-1121)
+    on a context that has already decoded past 1024 positions: the restored
+    512-position prefix, zeros from there on in every (layer, KV head) -- a
+    forward at a gapped position reads them as the reference does -- and the
+    restored last logits, whose argmax an empty-prompt generate continues
+    from (src/forward.c:909-912). Without logits, an empty-prompt generate
+    is refused until a forward."""
+    cfg = dict(TINY, n_layer=2)
+    model = amd.synth_model(cfg, 71)
+    n_ctx, n_pos, gap = 1100, 512, 700
+    g = amd.DeviceDecoder(dev, model, n_ctx)
+    print("[decode] kv_load after 1030 positions", flush=True)
+    try:
+        g.generate(_tokens(6, cfg["n_vocab"], 72), 1024)          # stale rows up to position 1029
+        assert g.n_past() == 1030
+        k, v = _kv_prefix(cfg, n_pos, 73)
+        last = np.random.default_rng(74).standard_normal(cfg["n_vocab"]).astype(np.float32)
+        last[[17, 402]] = 9.0                                    # a tie: the first maximum wins
+        g.kv_load(k, v, n_pos, logits=last)
+        assert g.n_past() == n_pos
+
+        def restored():
+            o = orc.Decoder(model, n_ctx)
+            ok, ov = o.caches()
+            ok[:, :, :n_pos] = k
+            ov[:, :, :n_pos] = v
+            return o
+
+        o = restored()
+        try:
+            got = g.generate([], 4)
+            want, nxt, pos = [], 17, n_pos
+            for _ in range(4):
+                want.append(nxt)
+                lg = o.forward(nxt, pos)
+                pos += 1
+                nxt = orc.orc().orc_argmax(orc._p(lg), cfg["n_vocab"])
+            assert list(got) == want
+        finally:
+            o.close()
+
+        g.kv_load(k, v, n_pos)                                   # no logits
+        out = np.zeros(2, np.int32)
+        assert amd.lib().sllm_gfx950_generate_greedy(g.m, g.c, None, 0, 2, amd.ptr(out)) == -1
+        o = restored()
+        try:
+            tok = _tokens(1, cfg["n_vocab"], 75)[0]
+            lg = o.forward(tok, gap)
+            assert np.array_equal(bits(g.forward(tok, gap)), bits(lg)), "gapped forward"
+            more = g.generate([], 2)                             # continues from the gapped forward
+            first = orc.orc().orc_argmax(orc._p(lg), cfg["n_vocab"])
+            second = orc.orc().orc_argmax(orc._p(o.forward(first, gap + 1)), cfg["n_vocab"])
+            assert list(more) == [first, second]
+        finally:
+            o.close()
+    finally:
+        g.close()
