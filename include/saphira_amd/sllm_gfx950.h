@@ -182,6 +182,28 @@ typedef struct sllm_gfx950_gemv_job {
  * plan uploads them once. */
 int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs);
 
+/* Device memory of sllm_gfx950_gemv_batch_noalloc: a static array on each
+ * device, held until the process ends. */
+#define SLLM_GFX950_NOALLOC_SCRATCH_BYTES (1u << 20)
+/* Most jobs one sllm_gfx950_gemv_batch_noalloc call takes. */
+#define SLLM_GFX950_NOALLOC_MAX_JOBS      1024
+
+/* sllm_gfx950_gemv_batch that allocates nothing. No counterpart in the
+ * reference (whose kernels allocate nothing per call either): it is for
+ * callers that cannot allocate device memory -- tight serving loops and
+ * harnesses that forbid hipMalloc. The job table, the per-workgroup
+ * descriptors and the quantised rows of streaming jobs that give no q / act
+ * go into a static device array of SLLM_GFX950_NOALLOC_SCRATCH_BYTES instead
+ * of per-call buffers; the results are sllm_gfx950_gemv_batch's, bit for
+ * bit. A batch whose tables and rows exceed the array, or more than
+ * SLLM_GFX950_NOALLOC_MAX_JOBS jobs, is refused with
+ * SLLM_GFX950_ERR_TOO_LARGE before anything is enqueued. Every call on one
+ * device shares that device's array: calls are serialised by a library lock
+ * and each waits for its launches before returning, so the array is free
+ * again when a call returns (nothing in it needs to start at zero). Like
+ * sllm_gfx950_gemv_batch, the call synchronises the library stream. */
+int sllm_gfx950_gemv_batch_noalloc(const sllm_gfx950_gemv_job *jobs, size_t n_jobs);
+
 typedef struct sllm_gfx950_plan sllm_gfx950_plan;
 int  sllm_gfx950_plan_create(const sllm_gfx950_gemv_job *jobs, size_t n_jobs,
                              sllm_gfx950_plan **plan);

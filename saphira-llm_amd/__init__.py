@@ -96,6 +96,7 @@ PROTOTYPES = {
     "sllm_gfx950_gemv_epilogue": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p]),
     "sllm_gfx950_linear": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p, c_void_p]),
     "sllm_gfx950_gemv_batch": (c_int, [POINTER(GemvJob), c_size_t]),
+    "sllm_gfx950_gemv_batch_noalloc": (c_int, [POINTER(GemvJob), c_size_t]),
     "sllm_gfx950_plan_create": (c_int, [POINTER(GemvJob), c_size_t, POINTER(c_void_p)]),
     "sllm_gfx950_plan_run": (c_int, [c_void_p]),
     "sllm_gfx950_plan_run_marked": (c_int, [c_void_p, c_int]),
@@ -304,6 +305,10 @@ class Device:
     def gemv_batch(self, jobs):
         arr = (GemvJob * len(jobs))(*jobs)
         check(self.lib.sllm_gfx950_gemv_batch(arr, len(jobs)), "gemv_batch")
+
+    def gemv_batch_noalloc(self, jobs):
+        arr = (GemvJob * len(jobs))(*jobs)
+        check(self.lib.sllm_gfx950_gemv_batch_noalloc(arr, len(jobs)), "gemv_batch_noalloc")
 
     def plan(self, jobs):
         arr = (GemvJob * len(jobs))(*jobs)

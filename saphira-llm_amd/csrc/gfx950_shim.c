@@ -135,7 +135,19 @@ static struct {
     /* scratch for the host-pointer row */
     void          *scratch;
     size_t         scratch_bytes;
+    /* the device address of noalloc.hip's static array on this device */
+    void          *noalloc_dev;
 } g;
+
+/* sllm_gfx950_gemv_batch_noalloc: host staging for its tables (static, so
+ * that the call allocates nothing), guarded by its own lock */
+static pthread_mutex_t g_noalloc_mtx = PTHREAD_MUTEX_INITIALIZER;
+static struct {
+    k_quant_job quant[SLLM_GFX950_NOALLOC_MAX_JOBS];
+    k_gemv_job  jobs[SLLM_GFX950_NOALLOC_MAX_JOBS];
+    uint8_t     is_slab[SLLM_GFX950_NOALLOC_MAX_JOBS];
+    uint8_t     tables[SLLM_GFX950_NOALLOC_SCRATCH_BYTES];
+} g_noalloc;
 
 static pthread_mutex_t g_mtx = PTHREAD_MUTEX_INITIALIZER;
 static char g_err[512];
@@ -275,6 +287,21 @@ int sllm_gfx950_open(int device) {
         hipModuleUnload(g.mod);
         st = hip_fail(e, "hipMalloc(row scratch)");
         goto out;
+    }
+    /* the no-allocation batch's device array, resolved once for this device
+     * with the device current */
+    {
+        const int rc = sllm_noalloc_resolve(device, &g.noalloc_dev);
+        if (rc != 0) {
+            hipFree(g.lin_scratch);
+            hipEventDestroy(g.ev_start);
+            hipEventDestroy(g.ev_stop);
+            hipStreamDestroy(g.stream);
+            hipModuleUnload(g.dec_mod);
+            hipModuleUnload(g.mod);
+            st = hip_fail((hipError_t) rc, "hipGetSymbolAddress(no-allocation scratch)");
+            goto out;
+        }
     }
     g.device = device;
     g.cu = prop.multiProcessorCount;
@@ -869,6 +896,54 @@ int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
     if (st != SLLM_GFX950_OK) return st;
     st = plan_launch(p, -1);
     sllm_gfx950_plan_destroy(p);      /* synchronises before freeing the tables */
+    return st;
+}
+
+/* A batch laid out in the static device array: quantised rows of streaming
+ * jobs first, then the tables, all staged on the host in static buffers and
+ * copied in on the library stream. */
+int sllm_gfx950_gemv_batch_noalloc(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
+    NEED_OPEN();
+    if (n_jobs == 0) return SLLM_GFX950_OK;
+    if (jobs == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemv_batch_noalloc: NULL job list");
+    if (n_jobs > SLLM_GFX950_NOALLOC_MAX_JOBS) {
+        return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemv_batch_noalloc: %zu jobs, at most %d", n_jobs,
+                    SLLM_GFX950_NOALLOC_MAX_JOBS);
+    }
+    const size_t cap = SLLM_GFX950_NOALLOC_SCRATCH_BYTES;
+    const size_t rows = align256(plan_scratch_bytes(jobs, n_jobs));
+    if (rows > cap) {
+        return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemv_batch_noalloc: %zu bytes of quantised rows, the array holds %zu",
+                    rows, cap);
+    }
+    pthread_mutex_lock(&g_noalloc_mtx);
+    sllm_gfx950_plan p;
+    memset(&p, 0, sizeof p);
+    p.scratch_dev = g.noalloc_dev;
+    int st = plan_layout(jobs, n_jobs, &p, g_noalloc.quant, g_noalloc.jobs, g_noalloc.is_slab);
+    if (st == SLLM_GFX950_OK) {
+        const size_t qbytes = p.n_quant * sizeof(k_quant_job), jbytes = n_jobs * sizeof(k_gemv_job);
+        const size_t dbytes = ((size_t) p.slab_wg + p.st_wg) * sizeof(k_wg_desc);
+        const size_t bytes = qbytes + jbytes + dbytes;
+        if (rows + bytes > cap) {
+            st = fail(SLLM_GFX950_ERR_TOO_LARGE, "gemv_batch_noalloc: %zu bytes of rows and tables, the array holds %zu",
+                      rows + bytes, cap);
+        } else {
+            uint8_t *host = g_noalloc.tables;
+            memcpy(host, g_noalloc.quant, qbytes);
+            memcpy(host + qbytes, g_noalloc.jobs, jbytes);
+            k_wg_desc *sd = (k_wg_desc *) (host + qbytes + jbytes);
+            plan_descriptors(&p, g_noalloc.jobs, g_noalloc.is_slab, sd, sd + p.slab_wg);
+            p.tables_dev = (uint8_t *) g.noalloc_dev + rows;
+            hipError_t e = hipMemcpyAsync(p.tables_dev, host, bytes, hipMemcpyHostToDevice, g.stream);
+            if (e != hipSuccess) st = hip_fail(e, "gemv_batch_noalloc: tables");
+            if (st == SLLM_GFX950_OK) st = plan_launch(&p, -1);
+            /* the array and the host staging are free again once the stream drains */
+            e = hipStreamSynchronize(g.stream);
+            if (st == SLLM_GFX950_OK && e != hipSuccess) st = hip_fail(e, "gemv_batch_noalloc: synchronise");
+        }
+    }
+    pthread_mutex_unlock(&g_noalloc_mtx);
     return st;
 }
 

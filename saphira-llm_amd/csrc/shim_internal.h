@@ -67,4 +67,8 @@ SLLM_HIDDEN int         sllm_shim_launch(hipFunction_t f, uint32_t gx, uint32_t 
 SLLM_HIDDEN int         sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz,
                                             uint32_t block, uint32_t lds, void **args);
 
+/* noalloc.hip: the address on `device` (current) of the static array behind
+ * sllm_gfx950_gemv_batch_noalloc; 0 or the HIP error */
+SLLM_HIDDEN int         sllm_noalloc_resolve(int device, void **out);
+
 #endif /* SLLM_SHIM_INTERNAL_H */
