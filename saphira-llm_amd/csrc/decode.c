@@ -540,11 +540,13 @@ int sllm_gfx950_ctx_reset(sllm_gfx950_ctx *c) {
     const hipStream_t s = sllm_shim_stream();
     hipError_t he = hipSuccess;
     if (c->n_past > 0) {
-        /* the live prefix of every (layer, KV head): n_past rows each */
+        /* the live prefix of every (layer, KV head): n_past key rows each, and
+         * n_past positions of every 8-dimension value slice */
         const size_t hd = (size_t) c->m->hd, rows = (size_t) c->m->n_layer * (size_t) c->m->n_head_kv;
         he = hipMemset2DAsync(c->k_cache, (size_t) c->n_ctx * hd * 4, 0, (size_t) c->n_past * hd * 4, rows, s);
         if (he == hipSuccess) {
-            he = hipMemset2DAsync(c->v_cache, (size_t) c->n_ctx * hd * 4, 0, (size_t) c->n_past * hd * 4, rows, s);
+            he = hipMemset2DAsync(c->v_cache, (size_t) c->n_ctx * PV_SLICE * 4, 0, (size_t) c->n_past * PV_SLICE * 4,
+                                  rows * (hd / PV_SLICE), s);
         }
     }
     if (he == hipSuccess) he = hipMemsetAsync(c->step, 0, sizeof(k_dec_step), s);
@@ -762,25 +764,46 @@ int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, 
     }
     const struct sllm_gfx950_model *m = c->m;
     const size_t hd = (size_t) m->hd, rows = (size_t) m->n_layer * (size_t) m->n_head_kv;
-    const size_t dpitch = (size_t) c->n_ctx * hd * 4;
+    const size_t n_sl = hd / PV_SLICE, np = (size_t) n_pos, nc = (size_t) c->n_ctx;
+    const size_t dpitch = nc * hd * 4, vpitch = nc * PV_SLICE * 4;
     const hipStream_t s = sllm_shim_stream();
+    /* the values go in slice-major, [layer][KV head][dimension / 8][position][8]:
+     * rearranged on the host first */
+    float *vs = NULL;
+    if (n_pos > 0) {
+        vs = malloc(rows * np * hd * sizeof *vs);
+        if (vs == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_kv_load: host staging");
+        for (size_t r = 0; r < rows; ++r) {
+            for (size_t sl = 0; sl < n_sl; ++sl) {
+                float *dst = vs + (r * n_sl + sl) * np * PV_SLICE;
+                for (size_t p = 0; p < np; ++p) memcpy(dst + p * PV_SLICE, v + (r * np + p) * hd + sl * PV_SLICE, PV_SLICE * 4);
+            }
+        }
+    }
     hipError_t he = hipSuccess;
     if (n_pos > 0) {
-        const size_t w = (size_t) n_pos * hd * 4;
+        const size_t w = np * hd * 4, wv = np * PV_SLICE * 4;
         he = hipMemcpy2DAsync(c->k_cache, dpitch, k, w, w, rows, hipMemcpyHostToDevice, s);
-        if (he == hipSuccess) he = hipMemcpy2DAsync(c->v_cache, dpitch, v, w, w, rows, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess) he = hipMemcpy2DAsync(c->v_cache, vpitch, vs, wv, wv, rows * n_sl, hipMemcpyHostToDevice, s);
     }
     /* positions past the restored prefix read as absent (zero) in every
      * (layer, KV head), as src/forward.c:1098-1118 clears them */
     if (he == hipSuccess && n_pos < c->n_ctx) {
-        const size_t from = (size_t) n_pos * hd * 4, w = dpitch - from;
+        const size_t from = np * hd * 4, w = dpitch - from;
         he = hipMemset2DAsync((uint8_t *) c->k_cache + from, dpitch, 0, w, rows, s);
-        if (he == hipSuccess) he = hipMemset2DAsync((uint8_t *) c->v_cache + from, dpitch, 0, w, rows, s);
+        if (he == hipSuccess) {
+            const size_t vfrom = np * PV_SLICE * 4;
+            he = hipMemset2DAsync((uint8_t *) c->v_cache + vfrom, vpitch, 0, vpitch - vfrom, rows * n_sl, s);
+        }
     }
     if (he == hipSuccess && logits != NULL) {
         he = hipMemcpyAsync(c->logits, logits, (size_t) m->n_vocab * 4, hipMemcpyHostToDevice, s);
     }
-    if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_kv_load");
+    if (he != hipSuccess) {
+        hipStreamSynchronize(s);               /* the staging buffer may still be read */
+        free(vs);
+        return sllm_shim_hip_fail(he, "ctx_kv_load");
+    }
     int st = SLLM_GFX950_OK;
     if (logits != NULL) {
         /* the restored logits' argmax becomes the step record's next token,
@@ -798,8 +821,9 @@ int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, 
         if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_keys, c->lm_wg, 1, 256, 0, kargs);
         if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_argmax, 1, 1, 256, 0, aargs);
     }
-    if (st != SLLM_GFX950_OK) return st;
     he = hipStreamSynchronize(s);
+    free(vs);
+    if (st != SLLM_GFX950_OK) return st;
     if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_kv_load");
     c->n_past = n_pos;
     c->have_logits = logits != NULL;

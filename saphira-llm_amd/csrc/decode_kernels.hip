@@ -378,7 +378,9 @@ __device__ __forceinline__ void dec_variant(const dec_stage &st, const gemv_job 
 
 struct dec_attn {
     const float    *q, *k, *v;          // projections: q [n_head*hd], k / v [n_kv*hd]
-    float          *k_cache, *v_cache;  // this layer's caches [n_kv][n_ctx][hd]
+    float          *k_cache;            // this layer's keys [n_kv][n_ctx][hd]
+    float          *v_cache;            // this layer's values [n_kv][hd / 8][n_ctx][8]: a slice of
+                                        // eight dimensions of every position is contiguous
     const float    *rope;               // [n_ctx][half] (cos, sin)
     float          *scores;             // [n_head][sc_stride]
     float          *out;                // [n_head*hd]
@@ -477,7 +479,7 @@ __device__ __forceinline__ void scores_body(const dec_attn &A) {
     if (s0 >= npast) return;
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, half = A.half, hd4 = hd / 4;
     float *kc = A.k_cache + (size_t) kvh * A.n_ctx * hd;
-    float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd;
+    float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd;               // this KV head's value slices
     const float *cs = A.rope + (size_t) pos * (half > 0 ? half : 1) * 2;
     const float *q = A.q + (size_t) t * A.n_head * hd;
     float *scores = A.scores + (size_t) t * A.n_head * A.sc_stride;
@@ -517,7 +519,7 @@ __device__ __forceinline__ void scores_body(const dec_attn &A) {
         const float val = rope_apply(ki, tid, half);
         kt[pos - s0][tid] = val;
         kc[(size_t) pos * hd + tid] = val;
-        vc[(size_t) pos * hd + tid] = vnew;
+        vc[((size_t) (tid / PV_SLICE) * A.n_ctx + pos) * PV_SLICE + tid % PV_SLICE] = vnew;
     }
 #pragma unroll
     for (int u = 0; u < KT_LOADS; ++u) {
@@ -659,7 +661,8 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
     const float *scores = A.scores + (size_t) t * A.n_head * ss;
     const uint32_t nb = npast / 8, nt = nb * 8;
-    const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d0;
+    // this workgroup's slice of V: dimensions d0 .. d0 + 7 of every position, contiguous
+    const float *vc = A.v_cache + ((size_t) kvh * A.n_ctx * hd + (size_t) blockIdx.y * A.n_ctx * PV_SLICE);
 
     auto group_sum = [](const float (&e)[8]) {
         const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
@@ -727,7 +730,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
         for (int u = 0; u < PV_VLOADS; ++u) {
             const uint32_t f = pt + (uint32_t) u * PV_PTHREADS;
             const uint32_t sp = min(base + f / PV_G4, npast - 1);
-            vr[u] = *G_CAST(const f32x4, vc + (size_t) sp * hd + 4 * (f % PV_G4));
+            vr[u] = *G_CAST(const f32x4, vc + (size_t) sp * PV_SLICE + 4 * (f % PV_G4));
         }
     };
     if (wave > 0) load_v(0);
@@ -1294,7 +1297,9 @@ sllm_k_chk_kv_store(dec_attn A) {
     for (uint32_t i = threadIdx.x; i < nq; i += ATT_THREADS) qs[i] = q[i];
     for (uint32_t i = threadIdx.x; i < gqa; i += ATT_THREADS) {
         ks[i] = k[i];
-        A.v_cache[((size_t) (i / hd) * A.n_ctx + pos) * hd + i % hd] = v[i];
+        // values slice-major: [KV head][dimension / 8][position][dimension % 8]
+        A.v_cache[(((size_t) (i / hd) * (hd / PV_SLICE) + (i % hd) / PV_SLICE) * A.n_ctx + pos) * PV_SLICE +
+                  i % PV_SLICE] = v[i];
     }
     for (uint32_t i = threadIdx.x; i < 2 * half; i += ATT_THREADS) cst[i] = cs[i];
     __syncthreads();
@@ -1563,7 +1568,8 @@ sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
     const uint32_t last_tok = min(tb + CP_TOK, n_tok) - 1;
     const uint32_t npast_max = A.chunk_base + last_tok + 1, npast_min = A.chunk_base + tb + 1;
     const uint32_t d = min(64u * half_id + lane, hd - 1);
-    const float *vc = A.v_cache + (size_t) kvh * A.n_ctx * hd + d;
+    // dimension d of position s: slice d / 8, element d % 8
+    const float *vc = A.v_cache + ((size_t) kvh * (hd / PV_SLICE) + d / PV_SLICE) * A.n_ctx * PV_SLICE + d % PV_SLICE;
     const float *prow[CP_TOK];                     // token rows past n_tok read the last one's
     float acc[CP_TOK];
     uint32_t npast_t[CP_TOK];                      // each token's own (past n_tok: never written out)
@@ -1578,7 +1584,7 @@ sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
     float va[16], vb[16];
     auto load16 = [&](uint32_t s, float (&v)[16]) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) v[q] = *G_CAST(const float, vc + (size_t) min(s + (uint32_t) q, npast_max - 1) * hd);
+        for (int q = 0; q < 16; ++q) v[q] = *G_CAST(const float, vc + (size_t) min(s + (uint32_t) q, npast_max - 1) * PV_SLICE);
     };
     // eight positions at which every token of the block is live, with p of
     // them in pc; the next eight's p go to pn. Scalar loads return out of
