@@ -26,7 +26,7 @@
 typedef struct k_dec_step {
     int32_t        token, pos, next, advance;
     uint64_t       reserved0;
-    uint32_t       reserved1, err;
+    uint32_t       lm_next, err;
     const int32_t *feed;
     int32_t       *gen;
     int32_t        n_feed, i_feed, n_gen, cap_gen;
@@ -62,6 +62,7 @@ typedef struct k_dec_lm {
     const uint16_t *embd;
     float          *logits;
     uint64_t       *partial;
+    k_dec_step     *step;
     float           eps;
     uint32_t        n_embd, n_vocab, pad;
 } k_dec_lm;
@@ -100,7 +101,7 @@ _Static_assert(sizeof(k_dec_step) == 64, "k_dec_step must match dec_step");
 _Static_assert(sizeof(k_dec_gemv_args) == 296, "k_dec_gemv_args must match dec_gemv_args");
 _Static_assert(sizeof(k_dec_stage) == 72, "k_dec_stage must match dec_stage");
 _Static_assert(sizeof(k_dec_attn) == 104, "k_dec_attn must match dec_attn");
-_Static_assert(sizeof(k_dec_lm) == 64, "k_dec_lm must match dec_lm");
+_Static_assert(sizeof(k_dec_lm) == 72, "k_dec_lm must match dec_lm");
 _Static_assert(sizeof(k_chk_prep) == 80, "k_chk_prep must match chk_prep");
 _Static_assert(sizeof(k_chk_lm) == 40, "k_chk_lm must match chk_lm");
 
@@ -491,7 +492,7 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
                 (uint32_t) n_ctx, sc_stride, 0 };
         }
         c->lm_args = (k_dec_lm) { c->down, c->ffn_inp, m->output_norm, m->tok_embd, c->logits, c->lm_partial,
-                                  m->eps, (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };
+                                  c->step, m->eps, (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };
         if ((st = sllm_shim_decode_function("sllm_k_dec_gemv", &c->f_gemv)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_dec_scores", &c->f_scores)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_dec_pv", &c->f_pv)) == SLLM_GFX950_OK &&

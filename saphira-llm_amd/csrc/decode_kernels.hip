@@ -40,7 +40,7 @@ struct dec_step {
     int32_t        next;        // argmax of the last logits
     int32_t        advance;     // nonzero: the step moves on by itself (greedy loop)
     uint64_t       reserved0;
-    uint32_t       reserved1;
+    uint32_t       lm_next;     // output passes handed out past the grid's first ones (reset per token)
     uint32_t       err;
     const int32_t *feed;        // prompt tokens still to consume: feed[i_feed .. n_feed)
     int32_t       *gen;         // generated tokens
@@ -989,10 +989,11 @@ struct dec_lm {
     const uint16_t *embd;        // [n_vocab][n_embd] f16, the tied output projection
     float          *logits;
     uint64_t       *partial;     // one argmax key per workgroup
+    dec_step       *step;        // its lm_next: the pass counter
     float           eps;
     uint32_t        n_embd, n_vocab, pad;
 };
-static_assert(sizeof(dec_lm) == 64, "dec_lm must match decode.c");
+static_assert(sizeof(dec_lm) == 72, "dec_lm must match decode.c");
 
 constexpr int LM_THREADS = 256;
 constexpr uint32_t LM_ROWS = 64;        // rows per pass: four lanes per row
@@ -1012,49 +1013,84 @@ __device__ __forceinline__ uint64_t argmax_key(float s, uint32_t row) {
 // acc[j][0..7], element 32i + 8j + l going into acc[j][l] by FMA; then
 // acc0 += acc2, acc1 += acc3, acc0 += acc1; t_l = acc0[l] + acc0[l+4];
 // (t0 + t1) + (t2 + t3). n_embd % 32 == 0, so there is no scalar tail.
-// Workgroup w takes the 64-row passes w, w + G, ... (G = gridDim.x); each
-// lane streams its rows in batches of eight 16-byte loads with the next
-// batch always in flight, and the first batch is issued before the norm.
+// Passes of 64 rows: workgroup w takes pass w first, then passes handed out
+// in order by an atomic counter (the step record's lm_next, which the argmax
+// kernel and the host reset for every token), so that workgroups that stream
+// faster take more passes. Each lane streams its rows in batches of eight
+// 16-byte loads with the next batch always in flight -- across a pass
+// boundary too: the next pass's number is taken a whole pass ahead. The
+// final residual and the norm weight are loaded before the first batch, so
+// that the norm does not wait behind the weight stream (loads complete in
+// order).
+constexpr int LM_XV = (int) (LM_MAX_E / 4 / LM_THREADS);   // float4 of the residual per thread
+
 extern "C" __global__ void __launch_bounds__(LM_THREADS)
 sllm_k_dec_lm_head(dec_lm L) {
     __shared__ __attribute__((aligned(16))) float xn[LM_MAX_E];
     __shared__ double red_d[LM_THREADS / 64], lane_d[4];
     __shared__ uint64_t red_k[LM_THREADS / 64];
+    __shared__ uint32_t s_next;
     const uint32_t e = L.n_embd, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t j = lane % 4, steps = e / 32, nb = (steps + LM_UNROLL - 1) / LM_UNROLL;
     const uint32_t n_pass = (L.n_vocab + LM_ROWS - 1) / LM_ROWS;
-    const uint32_t my_passes = blockIdx.x < n_pass ? (n_pass - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
-    const uint32_t total = my_passes * nb;               // (pass, batch) items of this workgroup
-    auto row_of = [&](uint32_t item) {
-        const uint32_t pass = blockIdx.x + (min(item, total - 1) / nb) * gridDim.x;
-        return min(pass * LM_ROWS + wave * 16 + lane / 4, L.n_vocab - 1);
-    };
-    auto load = [&](uint32_t item, u32x4 (&h)[LM_UNROLL]) {
-        const uint32_t it = min(item, total - 1), b = it % nb;
-        const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) row_of(it) * e) + j;
+    uint32_t *next_ctr = &L.step->lm_next;
+
+    // (1) the final residual and the norm weight, then the first batch
+    f32x4 av[LM_XV], bv[LM_XV], wv[LM_XV];
+#pragma unroll
+    for (int u = 0; u < LM_XV; ++u) {
+        const uint32_t i = min(4u * (tid + (uint32_t) u * LM_THREADS), e - 4);
+        av[u] = *G_CAST(const f32x4, L.a + i);
+        bv[u] = *G_CAST(const f32x4, L.b + i);
+        wv[u] = *G_CAST(const f32x4, L.norm_w + i);
+    }
+    auto load = [&](uint32_t pass, uint32_t b, u32x4 (&h)[LM_UNROLL]) {
+        const uint32_t row = min(pass * LM_ROWS + wave * 16 + lane / 4, L.n_vocab - 1);
+        const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) row * e) + j;
 #pragma unroll
         for (int u = 0; u < LM_UNROLL; ++u) h[u] = __builtin_nontemporal_load(w + 4 * min(b * LM_UNROLL + u, steps - 1));
     };
     u32x4 ha[LM_UNROLL], hb[LM_UNROLL];
-    if (total > 0) load(0, ha);
+    uint32_t p = blockIdx.x;
+    if (p < n_pass) load(p, 0, ha);
+    uint32_t grabbed = 0;                                    // thread 0: the counter's value, used a pass later
+    if (tid == 0 && p < n_pass) grabbed = atomicAdd(next_ctr, 1u);
 
+    // (2) RMSNorm of a + b into LDS
     double part = 0.0;
-    for (uint32_t i = tid; i < e; i += LM_THREADS) {
-        const float v = L.a[i] + L.b[i];
-        xn[i] = v;
-        part += (double) (v * v);
+#pragma unroll
+    for (int u = 0; u < LM_XV; ++u) {
+        const uint32_t i = 4u * (tid + (uint32_t) u * LM_THREADS);
+        if (i < e) {
+            const f32x4 v = av[u] + bv[u];
+            *reinterpret_cast<f32x4 *>(xn + i) = v;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part += (double) (v[c] * v[c]);
+        }
     }
     const float mean = rms_mean(part, e, red_d, lane_d, [&](uint32_t k) { return L.a[k] + L.b[k]; });
     const float scale = 1.0f / sqrtf(mean + L.eps);
-    for (uint32_t i = tid; i < e; i += LM_THREADS) xn[i] = (scale * xn[i]) * L.norm_w[i];
+#pragma unroll
+    for (int u = 0; u < LM_XV; ++u) {
+        const uint32_t i = 4u * (tid + (uint32_t) u * LM_THREADS);
+        if (i < e) {
+            f32x4 x = *reinterpret_cast<const f32x4 *>(xn + i);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = (scale * x[c]) * wv[u][c];
+            *reinterpret_cast<f32x4 *>(xn + i) = x;
+        }
+    }
+    if (tid == 0) s_next = gridDim.x + grabbed;
     __syncthreads();
+    uint32_t pn = s_next;                                   // the pass after p
+    __syncthreads();
+    if (tid == 0 && pn < n_pass) grabbed = atomicAdd(next_ctr, 1u);
 
     uint64_t best = 0;
     float acc[8];
 #pragma unroll
     for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
-    auto consume = [&](uint32_t item, const u32x4 (&h)[LM_UNROLL]) {
-        const uint32_t b = item % nb;
+    auto consume = [&](uint32_t pass, uint32_t b, const u32x4 (&h)[LM_UNROLL]) {
 #pragma unroll
         for (int u = 0; u < LM_UNROLL; ++u) {
             const uint32_t step = b * LM_UNROLL + (uint32_t) u;
@@ -1073,7 +1109,6 @@ sllm_k_dec_lm_head(dec_lm L) {
             for (int l = 0; l < 8; ++l) r[l] = r[l] + __shfl_xor(r[l], 1, 64);      // acc0 += acc1
             const float t0 = r[0] + r[4], t1 = r[1] + r[5], t2 = r[2] + r[6], t3 = r[3] + r[7];
             const float sdot = (t0 + t1) + (t2 + t3);
-            const uint32_t pass = blockIdx.x + (item / nb) * gridDim.x;
             const uint32_t row = pass * LM_ROWS + wave * 16 + lane / 4;
             if (j == 0 && row < L.n_vocab) {
                 G_CAST(float, L.logits)[row] = sdot;
@@ -1084,15 +1119,30 @@ sllm_k_dec_lm_head(dec_lm L) {
             for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
         }
     };
-    // pairs of items: the next batch is loaded before the current one is used
-    uint32_t item = 0;
-    for (; item + 1 < total; item += 2) {
-        load(item + 1, hb);
-        consume(item, ha);
-        load(item + 2, ha);
-        consume(item + 1, hb);
+    // items (pass p, batch b) in order, the next one loaded before the
+    // current one is used, buffers alternating by the item's parity
+    uint32_t b = 0, it = 0;
+    while (p < n_pass) {                                  // uniform
+        uint32_t p2 = p, b2 = b + 1;
+        if (b2 == nb) { p2 = pn; b2 = 0; }
+        if (it & 1u) {
+            if (p2 < n_pass) load(p2, b2, ha);
+            consume(p, b, hb);
+        } else {
+            if (p2 < n_pass) load(p2, b2, hb);
+            consume(p, b, ha);
+        }
+        ++it;
+        p = p2;
+        b = b2;
+        if (b == 0 && p < n_pass) {                       // entered pass p: learn the one after it
+            if (tid == 0) s_next = gridDim.x + grabbed;
+            __syncthreads();
+            pn = s_next;
+            __syncthreads();
+            if (tid == 0 && pn < n_pass) grabbed = atomicAdd(next_ctr, 1u);
+        }
     }
-    if (item < total) consume(item, ha);
 
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -1131,6 +1181,7 @@ sllm_k_dec_argmax(const uint64_t *__restrict__ partial, uint32_t n, const float 
     int32_t next = best == 0 ? 0 : (int32_t) (0xffffffffu - (uint32_t) best);
     if (__builtin_isnan(logits[0])) next = 0;
     st->next = next;
+    st->lm_next = 0;                                      // the next output pass counter starts over
     if (st->advance) {
         if (st->i_feed < st->n_feed) {
             st->token = st->feed[st->i_feed];
