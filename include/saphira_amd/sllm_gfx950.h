@@ -121,6 +121,13 @@ int   sllm_gfx950_event_elapsed(int i, int j, float *ms);
 int   sllm_gfx950_copy(void *dst, const void *src, size_t bytes);
 int   sllm_gfx950_checksum(const void *src, size_t bytes, uint32_t *partials, uint32_t n_partials);
 
+/* Diagnostic (no counterpart in the reference): the decode step's expf --
+ * the restatement of the C library's expf that the softmax's scalar tail
+ * runs on the device -- for the floats whose bit patterns are
+ * first + i * stride (mod 2^32), i < n, into out (device memory, n floats),
+ * so that a test can hold the device build against the host library. */
+int   sllm_gfx950_diag_expf(uint32_t first, uint32_t stride, uint32_t n, float *out);
+
 /* ------------------------------------------------------------------ */
 /* device-pointer kernels (asynchronous, library stream)               */
 /* ------------------------------------------------------------------ */

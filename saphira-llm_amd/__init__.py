@@ -91,6 +91,7 @@ PROTOTYPES = {
     "sllm_gfx950_event_elapsed": (c_int, [c_int, c_int, POINTER(c_float)]),
     "sllm_gfx950_copy": (c_int, [c_void_p, c_void_p, c_size_t]),
     "sllm_gfx950_checksum": (c_int, [c_void_p, c_size_t, c_void_p, c_uint]),
+    "sllm_gfx950_diag_expf": (c_int, [c_uint, c_uint, c_uint, c_void_p]),
     "sllm_gfx950_quant_act": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
     "sllm_gfx950_gemv": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
     "sllm_gfx950_gemv_epilogue": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p]),
@@ -152,6 +153,7 @@ SYNTH_PROTOTYPES = {
     "sllm_synth_normal": (None, [c_uint64, c_size_t, c_void_p]),
     "sllm_synth_normal_f16": (None, [c_uint64, c_size_t, c_void_p, c_int]),
     "sllm_expf_mismatches": (c_uint64, [c_uint64, c_uint64, c_int, POINTER(ctypes.c_uint32)]),
+    "sllm_expf_strided": (None, [c_uint, c_uint, c_uint64, c_void_p, c_int]),
 }
 
 _lib = None

@@ -1740,3 +1740,17 @@ sllm_k_chk_keys(const float *__restrict__ logits, uint32_t n, uint64_t *__restri
         partial[blockIdx.x] = best;
     }
 }
+
+// Diagnostic (no counterpart in the reference): the softmax tail's expf
+// (libm_expf.h, the C library's algorithm) on the device, for the float
+// whose bit pattern is first + i * stride (mod 2^32), i < n -- so that a
+// test can hold the device build against the host library's expf.
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_diag_expf(uint32_t first, uint32_t stride, uint32_t n, float *__restrict__ out) {
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = c_expf_tab[threadIdx.x];
+    __syncthreads();
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        out[i] = sllm_libm_expf(__uint_as_float(first + i * stride), tab);
+    }
+}

@@ -510,6 +510,17 @@ int sllm_gfx950_checksum(const void *src, size_t bytes, uint32_t *partials, uint
     return launch(g.k_checksum, n_partials, 256, 0, args);
 }
 
+int sllm_gfx950_diag_expf(uint32_t first, uint32_t stride, uint32_t n, float *out) {
+    NEED_OPEN();
+    if (n == 0) return SLLM_GFX950_OK;
+    if (out == NULL) return fail(SLLM_GFX950_ERR_ARG, "diag_expf: NULL output");
+    hipFunction_t f;
+    HIP_TRY(hipModuleGetFunction(&f, g.dec_mod, "sllm_k_diag_expf"));
+    const uint32_t grid = n / 256 + 1 < 4096u ? n / 256 + 1 : 4096u;
+    void *args[] = { &first, &stride, &n, &out };
+    return launch(f, grid, 256, 0, args);
+}
+
 int sllm_gfx950_quant_act(const float *x, size_t n, size_t n_tok, int8_t *q,
                           sllm_gfx950_act *act) {
     NEED_OPEN();

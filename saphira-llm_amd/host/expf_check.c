@@ -72,3 +72,41 @@ uint64_t sllm_expf_mismatches(uint64_t lo, uint64_t hi, int threads, uint32_t *f
     }
     return bad;
 }
+
+typedef struct strided {
+    uint32_t first, stride;
+    uint64_t lo, hi;
+    float   *out;
+} strided;
+
+static void *expf_strided(void *arg) {
+    strided *s = arg;
+    for (uint64_t i = s->lo; i < s->hi; ++i) {
+        const uint32_t b = s->first + (uint32_t) i * s->stride;
+        float x;
+        memcpy(&x, &b, 4);
+        s->out[i] = expf(x);
+    }
+    return NULL;
+}
+
+/* the host C library's expf of the floats whose bit patterns are
+ * first + i * stride (mod 2^32), i < n, into out, over `threads` threads:
+ * the reference values for the device build's expf */
+void sllm_expf_strided(uint32_t first, uint32_t stride, uint64_t n, float *out, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    strided sp[64];
+    pthread_t tid[64];
+    int made[64] = { 0 };
+    for (int t = 0; t < threads; ++t) {
+        sp[t] = (strided) { first, stride, n * (uint64_t) t / (uint64_t) threads,
+                            n * (uint64_t) (t + 1) / (uint64_t) threads, out };
+        if (t > 0) made[t] = pthread_create(&tid[t], NULL, expf_strided, &sp[t]) == 0;
+    }
+    expf_strided(&sp[0]);
+    for (int t = 1; t < threads; ++t) {
+        if (made[t]) pthread_join(tid[t], NULL);
+        else expf_strided(&sp[t]);
+    }
+}

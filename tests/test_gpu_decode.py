@@ -343,3 +343,55 @@ def test_kv_load_restores_a_state_like_the_reference(amd, orc, dev):
             o.close()
     finally:
         g.close()
+
+
+def test_full_2b_decode_after_a_1024_position_prefix(amd, orc, dev):
+    """The decode leg's workload in full: all 30 blocks at BitNet-2B shape
+    with the 128256-row F16 output, over a restored 1024-position cache of
+    binary16 values, two tokens at positions 1024 and 1025 -- every int32 dot,
+    every activation and the logits bit for bit against the oracle."""
+    cfg = dict(amd.BITNET_2B)
+    n_pos = 1024
+    print("[decode] building the 2B model and a 1024-position prefix", flush=True)
+    model = amd.synth_model(cfg, 2)
+    k, v = _kv_prefix(cfg, n_pos, 81)
+    g, o = amd.DeviceDecoder(dev, model, n_pos + 4), orc.Decoder(model, n_pos + 4)
+    ok, ov = o.caches()
+    ok[:, :, :n_pos] = k
+    ov[:, :, :n_pos] = v
+    g.kv_load(k, v, n_pos)
+    g.trace_start()
+    try:
+        for i, tok in enumerate(_tokens(2, cfg["n_vocab"], 82)):
+            print(f"[decode] 2B token at {n_pos + i}", flush=True)
+            _compare_step(g, o, tok, n_pos + i, "2b-prefix")
+    finally:
+        g.trace_stop()
+        g.close()
+        o.close()
+
+
+def test_device_expf_matches_the_c_library(amd, dev):
+    """The softmax tail's expf as the device build computes it
+    (sllm_gfx950_diag_expf) against the host C library, bit for bit, on
+    every 17th float bit pattern (252,645,136 inputs; NaN against NaN counts
+    as equal) -- the host build of the same restatement is held against the
+    library on all 2^32 in tests/test_decode_host.py."""
+    stride, chunk = 17, 1 << 26
+    total = (1 << 32) // stride + 1
+    out = dev.alloc(4 * chunk)
+    bad = 0
+    try:
+        for start in range(0, total, chunk):
+            n = min(chunk, total - start)
+            first = (start * stride) & 0xFFFFFFFF
+            amd.check(amd.lib().sllm_gfx950_diag_expf(first, stride, n, out.vp), "diag_expf")
+            got = out.download(np.float32, n)
+            want = np.empty(n, np.float32)
+            amd.synth_lib().sllm_expf_strided(first, stride, n, amd.ptr(want), 16)
+            diff = (got.view(np.uint32) != want.view(np.uint32)) & ~(np.isnan(got) & np.isnan(want))
+            bad += int(diff.sum())
+            print(f"[expf] {start + n}/{total} inputs, {bad} differ", flush=True)
+    finally:
+        out.free()
+    assert bad == 0

@@ -425,3 +425,44 @@ def test_config1_rotated_sets_match_oracle(amd, orc, dev):
     dev.plan_destroy(plan)
     for b in bufs:
         b.free()
+
+
+def test_thirty_block_plan_matches_oracle(amd, orc, dev):
+    """Config 2 as the bench runs it: the decode GEMVs of 30 independently
+    seeded BitNet-2B blocks (q/o 2560x2560, k/v 640x2560, gate/up 6912x2560,
+    down 2560x6912; 521 MB), f32 N(0,1) inputs quantised in-kernel, as one
+    plan -- a single launch of 210 GEMVs. Every raw int32 dot and every f32
+    output of all 210 against the oracle (quantiser, VNNI dots over a pool of
+    host threads, epilogue)."""
+    say("thirty-block plan")
+    pool = orc.Pool(16)
+    jobs, checks, bufs = [], [], []
+    try:
+        for il in range(30):
+            xs = {}
+            for slot, n in ((0, 2560), (1, 2560), (2, 2560), (3, 6912)):
+                x = amd.synth_normal(amd.synth_seed(2, 0, il, 200 + slot), n)
+                bx = dev.put(x)
+                bufs.append(bx)
+                xs[slot] = (x, bx)
+            for m, (name, n_rows, n, slot) in enumerate(BLOCK):
+                w = tensor(amd, amd.synth_seed(2, 0, il, m), n_rows, n)
+                bw, by, bi = dev.put(w), dev.alloc(4 * n_rows), dev.alloc(4 * n_rows)
+                bufs += [bw, by, bi]
+                jobs.append(amd.GemvJob(bw.ptr, n_rows, n, xs[slot][1].ptr, None, None, by.ptr, bi.ptr))
+                checks.append((w, n_rows, n, xs[slot][0], by, bi, f"layer {il} {name}"))
+        plan = dev.plan(jobs)
+        dev.plan_run(plan)
+        dev.sync()
+        dev.plan_destroy(plan)
+        say("thirty-block plan: checking 210 GEMVs")
+        for w, n_rows, n, x, by, bi, what in checks:
+            q, s, t = orc.quant_act(x)
+            d = np.empty(n_rows, np.int32)
+            pool.gemv(w, n_rows, n, q, d, orc.DOT_VNNI)
+            np.testing.assert_array_equal(bi.download(np.int32, n_rows), d, err_msg=what)
+            assert f32_bits_equal(by.download(np.float32, n_rows), orc.epilogue_np(d, t, s, orc.scale(w, n_rows * n))), what
+    finally:
+        pool.close()
+        for b in bufs:
+            b.free()
