@@ -14,6 +14,11 @@ before the timed region.
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Beside the headline line the JSON carries:
+  cfg0     one 2560 x 2560 GEMV per launch, hot and rotated over 192 tensors,
+           and the 192 as one launch;
+  dropin   the same FFN workload through the host-pointer row that a patched
+           reference forward.c calls (sllm_kdispatch_*), each call copying
+           across PCIe and waiting: what the drop-in costs per GEMV;
   block30  the decode GEMVs of 30 independently seeded 2B blocks, one launch;
   decode   a random-init BitNet-b1.58-2B decode step (30 blocks, F16 output,
            greedy argmax) after a 1024-position binary16 KV prefix, tokens/s
@@ -240,6 +245,73 @@ def measure_cfg0(amd, dev, calls=2000):
                                        f"{CFG0_COPIES} tensors ({CFG0_COPIES * (n * n // 4 + 32) / 1e6:.0f} MB); "
                                        f"and the {CFG0_COPIES} as one launch"),
                         bytes_per_call=per_call, calls=calls)
+
+
+def measure_dropin(amd, wl, passes=2):
+    """The drop-in row's cost on the FFN workload: what the reference's own
+    forward pass pays per GEMV once its sllm_gemv and quantiser calls go to
+    the gfx950 row (sllm_kdispatch_*, host pointers, src/forward.c:196-205 and
+    :651-788). Every tensor of the 32 sets is registered once (uploaded under
+    its host address); then per set, as the reference orders it: quantise the
+    FFN input, GEMV gate, GEMV up, quantise the down input, GEMV down --
+    each call copies its q / rows across PCIe and waits for the result.
+    Host wall clock; the epilogue is the reference's, on the host. Returns
+    the figures and the outputs of sets 0 and 31 for the oracle check."""
+    lib = amd.lib()
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    for ws in wl.host_w:
+        for w, (_, n_rows, n) in zip(ws, SHAPES):
+            amd.check(lib.sllm_gfx950_tensor_register(P(w), n_rows, n), "tensor_register")
+    amd.check(lib.sllm_kdispatch_select(b"gfx950"), "kdispatch_select")
+    q = np.empty(N_FF, np.int8)
+    dots = [np.empty(n_rows, np.int32) for _, n_rows, _ in SHAPES]
+    acts = [amd.Act(), amd.Act()]
+    checks = []
+
+    def one_set(s):
+        ws = wl.host_w[s]
+        lib.sllm_kdispatch_quant_act(P(wl.x_up[s]), K_UP, P(q), ctypes.byref(acts[0]))
+        lib.sllm_kdispatch_gemv(P(ws[0]), N_FF, K_UP, P(q), P(dots[0]))
+        lib.sllm_kdispatch_gemv(P(ws[1]), N_FF, K_UP, P(q), P(dots[1]))
+        lib.sllm_kdispatch_quant_act(P(wl.x_dn[s]), N_FF, P(q), ctypes.byref(acts[1]))
+        lib.sllm_kdispatch_gemv(P(ws[2]), K_UP, N_FF, P(q), P(dots[2]))
+
+    try:
+        for s in range(wl.sets):
+            one_set(s)
+        t0 = time.perf_counter()
+        for _ in range(passes):
+            for s in range(wl.sets):
+                one_set(s)
+        dt = time.perf_counter() - t0
+        for s in (0, wl.sets - 1):
+            one_set(s)
+            for m, (name, n_rows, n) in enumerate(SHAPES):
+                w = wl.host_w[s][m]
+                a = acts[0] if m < 2 else acts[1]
+                w_scale = np.frombuffer(w[n_rows * n // 4:n_rows * n // 4 + 4].tobytes(), np.float32)[0]
+                pq = np.float32(w_scale) / np.float32(a.scale)
+                y = (dots[m] - np.int32(a.sum)).astype(np.float32) * pq
+                x = wl.x_up[s] if n == K_UP else wl.x_dn[s]
+                checks.append((w, n_rows, n, x, y, f"drop-in row set {s} {name}"))
+    finally:
+        lib.sllm_kdispatch_reset()
+        for ws in wl.host_w:
+            for w in ws:
+                lib.sllm_gfx950_tensor_unregister(P(w))
+    gemvs = passes * wl.sets * len(SHAPES)
+    us_per_gemv = dt * 1e6 / gemvs
+    us_per_set = dt * 1e6 / (passes * wl.sets)
+    set_bytes = wl.step_bytes / wl.sets
+    log(f"drop-in row: {us_per_set:.1f} us per FFN set ({us_per_gemv:.1f} us per GEMV incl. its share of "
+        f"the quantiser calls), {set_bytes / us_per_set / 1e3:.1f} GB/s")
+    return checks, {
+        "workload": ("the FFN workload through the host-pointer row the patched reference forward.c "
+                     "calls (sllm_kdispatch_quant_act / sllm_kdispatch_gemv): per set 2 quantiser calls "
+                     "and 3 GEMVs, each copying q / int32 rows across PCIe and synchronising; host epilogue"),
+        "us_per_set": round(us_per_set, 1), "us_per_gemv": round(us_per_gemv, 1),
+        "GBps": round(set_bytes / us_per_set / 1e3, 1), "sets_timed": passes * wl.sets,
+        "clock": "host wall clock"}
 
 
 # the decode workload: random-init BitNet-b1.58-2B, a 1024-position KV prefix
@@ -618,7 +690,8 @@ def cpu_baseline(wl, checks, seconds=6.0, cfg0=None, host=None):
         want = orc.linear(w, n_rows, n, x, orc.DOT_VNNI)[0]
         if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
             raise SystemExit(f"bench: output mismatch against the oracle ({what})")
-    log(f"{len(checks)} GPU outputs (sets 0 and 31, block layers 0 and 29, cfg0 copies) match the oracle bit for bit")
+    log(f"{len(checks)} GPU outputs (sets 0 and 31, block layers 0 and 29, cfg0 copies, drop-in row) "
+        f"match the oracle bit for bit")
     use_ref = orc.ref_available()
     host = host or host_cpu()
     threads = host["thread_counts"][-1]
@@ -750,9 +823,9 @@ def main():
     ap.add_argument("--inflight", type=int, default=None,
                     help="decode leg: tokens the device greedy loop keeps enqueued ahead of the host "
                          "(default: the library's)")
-    ap.add_argument("--legs", default="cfg0,block,decode,prefill,gemm",
-                    help="comma-separated legs to run beside the headline GEMV (cfg0, block, decode, prefill, "
-                         "gemm); for profiling one leg")
+    ap.add_argument("--legs", default="cfg0,dropin,block,decode,prefill,gemm",
+                    help="comma-separated legs to run beside the headline GEMV (cfg0, dropin, block, decode, "
+                         "prefill, gemm); for profiling one leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the I2_S GEMV path runs on a single MI355X and "
@@ -796,8 +869,13 @@ def main():
     block_checks, block30, dec_check, decode, gemm_checks, gemm = [], None, None, None, [], None
     pre_check, prefill = None, None
     cfg0_checks, cfg0_host, cfg0 = [], None, None
+    dropin_checks, dropin = [], None
     if "cfg0" in legs:
         cfg0_checks, cfg0_host, cfg0 = measure_cfg0(amd, dev)
+    if "dropin" in legs:
+        dropin_checks, dropin = measure_dropin(amd, wl)
+        dropin["device_resident_us_per_set"] = round(gemv_avg * 1e3 / SETS, 2)
+        dropin["x_device_resident"] = round(dropin["us_per_set"] / (gemv_avg * 1e3 / SETS), 1)
     if "block" in legs:
         block_checks, block30 = measure_block_plan(amd, dev)
         log(f"block plan (30 layers, 210 GEMVs): {block30['us_per_launch']} us per launch, {block30['GBps']} GB/s")
@@ -835,6 +913,7 @@ def main():
         },
         "calibration": calib,
         "cfg0": cfg0,
+        "dropin": dropin,
         "block30": block30,
         "decode": decode,
         "prefill": prefill,
@@ -843,7 +922,7 @@ def main():
     if not args.no_cpu:
         log("timing the CPU baseline")
         host = host_cpu()
-        out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks + cfg0_checks, args.cpu_seconds, cfg0_host, host)
+        out["cpu_baseline"] = cpu_baseline(wl, checks + block_checks + cfg0_checks + dropin_checks, args.cpu_seconds, cfg0_host, host)
         cpu_gemm_check(gemm_checks)
         if dec_check is not None:
             dec = cpu_decode(dec_check, seconds=args.cpu_seconds, thread_counts=host["thread_counts"])

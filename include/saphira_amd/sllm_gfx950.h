@@ -288,7 +288,10 @@ int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, 
 /* Upload a packed I2_S tensor (n_rows*n/4 code bytes + 32-byte tail)
  * byte-for-byte and remember it under its host address, so the kernel-row
  * functions below can be handed the same borrowed pointers the reference's
- * model holds (include/saphira_llm/forward.h:27-31). */
+ * model holds (include/saphira_llm/forward.h:27-31). Registering the same
+ * range again (a second model over one image) shares the device copy and
+ * counts a reference; unregister drops one and frees the copy with the last.
+ * A range that overlaps a registered one otherwise is refused (-1). */
 int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n);
 int sllm_gfx950_tensor_unregister(const void *packed);
 /* The device copy of a registered host address (inside any tensor), or NULL. */

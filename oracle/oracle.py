@@ -21,6 +21,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libsllm_ref.so")
+# the same reference sources with src/forward.c patched to install the gfx950
+# row (gfx950_forward.patch): the reference's own forward pass, GEMVs on the GPU
+REF_GFX950_PATH = os.path.join(HERE, "_ref", "libsllm_ref_gfx950.so")
 
 DOT_SCALAR, DOT_V3, DOT_VNNI = 0, 1, 2
 
@@ -108,6 +111,7 @@ _REF_PROTOS = {
 # (include/saphira_llm/isa.h:35-42 orders V3 below VNNI)
 _orc = None
 _ref = None
+_ref_gfx950 = None
 
 
 def _bind(path, protos):
@@ -137,6 +141,18 @@ def ref():
     if _ref is None:
         _ref = _bind(REF_PATH, _REF_PROTOS)
     return _ref
+
+
+def ref_gfx950_available():
+    return os.path.exists(REF_GFX950_PATH)
+
+
+def ref_gfx950():
+    """The patched reference build (needs a gfx950 device to load a model)."""
+    global _ref_gfx950
+    if _ref_gfx950 is None:
+        _ref_gfx950 = _bind(REF_GFX950_PATH, _REF_PROTOS)
+    return _ref_gfx950
 
 
 def _p(a):
@@ -346,28 +362,29 @@ class RefDecoder:
     """The reference's own sllm_forward (oracle/_ref) on a GGUF image of the
     same model."""
 
-    def __init__(self, model, n_ctx, threads=1):
+    def __init__(self, model, n_ctx, threads=1, lib=None):
         from oracle.gguf_synth import gguf_image
+        self.lib = lib if lib is not None else ref()
         self.image = np.frombuffer(gguf_image(model), np.uint8)
         st = c_int()
-        self.r = ref().ref_model_open(_p(self.image), self.image.nbytes, ctypes.byref(st))
+        self.r = self.lib.ref_model_open(_p(self.image), self.image.nbytes, ctypes.byref(st))
         if not self.r:
             raise ValueError(f"ref_model_open: status {st.value}")
-        self.c = ref().ref_ctx_new(self.r, n_ctx)
-        self.pool = ref().ref_pool_create(threads) if threads > 1 else None
+        self.c = self.lib.ref_ctx_new(self.r, n_ctx)
+        self.pool = self.lib.ref_pool_create(threads) if threads > 1 else None
         if self.pool:
-            ref().ref_ctx_set_pool(self.c, self.pool)
+            self.lib.ref_ctx_set_pool(self.c, self.pool)
         self.n_vocab = model["cfg"]["n_vocab"]
 
     def state_load(self, path):
         """sllm_state_load: the cache prefix and last logits from a state file."""
-        st = ref().ref_state_load(self.r, self.c, path.encode())
+        st = self.lib.ref_state_load(self.r, self.c, path.encode())
         if st != 0:
             raise ValueError(f"sllm_state_load: status {st}")
 
     def forward(self, token, pos):
         logits = np.empty(self.n_vocab, np.float32)
-        st = ref().ref_forward(self.r, self.c, token, pos, _p(logits))
+        st = self.lib.ref_forward(self.r, self.c, token, pos, _p(logits))
         if st != 0:
             raise ValueError(f"sllm_forward: status {st}")
         return logits
@@ -376,7 +393,7 @@ class RefDecoder:
         """sllm_forward_chunk: logits [n][n_vocab] of n tokens at base.."""
         t = np.ascontiguousarray(tokens, np.int32)
         logits = np.empty((t.size, self.n_vocab), np.float32)
-        st = ref().ref_forward_chunk(self.r, self.c, _p(t), t.size, base, _p(logits))
+        st = self.lib.ref_forward_chunk(self.r, self.c, _p(t), t.size, base, _p(logits))
         if st != 0:
             raise ValueError(f"sllm_forward_chunk: status {st}")
         return logits
@@ -385,18 +402,18 @@ class RefDecoder:
         """sllm_forward_prefill_chunked: logits [n][n_vocab]."""
         t = np.ascontiguousarray(tokens, np.int32)
         logits = np.empty((t.size, self.n_vocab), np.float32)
-        st = ref().ref_prefill_chunked(self.r, self.c, _p(t), t.size, chunk, _p(logits))
+        st = self.lib.ref_prefill_chunked(self.r, self.c, _p(t), t.size, chunk, _p(logits))
         if st != 0:
             raise ValueError(f"sllm_forward_prefill_chunked: status {st}")
         return logits
 
     def close(self):
         if self.c:
-            ref().ref_ctx_free(self.c)
+            self.lib.ref_ctx_free(self.c)
             self.c = None
         if self.pool:
-            ref().sllm_pool_destroy(self.pool)
+            self.lib.sllm_pool_destroy(self.pool)
             self.pool = None
         if self.r:
-            ref().ref_model_close(self.r)
+            self.lib.ref_model_close(self.r)
             self.r = None

@@ -19,6 +19,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* ------------------------------------------------------------------ */
 /* the embedded code object                                            */
@@ -69,6 +70,7 @@ static const char *const k_stream_names[N_LPR] = {
 };
 
 #define QUANT_THREADS 256
+#define QUANT_HOST_THREADS 1024   /* sllm_k_quant_host: QH_THREADS */
 
 /* ------------------------------------------------------------------ */
 /* library state                                                       */
@@ -78,6 +80,7 @@ typedef struct reg_tensor {
     const uint8_t *host;
     size_t         bytes;    /* n_rows*n/4 + 32 */
     uint8_t       *dev;
+    size_t         refs;     /* registrations of this exact range */
 } reg_tensor;
 
 /* One row for the list quantiser (mirror of quant_job in i2s_kernels.hip). */
@@ -114,7 +117,7 @@ static struct {
     size_t         hbm;
     char           name[520];
     hipModule_t    mod, dec_mod;
-    hipFunction_t  k_quant, k_quant_list;
+    hipFunction_t  k_quant, k_quant_list, k_quant_host, k_host_done;
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
@@ -132,9 +135,20 @@ static struct {
     /* registry for the host-pointer row */
     reg_tensor    *regs;
     size_t         n_regs, cap_regs;
-    /* scratch for the host-pointer row */
-    void          *scratch;
-    size_t         scratch_bytes;
+    /* the host-pointer row's staging: pinned host memory the kernels read
+     * and write directly (pin_q: the list-quantiser table, act and q as
+     * last returned; pin_io: x in, int32 rows out), and the device copy of
+     * the quantised vector the GEMVs read, valid for the host buffer last_q
+     * while its bytes equal pin_q's */
+    uint8_t       *pin_q, *pin_q_dev;
+    size_t         pin_q_cap;
+    uint8_t       *pin_io, *pin_io_dev;
+    size_t         pin_io_cap;
+    int8_t        *dq;
+    size_t         dq_cap;
+    const int8_t  *last_q;
+    size_t         last_n;
+    uint32_t       seq;          /* last value asked of the pinned done word */
     /* the device address of noalloc.hip's static array on this device */
     void          *noalloc_dev;
 } g;
@@ -205,6 +219,8 @@ const char *sllm_gfx950_status_string(int status) {
 static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_quant, g.mod, "sllm_k_quant_act"));
     HIP_TRY(hipModuleGetFunction(&g.k_quant_list, g.mod, "sllm_k_quant_list"));
+    HIP_TRY(hipModuleGetFunction(&g.k_quant_host, g.mod, "sllm_k_quant_host"));
+    HIP_TRY(hipModuleGetFunction(&g.k_host_done, g.mod, "sllm_k_host_done"));
     HIP_TRY(hipModuleGetFunction(&g.k_copy, g.mod, "sllm_k_copy"));
     HIP_TRY(hipModuleGetFunction(&g.k_checksum, g.mod, "sllm_k_checksum"));
     HIP_TRY(hipModuleGetFunction(&g.k_slab, g.mod, "sllm_k_gemv_slab"));
@@ -319,7 +335,9 @@ void sllm_gfx950_close(void) {
         hipStreamSynchronize(g.stream);
         for (size_t i = 0; i < g.n_regs; ++i) hipFree(g.regs[i].dev);
         free(g.regs);
-        if (g.scratch) hipFree(g.scratch);
+        if (g.pin_q) hipHostFree(g.pin_q);
+        if (g.pin_io) hipHostFree(g.pin_io);
+        if (g.dq) hipFree(g.dq);
         if (g.lin_scratch) hipFree(g.lin_scratch);
         for (int i = 0; i < g.n_events; ++i) hipEventDestroy(g.events[i]);
         free(g.events);
@@ -972,7 +990,16 @@ static int single_launch(const sllm_gfx950_gemv_job *j) {
     if (slab_path(kj.n_rows, kj.k)) {
         kj.variant = (uint32_t) slab_variant_for(kj.k);
         uint32_t rows, flags = 0;
-        const uint32_t wg = job_workgroups(&kj, 1, &rows);
+        uint32_t wg = job_workgroups(&kj, 1, &rows);
+        if (g.slab_kib == 0) {
+            /* The slab size targets batches, whose many jobs fill the chip;
+             * a launch of its own spreads over one group of rows per
+             * workgroup, up to one workgroup per CU. */
+            const uint32_t group = 4u * (uint32_t) (64 / k_slab_geom[kj.variant].lpr);
+            const uint32_t n_groups = (kj.n_rows + group - 1) / group;
+            const uint32_t want = n_groups < (uint32_t) g.cu ? n_groups : (uint32_t) g.cu;
+            if (wg < want) wg = want;
+        }
         void *args[] = { (void *) &no_jobs, (void *) &no_descs, &zero, &kj, &flags };
         return launch(g.k_slab, wg, SLAB_THREADS, 0, args);
     }
@@ -1156,6 +1183,11 @@ int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n) {
     const uint8_t *h = packed;
     size_t pos = 0;
     while (pos < g.n_regs && g.regs[pos].host < h) ++pos;
+    if (pos < g.n_regs && g.regs[pos].host == h && g.regs[pos].bytes == bytes) {
+        /* a second model over the same image: share the device copy */
+        g.regs[pos].refs++;
+        goto out;
+    }
     if ((pos < g.n_regs && g.regs[pos].host < h + bytes) ||
         (pos > 0 && g.regs[pos - 1].host + g.regs[pos - 1].bytes > h)) {
         st = fail(SLLM_GFX950_ERR_ARG, "register: tensor overlaps a registered one");
@@ -1177,7 +1209,7 @@ int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n) {
         goto out;
     }
     memmove(&g.regs[pos + 1], &g.regs[pos], (g.n_regs - pos) * sizeof *g.regs);
-    g.regs[pos] = (reg_tensor) { h, bytes, dev };
+    g.regs[pos] = (reg_tensor) { h, bytes, dev, 1 };
     g.n_regs++;
 out:
     pthread_mutex_unlock(&g_mtx);
@@ -1191,7 +1223,7 @@ int sllm_gfx950_tensor_unregister(const void *packed) {
     int st = SLLM_GFX950_OK;
     if (i < 0 || g.regs[i].host != (const uint8_t *) packed) {
         st = fail(SLLM_GFX950_ERR_NOT_REGISTERED, "unregister: %p is not a registered tensor", packed);
-    } else {
+    } else if (--g.regs[i].refs == 0) {
         hipStreamSynchronize(g.stream);
         hipFree(g.regs[i].dev);
         memmove(&g.regs[i], &g.regs[i + 1], (g.n_regs - (size_t) i - 1) * sizeof *g.regs);
@@ -1210,18 +1242,50 @@ const void *sllm_gfx950_tensor_device(const void *host) {
     return d;
 }
 
-static int scratch_reserve(size_t bytes) {
-    if (bytes <= g.scratch_bytes) return SLLM_GFX950_OK;
+static size_t align16(size_t v) { return (v + 15u) & ~(size_t) 15u; }
+
+/* pin_q layout: the done word (a line of its own), act, then q */
+#define PIN_Q_DONE 0u
+#define PIN_Q_ACT  64u
+#define PIN_Q_Q    128u
+
+static int pinned_reserve(uint8_t **host, uint8_t **dev, size_t *cap, size_t bytes) {
+    if (bytes <= *cap) return SLLM_GFX950_OK;
     HIP_TRY(hipStreamSynchronize(g.stream));
-    if (g.scratch) HIP_TRY(hipFree(g.scratch));
-    g.scratch = NULL;
-    g.scratch_bytes = 0;
-    HIP_TRY(hipMalloc(&g.scratch, bytes));
-    g.scratch_bytes = bytes;
+    if (*host) HIP_TRY(hipHostFree(*host));
+    *host = *dev = NULL;
+    *cap = 0;
+    bytes = (bytes + 4095u) & ~(size_t) 4095u;
+    HIP_TRY(hipHostMalloc((void **) host, bytes, hipHostMallocDefault));
+    HIP_TRY(hipHostGetDevicePointer((void **) dev, *host, 0));
+    *cap = bytes;
     return SLLM_GFX950_OK;
 }
 
-static size_t align16(size_t v) { return (v + 15u) & ~(size_t) 15u; }
+/* Room for a quantised vector of n and for max(4n, io) bytes of x / rows. */
+static int hostrow_reserve(size_t n, size_t io) {
+    if (PIN_Q_Q + n > g.pin_q_cap) {
+        g.last_q = NULL;                    /* the kept copy goes with the old buffer */
+        int st = pinned_reserve(&g.pin_q, &g.pin_q_dev, &g.pin_q_cap, PIN_Q_Q + n);
+        if (st != SLLM_GFX950_OK) return st;
+        /* the next wait is for seq + 1: the fresh word must not read as it */
+        __atomic_store_n((uint32_t *) (g.pin_q + PIN_Q_DONE), g.seq, __ATOMIC_RELEASE);
+    }
+    if (io > g.pin_io_cap) {
+        int st = pinned_reserve(&g.pin_io, &g.pin_io_dev, &g.pin_io_cap, io);
+        if (st != SLLM_GFX950_OK) return st;
+    }
+    if (align16(n) + 16 > g.dq_cap) {             /* q, then act at align16(n) */
+        g.last_q = NULL;
+        HIP_TRY(hipStreamSynchronize(g.stream));
+        if (g.dq) HIP_TRY(hipFree(g.dq));
+        g.dq = NULL;
+        g.dq_cap = 0;
+        HIP_TRY(hipMalloc((void **) &g.dq, align16(n) + 16));
+        g.dq_cap = align16(n) + 16;
+    }
+    return SLLM_GFX950_OK;
+}
 
 /* The reference's hot-path functions cannot return a status; failing
  * silently (zeros) would read as a wrong answer, and falling back to a CPU
@@ -1231,24 +1295,75 @@ static void die(const char *fn, int st) {
     abort();
 }
 
+static uint64_t now_ns(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (uint64_t) ts.tv_sec * 1000000000u + (uint64_t) ts.tv_nsec;
+}
+
+/* Wait until the device has stored `seq` to the pinned done word: a spin on
+ * host memory sees it about 5 us sooner than a stream synchronisation. After
+ * 20 ms the wait becomes hipStreamSynchronize, which also reports a failed
+ * launch. */
+static int host_wait(uint32_t seq, const char *what) {
+    const volatile uint32_t *done = (const volatile uint32_t *) (g.pin_q + PIN_Q_DONE);
+    const uint64_t t0 = now_ns();
+    for (unsigned spins = 0; __atomic_load_n(done, __ATOMIC_ACQUIRE) != seq; ++spins) {
+        if ((spins & 255u) == 255u && now_ns() - t0 > 20000000u) {
+            hipError_t e = hipStreamSynchronize(g.stream);
+            if (e != hipSuccess) return hip_fail(e, what);
+            if (__atomic_load_n(done, __ATOMIC_ACQUIRE) != seq) {
+                return fail(SLLM_GFX950_ERR_HIP, "%s: the stream drained without the completion word", what);
+            }
+            break;
+        }
+        __builtin_ia32_pause();
+    }
+    return SLLM_GFX950_OK;
+}
+
+/*
+ * The host-pointer row. A call of the reference's hot path hands over host
+ * buffers and expects the result in host buffers on return, so each call is
+ * one launch and one wait -- on a pinned word the device sets last, which
+ * the host sees sooner than a stream synchronisation. The data moves through
+ * pinned host memory that the kernels read and write themselves (no
+ * copy-engine transfers):
+ *   quant_act: x is copied into pinned memory; one workgroup
+ *              (sllm_k_quant_host) reads it and writes q / act to the device
+ *              (for the GEMVs that follow) and to pinned memory (for the
+ *              caller);
+ *   gemv:      the device copy of q is reused when q is the buffer the last
+ *              quant_act filled and still holds those bytes (the reference
+ *              quantises once and runs two or three GEMVs on the result);
+ *              otherwise q goes up first. The GEMV writes its int32 rows
+ *              straight into pinned memory; sllm_k_host_done follows it.
+ */
 void sllm_gfx950_i2s_quant_act(const float *x, size_t n, int8_t *q_out, sllm_gfx950_act *out) {
     if (!g.open) die("sllm_gfx950_i2s_quant_act", fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open"));
     if (x == NULL || q_out == NULL || out == NULL || n == 0) return;
+    if (n > UINT32_MAX / 4) die("sllm_gfx950_i2s_quant_act", fail(SLLM_GFX950_ERR_ARG, "quant_act: n=%zu", n));
     pthread_mutex_lock(&g_mtx);
-    const size_t off_q = align16(n * sizeof(float));
-    const size_t off_a = off_q + align16(n);
-    int st = scratch_reserve(off_a + 16);
-    uint8_t *s = g.scratch;
+    int st = hostrow_reserve(n, n * sizeof(float));
     if (st == SLLM_GFX950_OK) {
-        hipError_t e = hipMemcpyAsync(s, x, n * sizeof(float), hipMemcpyHostToDevice, g.stream);
-        if (e != hipSuccess) st = hip_fail(e, "quant_act upload");
+        memcpy(g.pin_io, x, n * sizeof(float));
+        const float *xd = (const float *) g.pin_io_dev;
+        uint32_t n32 = (uint32_t) n;
+        int8_t *qd = g.dq, *qh = (int8_t *) (g.pin_q_dev + PIN_Q_Q);
+        sllm_gfx950_act *ad = (sllm_gfx950_act *) (g.dq + align16(n));
+        sllm_gfx950_act *ah = (sllm_gfx950_act *) (g.pin_q_dev + PIN_Q_ACT);
+        uint32_t *done = (uint32_t *) (g.pin_q_dev + PIN_Q_DONE);
+        uint32_t seq = ++g.seq;
+        void *args[] = { (void *) &xd, &n32, &qd, &ad, &qh, &ah, &done, &seq };
+        g.last_q = NULL;
+        st = launch(g.k_quant_host, 1, QUANT_HOST_THREADS, 0, args);
+        if (st == SLLM_GFX950_OK) st = host_wait(seq, "quant_act");
     }
-    if (st == SLLM_GFX950_OK) st = sllm_gfx950_quant_act((const float *) s, n, 1, (int8_t *) (s + off_q), (sllm_gfx950_act *) (s + off_a));
     if (st == SLLM_GFX950_OK) {
-        hipError_t e = hipMemcpyAsync(q_out, s + off_q, n, hipMemcpyDeviceToHost, g.stream);
-        if (e == hipSuccess) e = hipMemcpyAsync(out, s + off_a, sizeof *out, hipMemcpyDeviceToHost, g.stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
-        if (e != hipSuccess) st = hip_fail(e, "quant_act download");
+        memcpy(q_out, g.pin_q + PIN_Q_Q, n);
+        memcpy(out, g.pin_q + PIN_Q_ACT, sizeof *out);
+        g.last_q = q_out;
+        g.last_n = n;
     }
     pthread_mutex_unlock(&g_mtx);
     if (st != SLLM_GFX950_OK) die("sllm_gfx950_i2s_quant_act", st);
@@ -1270,21 +1385,29 @@ void sllm_gfx950_i2s_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_
     if (i < 0 || w + need > g.regs[i].host + g.regs[i].bytes) {
         st = fail(SLLM_GFX950_ERR_NOT_REGISTERED, "weights %p (+%zu bytes) are not inside a registered tensor", (const void *) w, need);
     }
-    const size_t off_o = align16(n);
-    if (st == SLLM_GFX950_OK) st = scratch_reserve(off_o + n_rows * sizeof(int32_t));
-    uint8_t *s = g.scratch;
-    if (st == SLLM_GFX950_OK) {
-        hipError_t e = hipMemcpyAsync(s, q, n, hipMemcpyHostToDevice, g.stream);
-        if (e != hipSuccess) st = hip_fail(e, "gemv upload");
+    if (st == SLLM_GFX950_OK) st = hostrow_reserve(n, n_rows * sizeof(int32_t));
+    if (st == SLLM_GFX950_OK && !(q == g.last_q && n == g.last_n && memcmp(q, g.pin_q + PIN_Q_Q, n) == 0)) {
+        memcpy(g.pin_q + PIN_Q_Q, q, n);
+        hipError_t e = hipMemcpyAsync(g.dq, g.pin_q + PIN_Q_Q, n, hipMemcpyHostToDevice, g.stream);
+        if (e != hipSuccess) {
+            g.last_q = NULL;
+            st = hip_fail(e, "gemv upload");
+        } else {
+            g.last_q = q;
+            g.last_n = n;
+        }
     }
     if (st == SLLM_GFX950_OK) {
         const uint8_t *wd = g.regs[i].dev + (w - g.regs[i].host);
-        st = sllm_gfx950_gemv(wd, n_rows, n, (const int8_t *) s, (int32_t *) (s + off_o));
+        st = sllm_gfx950_gemv(wd, n_rows, n, g.dq, (int32_t *) g.pin_io_dev);
     }
     if (st == SLLM_GFX950_OK) {
-        hipError_t e = hipMemcpyAsync(rows_out, s + off_o, n_rows * sizeof(int32_t), hipMemcpyDeviceToHost, g.stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
-        if (e != hipSuccess) st = hip_fail(e, "gemv download");
+        uint32_t *done = (uint32_t *) (g.pin_q_dev + PIN_Q_DONE);
+        uint32_t seq = ++g.seq;
+        void *args[] = { &done, &seq };
+        st = launch(g.k_host_done, 1, 64, 0, args);
+        if (st == SLLM_GFX950_OK) st = host_wait(seq, "gemv");
+        if (st == SLLM_GFX950_OK) memcpy(rows_out, g.pin_io, n_rows * sizeof(int32_t));
     }
     pthread_mutex_unlock(&g_mtx);
     if (st != SLLM_GFX950_OK) die("sllm_gfx950_i2s_gemv", st);

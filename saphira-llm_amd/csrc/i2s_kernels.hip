@@ -810,6 +810,100 @@ sllm_k_quant_list(const quant_job *__restrict__ jobs) {
     quant_row(j.x, j.n, j.q, j.act, red_f, red_i);
 }
 
+// The host-pointer row's quantiser (one workgroup): x lives in pinned host
+// memory, so every load of it crosses PCIe. The first QH_REG * 4 *
+// QH_THREADS values are loaded at once into registers and read once (the
+// rest, if any, twice); q and act are written to device memory, for the
+// GEMVs that follow, and to pinned host memory, for the caller; then `seq`
+// is stored to the pinned word `done` with system-scope release, for the
+// host to wait on. quant_row's arithmetic (max of |x| dropping NaN, s = 127 /
+// amax, quant_one, integer sum), so the same bits.
+constexpr int QH_THREADS = 1024, QH_REG = 4;
+
+extern "C" __global__ void __launch_bounds__(QH_THREADS)
+sllm_k_quant_host(const float *__restrict__ x, uint32_t n, int8_t *__restrict__ q_dev,
+                  act_t *__restrict__ act_dev, int8_t *__restrict__ q_host, act_t *__restrict__ act_host,
+                  uint32_t *done, uint32_t seq) {
+    __shared__ float red_f[QH_THREADS / 64];
+    __shared__ int red_i[QH_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool vec = (n & 3u) == 0;
+    constexpr uint32_t STEP = 4u * QH_THREADS;
+    f32x4 v[QH_REG];
+    float m = 0.0f;
+    if (vec) {
+#pragma unroll
+        for (int r = 0; r < QH_REG; ++r) {
+            const uint32_t i = 4u * tid + (uint32_t) r * STEP;
+            v[r] = i < n ? *G_CAST(const f32x4, x + i) : f32x4 { 0.0f, 0.0f, 0.0f, 0.0f };
+        }
+#pragma unroll
+        for (int r = 0; r < QH_REG; ++r)
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[r][0]), fabsf(v[r][1])), fmaxf(fabsf(v[r][2]), fabsf(v[r][3]))));
+        for (uint32_t i = 4u * tid + QH_REG * STEP; i < n; i += STEP) {
+            const f32x4 t = *G_CAST(const f32x4, x + i);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(t[0]), fabsf(t[1])), fmaxf(fabsf(t[2]), fabsf(t[3]))));
+        }
+    } else {
+        for (uint32_t i = tid; i < n; i += QH_THREADS) m = fmaxf(m, fabsf(G_CAST(const float, x)[i]));
+    }
+    m = wave_max(m);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    m = red_f[0];
+#pragma unroll
+    for (int w = 1; w < QH_THREADS / 64; ++w) m = fmaxf(m, red_f[w]);
+    const float s = m > 0.0f ? 127.0f / m : 0.0f;
+
+    int sum = 0;
+    auto put4 = [&](uint32_t i, const f32x4 t) {
+        const int a = quant_one(t[0] * s), b = quant_one(t[1] * s);
+        const int c = quant_one(t[2] * s), d = quant_one(t[3] * s);
+        sum += a + b + c + d;
+        const uint32_t packed = (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) |
+                                ((uint32_t) (c & 0xff) << 16) | ((uint32_t) (d & 0xff) << 24);
+        *G_CAST(uint32_t, q_dev + i) = packed;
+        *G_CAST(uint32_t, q_host + i) = packed;
+    };
+    if (vec) {
+#pragma unroll
+        for (int r = 0; r < QH_REG; ++r) {
+            const uint32_t i = 4u * tid + (uint32_t) r * STEP;
+            if (i < n) put4(i, v[r]);
+        }
+        for (uint32_t i = 4u * tid + QH_REG * STEP; i < n; i += STEP) put4(i, *G_CAST(const f32x4, x + i));
+    } else {
+        for (uint32_t i = tid; i < n; i += QH_THREADS) {
+            const int a = quant_one(G_CAST(const float, x)[i] * s);
+            sum += a;
+            G_CAST(int8_t, q_dev)[i] = (int8_t) a;
+            G_CAST(int8_t, q_host)[i] = (int8_t) a;
+        }
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red_i[wave] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < QH_THREADS / 64; ++w) t += red_i[w];
+        G_CAST(float, act_dev)[0] = s;
+        G_CAST(int32_t, act_dev)[1] = t;
+        G_CAST(float, act_host)[0] = s;
+        G_CAST(int32_t, act_host)[1] = t;
+        // every wave's q stores precede the barrier above
+        __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+// Completion word for the host-pointer row: launched behind a kernel on the
+// same stream, so it runs once that kernel has finished and released its
+// writes; the host waits on `done` instead of a stream synchronisation.
+extern "C" __global__ void __launch_bounds__(64)
+sllm_k_host_done(uint32_t *done, uint32_t seq) {
+    if (threadIdx.x == 0) __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Slab GEMV: blocks of SLAB_THREADS, static LDS. With descs null this is a
 // single-job launch: slab blockIdx.x of gridDim.x slabs of `single`.
 extern "C" __global__ void __launch_bounds__(SLAB_THREADS)

@@ -349,6 +349,27 @@ def test_host_pointer_row_matches_oracle(amd, orc, dev):
         d = lib.sllm_gfx950_i2s_dot(ctypes.c_void_p(w.ctypes.data + 7 * (n // 4)), amd.ptr(q), n)
         assert d == want[7]
         assert lib.sllm_gfx950_i2s_dot(None, amd.ptr(q), n) == 0
+        # the row keeps a device copy of the vector quant_act returned: a
+        # different buffer, and the same buffer rewritten by the host, are
+        # read afresh
+        q2 = np.random.default_rng(9).integers(-127, 128, n).astype(np.int8)
+        want2 = orc.gemv(w, n_rows, n, q2, orc.DOT_V3)
+        lib.sllm_gfx950_i2s_gemv(amd.ptr(w), n_rows, n, amd.ptr(q2), amd.ptr(out))
+        np.testing.assert_array_equal(out, want2)
+        lib.sllm_gfx950_i2s_quant_act(amd.ptr(x), n, amd.ptr(q), ctypes.byref(a))
+        q[:] = q2
+        lib.sllm_gfx950_i2s_gemv(amd.ptr(w), n_rows, n, amd.ptr(q), amd.ptr(out))
+        np.testing.assert_array_equal(out, want2)
+        lib.sllm_gfx950_i2s_quant_act(amd.ptr(x), n, amd.ptr(q), ctypes.byref(a))
+        np.testing.assert_array_equal(q, q_o)
+        # a shorter row (K 1024) through the same staging
+        xs = amd.synth_normal(6, 1024)
+        qs = np.empty(1024, np.int8)
+        lib.sllm_gfx950_i2s_quant_act(amd.ptr(xs), 1024, amd.ptr(qs), ctypes.byref(a))
+        qs_o, ss_o, ts_o = orc.quant_act(xs)
+        np.testing.assert_array_equal(qs, qs_o)
+        assert np.float32(a.scale) == ss_o and a.sum == ts_o
+        lib.sllm_gfx950_i2s_quant_act(amd.ptr(x), n, amd.ptr(q), ctypes.byref(a))
         assert lib.sllm_gfx950_tensor_device(amd.ptr(w))
         assert not lib.sllm_gfx950_tensor_device(amd.ptr(q))
         # the dispatch table with the gfx950 row installed
