@@ -19,6 +19,12 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* every entry point that reaches the device: -60 while the library is closed */
+#define DEC_NEED_OPEN()                                                                  \
+    do {                                                                                 \
+        if (!sllm_shim_is_open()) return sllm_shim_fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open"); \
+    } while (0)
+
 /* ------------------------------------------------------------------ */
 /* device-side layouts                                                 */
 /* ------------------------------------------------------------------ */
@@ -199,6 +205,7 @@ static int check_desc(const sllm_gfx950_model_desc *d) {
 }
 
 int sllm_gfx950_model_upload(const sllm_gfx950_model_desc *d, sllm_gfx950_model **out) {
+    DEC_NEED_OPEN();
     if (!sllm_shim_is_open()) return sllm_shim_fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open");
     if (d == NULL || out == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "model_upload: NULL argument");
     *out = NULL;
@@ -419,6 +426,7 @@ static int drop_graph(sllm_gfx950_ctx *c) {
 }
 
 int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_ctx **out) {
+    DEC_NEED_OPEN();
     if (!sllm_shim_is_open()) return sllm_shim_fail(SLLM_GFX950_ERR_NO_DEVICE, "library not open");
     if (m == NULL || out == NULL || n_ctx < 1) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_new: bad arguments");
     *out = NULL;
@@ -537,6 +545,7 @@ int32_t sllm_gfx950_ctx_n_past(const sllm_gfx950_ctx *c) { return c ? c->n_past 
 const float *sllm_gfx950_ctx_logits(const sllm_gfx950_ctx *c) { return c ? c->logits : NULL; }
 
 int sllm_gfx950_ctx_reset(sllm_gfx950_ctx *c) {
+    DEC_NEED_OPEN();
     if (c == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_reset: NULL");
     const hipStream_t s = sllm_shim_stream();
     hipError_t he = hipSuccess;
@@ -619,6 +628,7 @@ static int enqueue_token(sllm_gfx950_ctx *c) {
 }
 
 int sllm_gfx950_ctx_set_graph(sllm_gfx950_ctx *c, int on) {
+    DEC_NEED_OPEN();
     if (c == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_set_graph: NULL");
     c->graph_on = on != 0;
     if (!c->graph_on) {
@@ -637,6 +647,7 @@ static int set_step(sllm_gfx950_ctx *c, const k_dec_step *hs) {
 
 int sllm_gfx950_forward(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, int32_t token, int32_t pos,
                         float *logits) {
+    DEC_NEED_OPEN();
     if (m == NULL || c == NULL || c->m != m) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward: model / context");
     if (pos < c->n_past || pos >= c->n_ctx) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward: pos %d outside [n_past %d, n_ctx %d)", pos, c->n_past, c->n_ctx);
@@ -661,6 +672,7 @@ int sllm_gfx950_forward(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, int32_t 
 }
 
 int sllm_gfx950_ctx_argmax(sllm_gfx950_ctx *c, int32_t *token) {
+    DEC_NEED_OPEN();
     if (c == NULL || token == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_argmax: NULL");
     k_dec_step hs;
     hipError_t he = hipMemcpyAsync(&hs, c->step, sizeof hs, hipMemcpyDeviceToHost, sllm_shim_stream());
@@ -672,6 +684,7 @@ int sllm_gfx950_ctx_argmax(sllm_gfx950_ctx *c, int32_t *token) {
 
 int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *prompt,
                                 int32_t n_prompt, int32_t n_new, int32_t *out) {
+    DEC_NEED_OPEN();
     if (m == NULL || c == NULL || c->m != m || out == NULL || n_prompt < 0 || n_new < 0 ||
         (n_prompt > 0 && prompt == NULL)) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "generate_greedy: bad arguments");
@@ -760,6 +773,7 @@ int sllm_gfx950_generate_greedy(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, 
 
 int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, int32_t n_pos,
                             const float *logits) {
+    DEC_NEED_OPEN();
     if (c == NULL || k == NULL || v == NULL || n_pos < 0 || n_pos > c->n_ctx) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_kv_load: bad arguments");
     }
@@ -832,6 +846,7 @@ int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, 
 }
 
 int sllm_gfx950_ctx_set_inflight(sllm_gfx950_ctx *c, int32_t tokens) {
+    DEC_NEED_OPEN();
     if (c == NULL || tokens < 1 || tokens > SLLM_GFX950_DEC_MAX_INFLIGHT) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_set_inflight: tokens must be 1..%d",
                               SLLM_GFX950_DEC_MAX_INFLIGHT);
@@ -841,6 +856,7 @@ int sllm_gfx950_ctx_set_inflight(sllm_gfx950_ctx *c, int32_t tokens) {
 }
 
 int sllm_gfx950_ctx_trace(sllm_gfx950_ctx *c, int32_t *dots, sllm_gfx950_act *acts) {
+    DEC_NEED_OPEN();
     if (c == NULL || (dots == NULL) != (acts == NULL)) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "ctx_trace: give both buffers or neither");
     }
@@ -1002,6 +1018,7 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
 
 int sllm_gfx950_forward_chunk(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *tokens, int32_t n,
                               int32_t base, float *logits) {
+    DEC_NEED_OPEN();
     if (m == NULL || c == NULL || c->m != m || tokens == NULL) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_chunk: model / context / tokens");
     }
@@ -1042,6 +1059,7 @@ int sllm_gfx950_forward_chunk(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, co
 
 int sllm_gfx950_forward_prefill_chunked(const sllm_gfx950_model *m, sllm_gfx950_ctx *c, const int32_t *tokens,
                                         int32_t n, int32_t chunk, float *logits) {
+    DEC_NEED_OPEN();
     if (m == NULL || c == NULL || c->m != m || (tokens == NULL && n > 0) || n < 0) {
         return sllm_shim_fail(SLLM_GFX950_ERR_ARG, "forward_prefill_chunked: bad arguments");
     }

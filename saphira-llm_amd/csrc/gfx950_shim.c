@@ -174,8 +174,11 @@ static int fail(int status, const char *fmt, ...) {
     return status;
 }
 
+/* A failed HIP call: out of device or pinned memory is the reference's
+ * SLLM_ERR_NOMEM, anything else SLLM_GFX950_ERR_HIP. */
 static int hip_fail(hipError_t e, const char *what) {
-    return fail(SLLM_GFX950_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int) e);
+    const int status = e == hipErrorOutOfMemory ? SLLM_GFX950_ERR_NOMEM : SLLM_GFX950_ERR_HIP;
+    return fail(status, "%s: %s (%d)", what, hipGetErrorString(e), (int) e);
 }
 
 #define HIP_TRY(call)                                                      \
@@ -248,17 +251,20 @@ int sllm_gfx950_open(int device) {
         pthread_mutex_unlock(&g_mtx);
         return st;
     }
+    /* what has been created, for the unwind on failure */
+    int have_mod = 0, have_dec = 0, have_stream = 0, have_ev0 = 0, have_ev1 = 0;
     int count = 0;
+    hipDeviceProp_t prop;
     hipError_t e = hipGetDeviceCount(&count);
-    if (e != hipSuccess || count <= 0) {
-        st = fail(SLLM_GFX950_ERR_NO_DEVICE, "no HIP device (%s)", hipGetErrorString(e));
+    if (e == hipErrorNoDevice || (e == hipSuccess && count <= 0)) {
+        st = fail(SLLM_GFX950_ERR_NO_DEVICE, "no HIP device");
         goto out;
     }
+    if (e != hipSuccess) { st = hip_fail(e, "hipGetDeviceCount"); goto out; }
     if (device < 0 || device >= count) {
         st = fail(SLLM_GFX950_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, count);
         goto out;
     }
-    hipDeviceProp_t prop;
     if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) {
         st = hip_fail(e, "hipGetDeviceProperties");
         goto out;
@@ -270,53 +276,36 @@ int sllm_gfx950_open(int device) {
     if ((e = hipSetDevice(device)) != hipSuccess) { st = hip_fail(e, "hipSetDevice"); goto out; }
     if ((e = hipModuleLoadData(&g.mod, sllm_gfx950_code_object)) != hipSuccess) {
         st = hip_fail(e, "hipModuleLoadData");
-        goto out;
+        goto unwind;
     }
-    if ((st = load_functions()) != SLLM_GFX950_OK) {
-        hipModuleUnload(g.mod);
-        goto out;
-    }
+    have_mod = 1;
+    if ((st = load_functions()) != SLLM_GFX950_OK) goto unwind;
     if ((e = hipModuleLoadData(&g.dec_mod, sllm_gfx950_decode_object)) != hipSuccess) {
-        hipModuleUnload(g.mod);
         st = hip_fail(e, "hipModuleLoadData(decode)");
-        goto out;
+        goto unwind;
     }
+    have_dec = 1;
     if ((e = hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking)) != hipSuccess) {
-        hipModuleUnload(g.dec_mod);
-        hipModuleUnload(g.mod);
         st = hip_fail(e, "hipStreamCreateWithFlags");
-        goto out;
+        goto unwind;
     }
-    if ((e = hipEventCreate(&g.ev_start)) != hipSuccess ||
-        (e = hipEventCreate(&g.ev_stop)) != hipSuccess) {
-        hipStreamDestroy(g.stream);
-        hipModuleUnload(g.dec_mod);
-        hipModuleUnload(g.mod);
-        st = hip_fail(e, "hipEventCreate");
-        goto out;
-    }
+    have_stream = 1;
+    if ((e = hipEventCreate(&g.ev_start)) != hipSuccess) { st = hip_fail(e, "hipEventCreate"); goto unwind; }
+    have_ev0 = 1;
+    if ((e = hipEventCreate(&g.ev_stop)) != hipSuccess) { st = hip_fail(e, "hipEventCreate"); goto unwind; }
+    have_ev1 = 1;
     if ((e = hipMalloc(&g.lin_scratch, SLLM_GFX950_MAX_K + 256)) != hipSuccess) {
-        hipEventDestroy(g.ev_start);
-        hipEventDestroy(g.ev_stop);
-        hipStreamDestroy(g.stream);
-        hipModuleUnload(g.dec_mod);
-        hipModuleUnload(g.mod);
+        g.lin_scratch = NULL;
         st = hip_fail(e, "hipMalloc(row scratch)");
-        goto out;
+        goto unwind;
     }
     /* the no-allocation batch's device array, resolved once for this device
      * with the device current */
     {
         const int rc = sllm_noalloc_resolve(device, &g.noalloc_dev);
         if (rc != 0) {
-            hipFree(g.lin_scratch);
-            hipEventDestroy(g.ev_start);
-            hipEventDestroy(g.ev_stop);
-            hipStreamDestroy(g.stream);
-            hipModuleUnload(g.dec_mod);
-            hipModuleUnload(g.mod);
             st = hip_fail((hipError_t) rc, "hipGetSymbolAddress(no-allocation scratch)");
-            goto out;
+            goto unwind;
         }
     }
     g.device = device;
@@ -324,6 +313,15 @@ int sllm_gfx950_open(int device) {
     g.hbm = prop.totalGlobalMem;
     snprintf(g.name, sizeof g.name, "%s (%s)", prop.name, prop.gcnArchName);
     g.open = 1;
+    goto out;
+unwind:
+    if (g.lin_scratch) hipFree(g.lin_scratch);
+    if (have_ev1) hipEventDestroy(g.ev_stop);
+    if (have_ev0) hipEventDestroy(g.ev_start);
+    if (have_stream) hipStreamDestroy(g.stream);
+    if (have_dec) hipModuleUnload(g.dec_mod);
+    if (have_mod) hipModuleUnload(g.mod);
+    memset(&g, 0, sizeof g);
 out:
     pthread_mutex_unlock(&g_mtx);
     return st;
@@ -434,10 +432,15 @@ int sllm_gfx950_events_reserve(int n) {
     hipEvent_t *ev = realloc(g.events, (size_t) n * sizeof *ev);
     if (ev == NULL) return fail(SLLM_GFX950_ERR_NOMEM, "events");
     g.events = ev;
-    while (g.n_events < n) {
-        HIP_TRY(hipEventCreate(&g.events[g.n_events]));
-        g.n_events++;
+    /* all or nothing: a failure destroys what this call created */
+    for (int i = g.n_events; i < n; ++i) {
+        const hipError_t e = hipEventCreate(&g.events[i]);
+        if (e != hipSuccess) {
+            while (i-- > g.n_events) hipEventDestroy(g.events[i]);
+            return hip_fail(e, "hipEventCreate(events)");
+        }
     }
+    g.n_events = n;
     return SLLM_GFX950_OK;
 }
 
@@ -906,14 +909,19 @@ int sllm_gfx950_plan_run_marked(const sllm_gfx950_plan *p, int event) {
     return plan_launch(p, event);
 }
 
-void sllm_gfx950_plan_destroy(sllm_gfx950_plan *p) {
-    if (p == NULL) return;
+/* Free a plan whose launches have all finished. */
+static void plan_free(sllm_gfx950_plan *p) {
     if (g.open) {
-        hipStreamSynchronize(g.stream);
         hipFree(p->tables_dev);
         if (p->scratch_dev) hipFree(p->scratch_dev);
     }
     free(p);
+}
+
+void sllm_gfx950_plan_destroy(sllm_gfx950_plan *p) {
+    if (p == NULL) return;
+    if (g.open) hipStreamSynchronize(g.stream);
+    plan_free(p);
 }
 
 /* A batch is a plan used once; its tables are freed after the stream drains. */
@@ -924,7 +932,13 @@ int sllm_gfx950_gemv_batch(const sllm_gfx950_gemv_job *jobs, size_t n_jobs) {
     int st = sllm_gfx950_plan_create(jobs, n_jobs, &p);
     if (st != SLLM_GFX950_OK) return st;
     st = plan_launch(p, -1);
-    sllm_gfx950_plan_destroy(p);      /* synchronises before freeing the tables */
+    if (st == SLLM_GFX950_OK) {
+        /* the tables are freed below: wait for the launch, and report it */
+        const hipError_t e = hipStreamSynchronize(g.stream);
+        if (e != hipSuccess) st = hip_fail(e, "gemv_batch");
+    }
+    if (st == SLLM_GFX950_OK) plan_free(p);
+    else sllm_gfx950_plan_destroy(p);
     return st;
 }
 
@@ -1224,10 +1238,12 @@ int sllm_gfx950_tensor_unregister(const void *packed) {
     if (i < 0 || g.regs[i].host != (const uint8_t *) packed) {
         st = fail(SLLM_GFX950_ERR_NOT_REGISTERED, "unregister: %p is not a registered tensor", packed);
     } else if (--g.regs[i].refs == 0) {
-        hipStreamSynchronize(g.stream);
+        /* the copy goes either way; a failed wait is still reported */
+        const hipError_t e = hipStreamSynchronize(g.stream);
         hipFree(g.regs[i].dev);
         memmove(&g.regs[i], &g.regs[i + 1], (g.n_regs - (size_t) i - 1) * sizeof *g.regs);
         g.n_regs--;
+        if (e != hipSuccess) st = hip_fail(e, "unregister");
     }
     pthread_mutex_unlock(&g_mtx);
     return st;
