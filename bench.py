@@ -504,6 +504,88 @@ def measure_gemm(amd, dev):
     return checks, rows
 
 
+def measure_gemm_plan(amd, dev, wl, token_counts=(4, 16, 64)):
+    """The multi-tensor form: the FFN workload's 96 tensors (32 rotated sets
+    of gate / up / down, 424.7 MB) against m tokens each, as one GEMM plan
+    launch -- every tensor with its own quantised rows (gate and up share
+    theirs) -- beside the GEMV plan doing the same work (one job per tensor
+    and token, each quantising its token in-kernel). Bytes: packed weights,
+    int8 rows and f32 outputs. The plan's outputs of sets 0 and 31 are
+    checked bit for bit against sllm_gfx950_gemm tensor by tensor."""
+    rows = []
+    for m in token_counts:
+        xs_up = [np.concatenate([amd.synth_normal(amd.synth_seed(7, s, t, 100), K_UP) for t in range(m)])
+                 for s in range(wl.sets)]
+        xs_dn = [np.concatenate([amd.synth_normal(amd.synth_seed(7, s, t, 101), N_FF) for t in range(m)])
+                 for s in range(wl.sets)]
+        bxu, bxd = dev.put(np.concatenate(xs_up)), dev.put(np.concatenate(xs_dn))
+        bqu, bqd = dev.alloc(wl.sets * m * K_UP), dev.alloc(wl.sets * m * N_FF)
+        bau, bad = dev.alloc(wl.sets * m * 8), dev.alloc(wl.sets * m * 8)
+        dev.quant_act(bxu.vp, K_UP, wl.sets * m, bqu.vp, bau.vp)
+        dev.quant_act(bxd.vp, N_FF, wl.sets * m, bqd.vp, bad.vp)
+        outs = [dev.alloc(4 * m * n_rows) for s in range(wl.sets) for _, n_rows, _ in SHAPES]
+        jobs = []
+        for s in range(wl.sets):
+            for t_, (name, n_rows, n) in enumerate(SHAPES):
+                up = n == K_UP
+                q = (bqu if up else bqd).ptr + s * m * n
+                a = (bau if up else bad).ptr + s * m * 8
+                jobs.append((wl.jobs[3 * s + t_].w, n_rows, n, q, a, outs[3 * s + t_].ptr, None))
+        plan = dev.gemm_plan(jobs, m)
+        for _ in range(5):
+            dev.gemm_plan_run(plan)
+        dev.sync()
+        dev.events(2)
+        reps = 20
+        dev.record(0)
+        for _ in range(reps):
+            dev.gemm_plan_run(plan)
+        dev.record(1)
+        plan_us = dev.elapsed(0, 1) * 1e3 / reps
+        # the same tensors one sllm_gfx950_gemm at a time, for the check
+        ref = dev.alloc(4 * m * N_FF)
+        for s in (0, wl.sets - 1):
+            for t_, (name, n_rows, n) in enumerate(SHAPES):
+                j = jobs[3 * s + t_]
+                dev.gemm(j[0], n_rows, n, j[3], j[4], m, ref.vp)
+                dev.sync()
+                got = outs[3 * s + t_].download(np.float32, m * n_rows)
+                want = ref.download(np.float32, m * n_rows)
+                if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+                    raise SystemExit(f"bench: GEMM plan output differs from sllm_gfx950_gemm (set {s} {name}, m={m})")
+        ref.free()
+        dev.gemm_plan_destroy(plan)
+        # the GEMV plan over the same tensors and tokens
+        gjobs = []
+        for s in range(wl.sets):
+            for t_, (name, n_rows, n) in enumerate(SHAPES):
+                bx = bxu if n == K_UP else bxd
+                for t in range(m):
+                    gjobs.append(amd.GemvJob(wl.jobs[3 * s + t_].w, n_rows, n, bx.ptr + 4 * (s * m + t) * n, None, None,
+                                             outs[3 * s + t_].ptr + 4 * t * n_rows, None))
+        gplan = dev.plan(gjobs)
+        dev.plan_run(gplan)
+        dev.sync()
+        greps = 3
+        dev.record(0)
+        for _ in range(greps):
+            dev.plan_run(gplan)
+        dev.record(1)
+        gemv_us = dev.elapsed(0, 1) * 1e3 / greps
+        dev.plan_destroy(gplan)
+        for b in [bxu, bxd, bqu, bqd, bau, bad] + outs:
+            b.free()
+        byts = wl.weight_bytes + wl.sets * m * (K_UP + N_FF) + wl.sets * m * 8 * 2 + \
+            4 * m * sum(n_rows for _, n_rows, _ in SHAPES) * wl.sets
+        ops = 2.0 * m * sum(n_rows * n for _, n_rows, n in SHAPES) * wl.sets
+        rows.append({"tokens": m, "tensors": len(jobs), "plan_us": round(plan_us, 2),
+                     "plan_GBps": round(byts / plan_us / 1e3, 1), "plan_TOPS": round(ops / plan_us / 1e6, 1),
+                     "gemv_plan_us": round(gemv_us, 2), "faster": "mfma" if plan_us < gemv_us else "gemv"})
+        log(f"gemm plan, 96 tensors x {m} tokens: {plan_us:.1f} us ({byts / plan_us / 1e3:.0f} GB/s), "
+            f"GEMV plan {gemv_us:.1f} us")
+    return rows
+
+
 def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
     """Plain device copy and read-only checksum of known size: the achievable
     HBM figure beside the GEMV."""
@@ -890,6 +972,7 @@ def main():
             f"({prefill['tokens_per_s']} tokens/s); with every token's logits {prefill['ms_all_logits_incl_host_copy']} ms")
     if "gemm" in legs:
         gemm_checks, gemm = measure_gemm(amd, dev)
+        gemm = {"per_tensor": gemm, "plan_96_tensors": measure_gemm_plan(amd, dev, wl)}
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,

@@ -260,12 +260,38 @@ int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size
 int sllm_gfx950_linear_batch(const uint8_t *w, size_t n_rows, size_t n, const float *x, size_t m,
                              int8_t *q, sllm_gfx950_act *act, float *out, int32_t *rows_out);
 
+/* A plan of GEMMs over many tensors in one launch (no counterpart in the
+ * reference, whose chunk path runs each tensor of each token on its own):
+ * every job is one sllm_gfx950_gemm -- its own packed tensor, K, m token
+ * rows q / act and outputs -- and all jobs share m. The tables are uploaded
+ * once, at creation; each run is one launch on the library stream. K must
+ * be a multiple of 256 (every BitNet-2B projection); at most 2^31 row tiles.
+ * Outputs are sllm_gfx950_gemm's, bit for bit. */
+typedef struct sllm_gfx950_gemm_plan_job {
+    const uint8_t         *w;
+    size_t                 n_rows;
+    size_t                 n;          /* K */
+    const int8_t          *q;          /* [m][n] int8 */
+    const sllm_gfx950_act *act;        /* [m]; NULL only without out */
+    float                 *out;        /* [m][n_rows] epilogue, or NULL */
+    int32_t               *rows_out;   /* [m][n_rows] raw dots, or NULL (not both) */
+} sllm_gfx950_gemm_plan_job;
+
+typedef struct sllm_gfx950_gemm_plan sllm_gfx950_gemm_plan;
+int  sllm_gfx950_gemm_plan_create(const sllm_gfx950_gemm_plan_job *jobs, size_t n_jobs, size_t m,
+                                  sllm_gfx950_gemm_plan **plan);
+int  sllm_gfx950_gemm_plan_run(const sllm_gfx950_gemm_plan *plan);
+void sllm_gfx950_gemm_plan_destroy(sllm_gfx950_gemm_plan *plan);
+
 /* GEMM tile override for tuning and tests: 0 automatic (by m and the grid),
  * 1: 16 tokens x 16 rows per workgroup (K split over its waves), 2: 32 x 128,
  * 3: 64 x 128, 4: 128 x 128 staged through two LDS buffers, 5: the same
  * through one buffer, 6..9: 16 x 64, 32 x 64, 32 x 128 and 64 x 256 copied
- * straight into a ring of LDS stages (4..9 need K % 256 == 0; tile 3
- * otherwise). */
+ * straight into a ring of LDS stages, 10..13: 64 x 256, 64 x 128, 32 x 256
+ * and 32 x 128 the same way with eight waves in two K groups, 14 and 15:
+ * 16 x 64 and 32 x 64 with sixteen waves in four K groups (4 and up need
+ * K % 256 == 0; tile 3 otherwise). A plan takes the override when it is
+ * one of 6, 7, 10, 11 or 13, else its own choice. */
 int sllm_gfx950_set_gemm_tile(int tile);
 
 /* Launch-geometry override for tuning sweeps and tests; affects launches

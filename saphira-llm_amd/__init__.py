@@ -62,6 +62,12 @@ class GemmJob(ctypes.Structure):
     _fields_ = [("w", c_void_p), ("n_rows", c_size_t), ("out", c_void_p), ("rows_out", c_void_p)]
 
 
+class GemmPlanJob(ctypes.Structure):
+    """sllm_gfx950_gemm_plan_job: one tensor of a GEMM plan."""
+    _fields_ = [("w", c_void_p), ("n_rows", c_size_t), ("n", c_size_t), ("q", c_void_p),
+                ("act", c_void_p), ("out", c_void_p), ("rows_out", c_void_p)]
+
+
 class ModelDesc(ctypes.Structure):
     """sllm_gfx950_model_desc."""
     _fields_ = [("n_layer", c_int32), ("n_embd", c_int32), ("n_ff", c_int32), ("n_head", c_int32),
@@ -122,6 +128,9 @@ PROTOTYPES = {
     "sllm_gfx950_linear_batch": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p, c_void_p,
                                          c_void_p, c_void_p]),
     "sllm_gfx950_set_gemm_tile": (c_int, [c_int]),
+    "sllm_gfx950_gemm_plan_create": (c_int, [POINTER(GemmPlanJob), c_size_t, c_size_t, POINTER(c_void_p)]),
+    "sllm_gfx950_gemm_plan_run": (c_int, [c_void_p]),
+    "sllm_gfx950_gemm_plan_destroy": (None, [c_void_p]),
     "sllm_gfx950_gemm_multi": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t]),
     "sllm_gfx950_model_upload": (c_int, [POINTER(ModelDesc), POINTER(c_void_p)]),
     "sllm_gfx950_model_free": (None, [c_void_p]),
@@ -337,6 +346,19 @@ class Device:
 
     def linear_batch(self, w, n_rows, n, x, m, q, act, out, rows_out=None):
         check(self.lib.sllm_gfx950_linear_batch(w, n_rows, n, x, m, q, act, out, rows_out), "linear_batch")
+
+    def gemm_plan(self, jobs, m):
+        """A GEMM plan over (w, n_rows, k, q, act, out, rows_out) jobs of m tokens."""
+        arr = (GemmPlanJob * len(jobs))(*[GemmPlanJob(*j) for j in jobs])
+        p = ctypes.c_void_p()
+        check(self.lib.sllm_gfx950_gemm_plan_create(arr, len(jobs), m, ctypes.byref(p)), "gemm_plan_create")
+        return p
+
+    def gemm_plan_run(self, p):
+        check(self.lib.sllm_gfx950_gemm_plan_run(p), "gemm_plan_run")
+
+    def gemm_plan_destroy(self, p):
+        self.lib.sllm_gfx950_gemm_plan_destroy(p)
 
     def set_gemm_tile(self, tile=0):
         check(self.lib.sllm_gfx950_set_gemm_tile(tile), "set_gemm_tile")

@@ -472,7 +472,10 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
     hipError_t he = hipSuccess;
     if (st == SLLM_GFX950_OK) {
         he = hipMalloc(&c->dev, total);
-        if (he == hipSuccess) he = hipMemset(c->dev, 0, total);
+        /* cleared on the library stream, which does not order against the
+         * null stream */
+        if (he == hipSuccess) he = hipMemsetAsync(c->dev, 0, total, sllm_shim_stream());
+        if (he == hipSuccess) he = hipStreamSynchronize(sllm_shim_stream());
         if (he != hipSuccess) st = sllm_shim_hip_fail(he, "ctx_new: device memory");
     }
     if (st == SLLM_GFX950_OK) {

@@ -121,7 +121,8 @@ static struct {
     hipFunction_t  k_slab;
     hipFunction_t  k_stream[N_LPR];
     hipFunction_t  k_copy;
-    hipFunction_t  k_gemm[9];
+    hipFunction_t  k_gemm[15];
+    hipFunction_t  k_gemm_t[5];
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -236,6 +237,17 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[6], g.mod, "sllm_k_gemm_dl2x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[7], g.mod, "sllm_k_gemm_dl2x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[8], g.mod, "sllm_k_gemm_dl4x4"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[9], g.mod, "sllm_k_gemm_dk4x4"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[10], g.mod, "sllm_k_gemm_dk4x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[11], g.mod, "sllm_k_gemm_dk2x4"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[12], g.mod, "sllm_k_gemm_dk2x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[13], g.mod, "sllm_k_gemm_dq1x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm[14], g.mod, "sllm_k_gemm_dq2x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[0], g.mod, "sllm_k_gemm_tdl1x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[1], g.mod, "sllm_k_gemm_tdl2x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[2], g.mod, "sllm_k_gemm_tdk2x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[3], g.mod, "sllm_k_gemm_tdk4x2"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[4], g.mod, "sllm_k_gemm_tdk4x4"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
@@ -1071,10 +1083,13 @@ _Static_assert(sizeof(k_gemm_args) == 128, "k_gemm_args must match gemm_args in 
  * tile through LDS -- 3 with two buffers, one workgroup per CU; 4 with one,
  * two per CU; shapes 5..8 copy it straight into an LDS ring). Shapes 3 and
  * up need K % 256 == 0. */
-#define N_GEMM_TILES 9
+#define N_GEMM_TILES 15
 #define GEMM_DL_FIRST 5
-static const uint32_t k_gemm_tokens[N_GEMM_TILES] = { 16, 32, 64, 128, 128, 16, 32, 32, 64 };
-static const uint32_t k_gemm_rows[N_GEMM_TILES] = { 16, 128, 128, 128, 128, 64, 64, 128, 256 };
+static const uint32_t k_gemm_tokens[N_GEMM_TILES] = { 16, 32, 64, 128, 128, 16, 32, 32, 64, 64, 64, 32, 32, 16, 32 };
+static const uint32_t k_gemm_rows[N_GEMM_TILES] = { 16, 128, 128, 128, 128, 64, 64, 128, 256, 256, 128, 256, 128, 64, 64 };
+/* threads per workgroup: shapes 9..12 are two K groups of four waves */
+static const uint32_t k_gemm_threads[N_GEMM_TILES] = { 256, 256, 256, 256, 256, 256, 256, 256, 256, 512, 512, 512, 512,
+                                                       1024, 1024 };
 
 /* workgroups of tile shape t for these jobs and tokens */
 static uint64_t gemm_grid(int t, const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t m) {
@@ -1105,17 +1120,18 @@ int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size
     }
     int tile = g.force_gemm_tile - 1;
     if (tile < 0 && n % 256 == 0) {
-        /* measured on MI355X (K = 2560 and 6912, 16 to 512 tokens): the
-         * direct-load tiles win everywhere. Pick the largest whose grid still
-         * gives every CU work: 64 x 256 from 1.5 workgroups per CU, 32 x 128
-         * from 1.9, else 32 x 64, and 16 x 64 for up to 32 tokens or when
-         * 32 x 64 would leave CUs idle. */
+        /* measured on MI355X (K = 2560 and 6912, 4 to 512 tokens): the
+         * direct-load tiles win everywhere. Up to 64 tokens the sixteen-wave
+         * 16 x 64 / 32 x 64 tiles (four K groups; each tensor streamed once
+         * per token tile); to 256 tokens the eight-wave 32 x 128, or 32 x 64
+         * when that grid would cover under half the CUs; above 256 tokens the
+         * eight-wave 64 x 256 when its grid covers three quarters of the
+         * CUs, else 32 x 128. */
         const uint64_t cu = (uint64_t) (g.cu > 0 ? g.cu : 256);
-        if (m <= 32) tile = 5;
-        else if (m > 128 && gemm_grid(8, jobs, n_jobs, m) * 2 >= cu * 3) tile = 8;
-        else if (m > 128 && gemm_grid(7, jobs, n_jobs, m) * 8 >= cu * 15) tile = 7;
-        else if (gemm_grid(6, jobs, n_jobs, m) * 2 >= cu * 3) tile = 6;
-        else tile = 5;
+        if (m <= 16) tile = 13;
+        else if (m <= 64) tile = gemm_grid(14, jobs, n_jobs, m) * 4 >= cu * 3 ? 14 : 13;
+        else if (m <= 256) tile = gemm_grid(12, jobs, n_jobs, m) * 2 >= cu ? 12 : 14;
+        else tile = gemm_grid(9, jobs, n_jobs, m) * 4 >= cu * 3 ? 9 : 12;
     } else if (tile < 0) {
         /* K % 256 != 0: split-K tiles up to 64 tokens, else 64 x 128 */
         tile = m <= 64 ? 0 : 2;
@@ -1139,8 +1155,128 @@ int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size
     if (gx == 0) return SLLM_GFX950_OK;
     if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");
     void *args[] = { &a };
-    HIP_TRY(hipModuleLaunchKernel(g.k_gemm[tile], (uint32_t) gx, (uint32_t) gy, 1, 256, 1, 1, 0, g.stream, args, NULL));
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm[tile], (uint32_t) gx, (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
+                                  g.stream, args, NULL));
     return SLLM_GFX950_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* GEMM plans (i2s_kernels.hip: gemm_table, gemm_tjob)                 */
+/* ------------------------------------------------------------------ */
+
+typedef struct k_gemm_tjob {
+    const uint8_t         *w;
+    const int8_t          *q;
+    const sllm_gfx950_act *act;
+    float                 *out;
+    int32_t               *out_i;
+    uint32_t               n_rows, k, tile0, pad;
+} k_gemm_tjob;
+
+typedef struct k_gemm_table {
+    const k_gemm_tjob *jobs;
+    const uint32_t    *tile_job;
+    uint32_t           m, pad;
+} k_gemm_table;
+
+_Static_assert(sizeof(k_gemm_tjob) == 56, "k_gemm_tjob must match gemm_tjob in i2s_kernels.hip");
+_Static_assert(sizeof(k_gemm_table) == 24, "k_gemm_table must match gemm_table in i2s_kernels.hip");
+
+/* the plan kernels: the tile shapes 6, 7, 13, 11 and 10 over a table */
+static const int k_gemm_t_shape[5] = { 5, 6, 12, 10, 9 };
+
+struct sllm_gfx950_gemm_plan {
+    uint8_t      *tables_dev;     /* jobs, then the row tile -> job map */
+    k_gemm_table  table;
+    uint32_t      gx, gy;
+    int           kind;           /* index into k_gemm_t */
+};
+
+int sllm_gfx950_gemm_plan_create(const sllm_gfx950_gemm_plan_job *jobs, size_t n_jobs, size_t m,
+                                 sllm_gfx950_gemm_plan **plan) {
+    NEED_OPEN();
+    if (plan == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan: NULL out pointer");
+    *plan = NULL;
+    if (jobs == NULL || n_jobs == 0 || n_jobs > UINT32_MAX / 2) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan: bad job list");
+    if (m == 0 || m > (size_t) 65535 * 16) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm_plan: m = %zu", m);
+    for (size_t j = 0; j < n_jobs; ++j) {
+        const sllm_gfx950_gemm_plan_job *J = &jobs[j];
+        const int st = check_weights(J->w, J->n_rows, J->n);
+        if (st != SLLM_GFX950_OK) return st;
+        if (J->n % 256 != 0) return fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "gemm_plan: job %zu K=%zu is not a multiple of 256", j, J->n);
+        if (J->q == NULL || ((uintptr_t) J->q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan: job %zu q must be given and 16-byte aligned", j);
+        if (J->out == NULL && J->rows_out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan: job %zu has no output", j);
+        if (J->out != NULL && J->act == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan: job %zu: the epilogue needs act", j);
+        if ((uint64_t) m * J->n_rows > (uint64_t) 1 << 40) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm_plan: m x rows too large");
+    }
+    /* the tile: forced, or by token count (measured on the FFN tensors of
+     * 32 weight sets: 32 x 128 up to 32 tokens, 64 x 256 above) */
+    int kind = -1;
+    for (int i = 0; i < 5; ++i) if (g.force_gemm_tile - 1 == k_gemm_t_shape[i]) kind = i;
+    if (kind < 0) kind = m <= 32 ? 2 : 4;
+    const int shape = k_gemm_t_shape[kind];
+    const uint32_t rows_per = k_gemm_rows[shape], tok_per = k_gemm_tokens[shape];
+    uint64_t gx = 0;
+    for (size_t j = 0; j < n_jobs; ++j) gx += (jobs[j].n_rows + rows_per - 1) / rows_per;
+    const uint64_t gy = (m + tok_per - 1) / tok_per;
+    if (gx == 0) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan: no rows");
+    if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm_plan: grid too large");
+    const size_t jbytes = n_jobs * sizeof(k_gemm_tjob), bytes = jbytes + (size_t) gx * sizeof(uint32_t);
+    uint8_t *host = malloc(bytes);
+    sllm_gfx950_gemm_plan *p = calloc(1, sizeof *p);
+    if (host == NULL || p == NULL) {
+        free(host);
+        free(p);
+        return fail(SLLM_GFX950_ERR_NOMEM, "gemm_plan: host tables");
+    }
+    k_gemm_tjob *kj = (k_gemm_tjob *) host;
+    uint32_t *tile_job = (uint32_t *) (host + jbytes);
+    uint32_t tile = 0;
+    for (size_t j = 0; j < n_jobs; ++j) {
+        const uint32_t tiles = (uint32_t) ((jobs[j].n_rows + rows_per - 1) / rows_per);
+        kj[j] = (k_gemm_tjob) { jobs[j].w, jobs[j].q, jobs[j].act, jobs[j].out, jobs[j].rows_out,
+                                (uint32_t) jobs[j].n_rows, (uint32_t) jobs[j].n, tile, 0 };
+        for (uint32_t t = 0; t < tiles; ++t) tile_job[tile + t] = (uint32_t) j;
+        tile += tiles;
+    }
+    hipError_t e = hipMalloc((void **) &p->tables_dev, bytes);
+    if (e != hipSuccess) {
+        p->tables_dev = NULL;
+    } else {
+        e = hipMemcpy(p->tables_dev, host, bytes, hipMemcpyHostToDevice);
+    }
+    free(host);
+    if (e != hipSuccess) {
+        if (p->tables_dev) hipFree(p->tables_dev);
+        free(p);
+        return hip_fail(e, "gemm_plan: tables");
+    }
+    p->table = (k_gemm_table) { (const k_gemm_tjob *) p->tables_dev,
+                                (const uint32_t *) (p->tables_dev + jbytes), (uint32_t) m, 0 };
+    p->gx = (uint32_t) gx;
+    p->gy = (uint32_t) gy;
+    p->kind = kind;
+    *plan = p;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_gemm_plan_run(const sllm_gfx950_gemm_plan *p) {
+    NEED_OPEN();
+    if (p == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan_run: NULL plan");
+    k_gemm_table t = p->table;
+    void *args[] = { &t };
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm_t[p->kind], p->gx, p->gy, 1, k_gemm_threads[k_gemm_t_shape[p->kind]],
+                                  1, 1, 0, g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
+void sllm_gfx950_gemm_plan_destroy(sllm_gfx950_gemm_plan *p) {
+    if (p == NULL) return;
+    if (g.open) {
+        hipStreamSynchronize(g.stream);
+        hipFree(p->tables_dev);
+    }
+    free(p);
 }
 
 int sllm_gfx950_gemm(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,

@@ -324,16 +324,36 @@ struct gemm_view {
     float         *out;
     int32_t       *out_i;
     uint32_t       n_rows, tile;
+    const int8_t  *q;
+    const act_t   *act;
 };
 
-__device__ __forceinline__ gemm_view gemm_pick(const gemm_args &G) {
-    const uint32_t b = blockIdx.x, t0 = G.tiles[0], t01 = t0 + G.tiles[1];
+// One tensor of a GEMM plan (gemm_table): its own token rows, K and
+// outputs; tile0 is its first row tile in the plan (mirrored in
+// gfx950_shim.c).
+struct gemm_tjob {
+    const uint8_t *w;
+    const int8_t  *q;            // [m][k] int8
+    const act_t   *act;          // [m], or null without an epilogue
+    float         *out;          // [m][n_rows] epilogue, or null
+    int32_t       *out_i;        // [m][n_rows] raw dots, or null
+    uint32_t       n_rows, k, tile0, pad;
+};
+
+struct gemm_table {
+    const gemm_tjob *jobs;
+    const uint32_t  *tile_job;   // row tile -> job
+    uint32_t         m, pad;
+};
+
+__device__ __forceinline__ gemm_view gemm_pick(const gemm_args &G, uint32_t b = blockIdx.x) {
+    const uint32_t t0 = G.tiles[0], t01 = t0 + G.tiles[1];
     const uint32_t j = b < t0 ? 0u : (b < t01 ? 1u : 2u);       // uniform; selects, no indexing
     return { j == 0 ? G.w[0] : (j == 1 ? G.w[1] : G.w[2]),
              j == 0 ? G.out[0] : (j == 1 ? G.out[1] : G.out[2]),
              j == 0 ? G.out_i[0] : (j == 1 ? G.out_i[1] : G.out_i[2]),
              j == 0 ? G.n_rows[0] : (j == 1 ? G.n_rows[1] : G.n_rows[2]),
-             b - (j == 0 ? 0u : (j == 1 ? t0 : t01)) };
+             b - (j == 0 ? 0u : (j == 1 ? t0 : t01)), G.q, G.act };
 }
 
 template <int TM, int TN>
@@ -640,19 +660,52 @@ __device__ __forceinline__ void wait_vmem() {   // s_waitcnt vmcnt(N), the other
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *) (p))
 
-template <int TM, int TN, int STAGES>
-__device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
+// XCD-aware placement. Workgroups are dealt to the eight XCDs round-robin by
+// linear id (x fastest); XCD s is given a contiguous run of the tiles, row
+// tile slowest, so the workgroups that share a weight tile (all its token
+// tiles) share one L2 and the weights cross the fabric once, not once per
+// token tile. (bx, by): this workgroup's row tile and token tile.
+__device__ __forceinline__ void gemm_place(uint32_t &bx, uint32_t &by) {
+    const uint32_t gx = gridDim.x, gy = gridDim.y, n = gx * gy;
+    const uint32_t lin = blockIdx.y * gx + blockIdx.x;
+    const uint32_t s = lin & 7u, q = n >> 3, r = n & 7u;     // XCD s holds q + (s < r) workgroups
+    const uint32_t t = s * q + min(s, r) + (lin >> 3);
+    bx = t / gy;
+    by = t - bx * gy;
+}
+
+// KG K groups: with KG = 2 the workgroup is eight waves, two groups of four
+// over the same tile; group k takes super-steps k, k + 2, k + 4, ... (two
+// waves on every SIMD, one of each group, so that one's waits are covered by
+// the other's MFMAs), and the groups' int32 sums meet in LDS at the end
+// (exact in any order).
+template <int TM, int TN, int STAGES, int KG = 1>
+__device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
     constexpr uint32_t A_BYTES = BM * 256u, STAGE = A_BYTES + BN * 64u;
     constexpr int VM = TM + TN;                     // copies per wave per super-step
-    static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 2) * VM < 64, "stages");
-    __shared__ __attribute__((aligned(1024))) uint8_t S[STAGES * STAGE];
-    const gemm_view V = gemm_pick(G);
+    constexpr int D = STAGES / KG;                  // ring depth in iterations
+    static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
+    static_assert(STAGES % KG == 0 && D >= 2 && (D - 2) * VM < 64, "stages");
+    // the epilogue reuses the ring: the tile as BM rows of EP (BN + 4) words,
+    // then post and sum of the BM tokens
+    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = E_TILE + BM * 8u;
+    constexpr uint32_t S_BYTES = STAGES * STAGE > E_BYTES ? STAGES * STAGE : E_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t S[S_BYTES];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wave = wave_all & 3u, kgrp = wave_all >> 2;   // place in the tile, K group
     const uint32_t g = lane >> 4, li = lane & 15u;
-    const uint32_t t0 = blockIdx.y * BM, n0 = V.tile * BN;
-    const uint32_t nsup = G.k / 256u, kb = G.k >> 2;
+    const uint32_t t0 = by * BM, n0 = V.tile * BN;
+    const uint32_t nsup = k / 256u, kb = k >> 2;
+    // the epilogue's operands, loaded now so that their latency hides behind
+    // the main loop: w_scale, and token t0 + tid's act for the first BM threads
+    float ep_ws = 0.0f;
+    act_t ep_at = { 1.0f, 0 };
+    if (tid < BM) {
+        ep_ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+        if (V.act != nullptr) ep_at = V.act[min(t0 + tid, m - 1)];
+    }
     // copy sources: instruction j of this wave fills LDS granules
     // (4 j + wave) * 64 + lane of the token and the weight block
     const int8_t *asrc[TM];
@@ -660,7 +713,7 @@ __device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
     for (int j = 0; j < TM; ++j) {
         const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
         const uint32_t t = p >> 4, gr = (p & 15u) ^ (t & 15u);
-        asrc[j] = G.q + (size_t) min(t0 + t, G.m - 1) * G.k + gr * 16u;
+        asrc[j] = V.q + (size_t) min(t0 + t, m - 1) * k + gr * 16u;
     }
     const uint8_t *bsrc[TN];
 #pragma unroll
@@ -669,9 +722,11 @@ __device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
         const uint32_t r = p >> 2, ch = (p & 3u) ^ ((r >> 2) & 3u);
         bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb + ch * 16u;
     }
-    auto issue = [&](uint32_t s, uint32_t slot) {   // super-steps past the end re-copy the last (never read)
+    // super-step s lives in slot s % STAGES; past the end the last one is
+    // copied again (never read)
+    auto issue = [&](uint32_t s) {
         const uint32_t sc = min(s, nsup - 1);
-        uint8_t *base = S + slot * STAGE;
+        uint8_t *base = S + (s % STAGES) * STAGE;
 #pragma unroll
         for (int j = 0; j < TM; ++j)
             __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + sc * 256u),
@@ -692,19 +747,24 @@ __device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
     }
+    // iteration it: group k multiplies super-step KG it + k
+    const uint32_t iters = (nsup + KG - 1) / KG;
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) issue((uint32_t) s, (uint32_t) s);
-    for (uint32_t s = 0; s < nsup; ++s) {
-        // this super-step's copies done (later ones may stay in flight), then everyone's
-        const uint32_t ahead = min(nsup - 1u - s, (uint32_t) STAGES - 2u);
-        if (ahead == 0) wait_vmem<0>();
+    for (int i = 0; i < D - 1; ++i) issue((uint32_t) (KG * i) + kgrp);
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t s = KG * it + kgrp;
+        // this iteration's copies done (later ones may stay in flight), then everyone's
+        // (near the end, fewer are in flight: wait for all but the next one)
+        const uint32_t ahead = min(iters - 1u - it, (uint32_t) D - 2u);
+        if (ahead == (uint32_t) D - 2u) wait_vmem<(D - 2) * VM>();
         else if (ahead == 1) wait_vmem<VM>();
-        else wait_vmem<(STAGES - 2) * VM>();
+        else wait_vmem<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's reads of the stage being refilled done
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        issue(s + STAGES - 1, (s + STAGES - 1) % STAGES);
+        issue(s + (uint32_t) (KG * (D - 1)));
         __builtin_amdgcn_sched_barrier(0);
+        if (KG > 1 && s >= nsup) continue;          // an odd count: the last iteration is group 0's alone
         const uint8_t *st = S + (s % STAGES) * STAGE;
         u32x4 raw[TN];
 #pragma unroll
@@ -753,27 +813,101 @@ __device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
     wait_vmem<0>();                                 // no copy may land after the workgroup leaves
 
     // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
-    // token, (float)(dot - sum) * post
-    const float ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+    // token, (float)(dot - sum) * post. The tile goes through LDS so that
+    // every store writes whole rows of the output: a lane's accumulators hold
+    // rows 16 apart, the store wants four consecutive ones per lane.
+    __syncthreads();                                // every wave done with the ring
+    uint32_t *tile = reinterpret_cast<uint32_t *>(S);
+    float *post_s = reinterpret_cast<float *>(S + E_TILE);
+    int32_t *sum_s = reinterpret_cast<int32_t *>(S + E_TILE + BM * 4u);
+    auto tile_at = [&](int tm, int tn, int r) -> uint32_t & {
+        return tile[(16u * (uint32_t) tm + 4u * g + (uint32_t) r) * EP + wr + 16u * (uint32_t) tn + li];
+    };
+    // the other groups' sums into group 0's, one group at a time
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
+    for (uint32_t k2 = 1; k2 < (uint32_t) KG; ++k2) {
+        if (kgrp == k2) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t t = t0 + 16u * (uint32_t) tm + 4u * g + (uint32_t) r;
-            if (t >= G.m) continue;
-            const act_t at = G.act != nullptr ? G.act[t] : act_t { 1.0f, 0 };
-            const float post = ws / at.scale;
+            for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                const uint32_t n = n0 + wr + 16u * (uint32_t) tn + li;
-                if (n < V.n_rows) {
-                    const int32_t d = c[tm][tn][r];
-                    if (V.out_i != nullptr) G_CAST(int32_t, V.out_i)[(size_t) t * V.n_rows + n] = d;
-                    if (V.out != nullptr) G_CAST(float, V.out)[(size_t) t * V.n_rows + n] = (float) (d - at.sum) * post;
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tile_at(tm, tn, r) = (uint32_t) c[tm][tn][r];
+        }
+        __syncthreads();
+        if (kgrp == 0) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) c[tm][tn][r] += (int32_t) tile_at(tm, tn, r);
+        }
+        __syncthreads();
+    }
+    if (tid < BM) {
+        post_s[tid] = ep_ws / ep_at.scale;
+        sum_s[tid] = ep_at.sum;
+    }
+    __syncthreads();
+    constexpr uint32_t LPT = BN / 4u;               // lanes per tile row in the stores
+    constexpr uint32_t RPS = 64u / LPT;             // tile rows per store instruction
+    const uint32_t srow = lane / LPT, scol = 4u * (lane % LPT);
+    auto emit = [&](bool raw, uint32_t *dst) {
+        if (kgrp == 0) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = 16u * (uint32_t) tm + 4u * g + (uint32_t) r;
+                    const float post = post_s[row];
+                    const int32_t sum = sum_s[row];
+#pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) {
+                        const int32_t d = c[tm][tn][r];
+                        tile_at(tm, tn, r) = raw ? (uint32_t) d : __float_as_uint((float) (d - sum) * post);
+                    }
                 }
             }
         }
-    }
+        __syncthreads();
+        const bool vec = (V.n_rows & 3u) == 0 && ((uintptr_t) dst & 15u) == 0;
+        for (uint32_t row0 = wave_all * RPS; row0 < BM; row0 += 4u * KG * RPS) {
+            const uint32_t row = row0 + srow, t = t0 + row, n = n0 + scol;
+            if (t < m && n < V.n_rows) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + row * EP + scol);
+                GLOBAL uint32_t *o = G_CAST(uint32_t, dst) + (size_t) t * V.n_rows + n;
+                // streaming stores: written through as the tiles finish
+                // rather than left dirty in L2 for the end-of-kernel writeback
+                if (vec) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<GLOBAL u32x4 *>(o));
+                } else {
+#pragma unroll
+                    for (uint32_t e = 0; e < 4u; ++e) if (n + e < V.n_rows) __builtin_nontemporal_store(v[e], o + e);
+                }
+            }
+        }
+        __syncthreads();                            // before the tile is written again
+    };
+    if (V.out_i != nullptr) emit(true, reinterpret_cast<uint32_t *>(V.out_i));
+    if (V.out != nullptr) emit(false, reinterpret_cast<uint32_t *>(V.out));
+}
+
+// the tile of a three-job launch (gemm_args) or of a plan (gemm_table)
+template <int TM, int TN, int STAGES, int KG = 1>
+__device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
+    uint32_t bx, by;
+    gemm_place(bx, by);
+    gemm_dl_tile<TM, TN, STAGES, KG>(gemm_pick(G, bx), G.k, G.m, by);
+}
+
+template <int TM, int TN, int STAGES, int KG = 1>
+__device__ __forceinline__ void gemm_dl_table(const gemm_table &T) {
+    uint32_t bx, by;
+    gemm_place(bx, by);
+    const gemm_tjob &J = T.jobs[T.tile_job[bx]];
+    const gemm_view V = { J.w, J.out, J.out_i, J.n_rows, bx - J.tile0, J.q, J.act };
+    gemm_dl_tile<TM, TN, STAGES, KG>(V, J.k, T.m, by);
 }
 
 } // namespace
@@ -975,6 +1109,33 @@ extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_dl2x2(gemm_args G) { gemm_dl_block<2, 2, 4>(G); }
 extern "C" __global__ void __launch_bounds__(256)
 sllm_k_gemm_dl4x4(gemm_args G) { gemm_dl_block<4, 4, 2>(G); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk4x4(gemm_args G) { gemm_dl_block<4, 4, 4, 2>(G); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk4x2(gemm_args G) { gemm_dl_block<4, 2, 4, 2>(G); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk2x4(gemm_args G) { gemm_dl_block<2, 4, 4, 2>(G); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk2x2(gemm_args G) { gemm_dl_block<2, 2, 4, 2>(G); }
+// sixteen waves in four K groups over a 16 x 64 / 32 x 64 tile: for grids
+// of fewer workgroups than CUs (a lone tensor against a few tokens), each
+// group walks a quarter of the super-steps
+extern "C" __global__ void __launch_bounds__(1024)
+sllm_k_gemm_dq1x1(gemm_args G) { gemm_dl_block<1, 1, 8, 4>(G); }
+extern "C" __global__ void __launch_bounds__(1024)
+sllm_k_gemm_dq2x1(gemm_args G) { gemm_dl_block<2, 1, 8, 4>(G); }
+
+// the same tiles over a plan's table of tensors
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_tdl1x1(gemm_table T) { gemm_dl_table<1, 1, 4>(T); }
+extern "C" __global__ void __launch_bounds__(256)
+sllm_k_gemm_tdl2x1(gemm_table T) { gemm_dl_table<2, 1, 4>(T); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_tdk2x2(gemm_table T) { gemm_dl_table<2, 2, 4, 2>(T); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_tdk4x2(gemm_table T) { gemm_dl_table<4, 2, 4, 2>(T); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_tdk4x4(gemm_table T) { gemm_dl_table<4, 4, 4, 2>(T); }
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

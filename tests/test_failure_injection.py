@@ -94,6 +94,9 @@ class Env:
         assert L.sllm_gfx950_plan_create(self.jobs, 2, byref(self.plan)) == 0
         self.gemm_jobs = (amd.GemmJob * 2)(amd.GemmJob(self.w, self.n_rows, self.out, None),
                                            amd.GemmJob(self.w, self.n_rows, None, self.out_i))
+        gp = (amd.GemmPlanJob * 1)(amd.GemmPlanJob(self.w, self.n_rows, self.n, self.q, self.act, self.out, None))
+        self.gemm_plan = c_void_p()
+        assert L.sllm_gfx950_gemm_plan_create(gp, 1, 4, byref(self.gemm_plan)) == 0, _err(L)
         assert L.sllm_gfx950_events_reserve(4) == 0
         assert L.sllm_gfx950_event_record(0) == 0 and L.sllm_gfx950_event_record(1) == 0
         # a tiny model, as host arrays and as a GGUF image
@@ -143,6 +146,7 @@ class Env:
             L.sllm_gfx950_ctx_free(self.c)
             L.sllm_gfx950_model_free(self.m)
             L.sllm_gfx950_plan_destroy(self.plan)
+            L.sllm_gfx950_gemm_plan_destroy(self.gemm_plan)
             for p in self.keep:
                 L.sllm_gfx950_free(p)
         self.keep = []
@@ -213,6 +217,15 @@ def scenarios(E):
                                                            V(E.act), 4)))
     add("linear_batch", lambda: st(L.sllm_gfx950_linear_batch(V(E.w), nr, n, V(E.x), 4, V(E.q), V(E.act),
                                                                V(E.out), None)))
+    gp_jobs = (amd.GemmPlanJob * 2)(amd.GemmPlanJob(E.w, nr, n, E.q, E.act, E.out, None),
+                                    amd.GemmPlanJob(E.w, nr, n, E.q, E.act, None, E.out_i))
+
+    def gemm_plan_create():
+        p = c_void_p()
+        return L.sllm_gfx950_gemm_plan_create(gp_jobs, 2, 4, byref(p)), p
+
+    add("gemm_plan_create", gemm_plan_create, cleanup=lambda p: L.sllm_gfx950_gemm_plan_destroy(p))
+    add("gemm_plan_run", lambda: st(L.sllm_gfx950_gemm_plan_run(E.gemm_plan)))
 
     def register():
         return L.sllm_gfx950_tensor_register(P(E.w_host), nr, n), None
@@ -330,7 +343,7 @@ def test_every_failed_allocation_returns_nomem(env):
                         _sweep(env.L, name, *s, "hipHostMalloc", HIP_OUT_OF_MEMORY, NOMEM))
     # the calls that allocate were driven through their allocations
     for name in ("malloc", "plan_create", "gemv_batch", "tensor_register", "model_upload", "model_load_gguf",
-                 "ctx_new"):
+                 "ctx_new", "gemm_plan_create"):
         assert points[name] > 0, name
 
 
@@ -412,6 +425,8 @@ calls = {{
   "gemm": lambda: L.sllm_gfx950_gemm(None, 1, 128, None, None, 1, None, None),
   "gemm_multi": lambda: L.sllm_gfx950_gemm_multi(None, 1, 128, None, None, 1),
   "linear_batch": lambda: L.sllm_gfx950_linear_batch(None, 1, 128, None, 1, None, None, None, None),
+  "gemm_plan_create": lambda: L.sllm_gfx950_gemm_plan_create(None, 1, 1, ctypes.byref(p)),
+  "gemm_plan_run": lambda: L.sllm_gfx950_gemm_plan_run(None),
   "tensor_register": lambda: L.sllm_gfx950_tensor_register(None, 1, 128),
   "tensor_unregister": lambda: L.sllm_gfx950_tensor_unregister(None),
   "device_info": lambda: L.sllm_gfx950_device_info(None, 0, None, None),

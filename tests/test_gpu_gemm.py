@@ -10,6 +10,8 @@ projection (640 x 2560) and a ragged one (200 rows, K = 384); token counts
 on and off the 16-token MFMA tile, up to the 512-token prefill chunk; every
 tile shape the kernel has.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -65,7 +67,7 @@ def test_gemm_matches_the_oracle_token_by_token(amd, orc, dev, n_rows, n, m):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"{n_rows}x{n} m={m}")
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("tile", list(range(1, 16)))
 def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     n_rows, n, m = 640, 2560, 37
     w, x = _case(amd, 2, n_rows, n, m)
@@ -77,7 +79,7 @@ def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"tile {tile}")
 
 
-@pytest.mark.parametrize("tile", [0, 1, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("tile", [0, 1, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15])
 @pytest.mark.parametrize("m", [37, 512])
 def test_several_tensors_in_one_launch(amd, orc, dev, tile, m):
     """Q, K and V (2560, 640, 640 rows) against the same quantised rows in
@@ -141,7 +143,78 @@ def test_gemm_refuses_bad_arguments(amd, dev):
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, None, 2, o.vp, None) == -1     # epilogue without act
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 2, None, None) == -1     # no output
         assert lib.sllm_gfx950_gemm(w.vp, 64, 256, q.vp, a.vp, 0, o.vp, None) == 0      # nothing to do
-        assert lib.sllm_gfx950_set_gemm_tile(10) == -1
+        assert lib.sllm_gfx950_set_gemm_tile(16) == -1
     finally:
         for b in (w, q, a, o):
             b.free()
+
+
+@pytest.mark.parametrize("tile", [0, 6, 7, 10, 11, 13])
+@pytest.mark.parametrize("m", [4, 17, 64, 100])
+def test_gemm_plan_over_many_tensors(amd, orc, dev, tile, m):
+    """A GEMM plan of six tensors with their own K (2560 and 6912), token
+    rows and outputs, one launch: each job's dots and outputs are the single
+    sllm_gfx950_gemm's for it, and the oracle's on the first and last token."""
+    shapes = [(640, 2560), (2560, 6912), (384, 2560), (128, 6912), (2560, 2560), (64, 2560)]
+    ws = [amd.synth_i2s(amd.synth_seed(8, j, r, k), r, k) for j, (r, k) in enumerate(shapes)]
+    xs = [np.concatenate([amd.synth_normal(amd.synth_seed(8, j, t, 3000), k) for t in range(m)]).astype(np.float32)
+          for j, (r, k) in enumerate(shapes)]
+    bw = [dev.put(w) for w in ws]
+    bx = [dev.put(x) for x in xs]
+    bq = [dev.alloc(m * k) for r, k in shapes]
+    ba = [dev.alloc(8 * m) for _ in shapes]
+    outs = [(dev.alloc(4 * m * r), dev.alloc(4 * m * r)) for r, k in shapes]
+    refs = [(dev.alloc(4 * m * r), dev.alloc(4 * m * r)) for r, k in shapes]
+    print(f"[gemm plan] tile {tile} m={m}", flush=True)
+    dev.set_gemm_tile(tile)
+    plan = None
+    try:
+        for j, (r, k) in enumerate(shapes):
+            dev.quant_act(bx[j].vp, k, m, bq[j].vp, ba[j].vp)
+        # job 1 writes only raw dots, job 4 only the epilogue
+        plan = dev.gemm_plan([(bw[j].vp, r, k, bq[j].vp, ba[j].vp, None if j == 1 else outs[j][0].vp,
+                               None if j == 4 else outs[j][1].vp) for j, (r, k) in enumerate(shapes)], m)
+        dev.gemm_plan_run(plan)
+        dev.set_gemm_tile(0)
+        for j, (r, k) in enumerate(shapes):
+            dev.gemm(bw[j].vp, r, k, bq[j].vp, ba[j].vp, m, refs[j][0].vp, refs[j][1].vp)
+        dev.sync()
+        for j, (r, k) in enumerate(shapes):
+            yr = refs[j][0].download(np.float32, m * r).reshape(m, r)
+            dr = refs[j][1].download(np.int32, m * r).reshape(m, r)
+            if j != 1:
+                y = outs[j][0].download(np.float32, m * r).reshape(m, r)
+                assert np.array_equal(bits(y), bits(yr)), f"job {j}"
+            if j != 4:
+                d = outs[j][1].download(np.int32, m * r).reshape(m, r)
+                assert np.array_equal(d, dr), f"job {j}"
+            for t in (0, m - 1):
+                yo, qo, do, so, su = orc.linear(ws[j], r, k, xs[j][t * k:(t + 1) * k])
+                assert np.array_equal(dr[t], do) and np.array_equal(bits(yr[t]), bits(yo)), f"job {j} token {t}"
+    finally:
+        dev.set_gemm_tile(0)
+        if plan is not None:
+            dev.gemm_plan_destroy(plan)
+        for b in bw + bx + bq + ba + [b for p in outs + refs for b in p]:
+            b.free()
+
+
+def test_gemm_plan_refuses_bad_jobs(amd, dev):
+    lib = amd.lib()
+    w = dev.put(amd.synth_i2s(1, 64, 384))
+    q, a, o = dev.alloc(384 * 2), dev.alloc(16), dev.alloc(4 * 64 * 2)
+    p = ctypes.c_void_p()
+    try:
+        def create(job, m=2):
+            arr = (amd.GemmPlanJob * 1)(amd.GemmPlanJob(*job))
+            return lib.sllm_gfx950_gemm_plan_create(arr, 1, m, ctypes.byref(p))
+        assert create((w.vp, 64, 384, q.vp, a.vp, o.vp, None)) == -34        # K % 256
+        assert create((w.vp, 64, 256, q.vp, None, o.vp, None)) == -1         # epilogue without act
+        assert create((w.vp, 64, 256, q.vp, a.vp, None, None)) == -1         # no output
+        assert create((w.vp, 64, 256, None, a.vp, o.vp, None)) == -1         # no q
+        assert create((w.vp, 64, 256, q.vp, a.vp, o.vp, None), m=0) == -36
+        assert lib.sllm_gfx950_gemm_plan_run(None) == -1
+    finally:
+        for b in (w, q, a, o):
+            b.free()
+
