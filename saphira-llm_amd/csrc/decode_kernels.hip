@@ -91,10 +91,24 @@ __device__ __forceinline__ float silu(float v) {
     return v / (1.0f + ggml_v_expf(0.0f - v));
 }
 
+// Sum over the wave in double, as wave_sum (every lane gets it). The order
+// of the additions is not the reference's: the callers' checks allow any.
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_d(double v) {
+    return __hiloint2double(dpp_mov<CTRL>(__double2hiint(v)), dpp_mov<CTRL>(__double2loint(v)));
+}
+
+__device__ __forceinline__ double read_lane_d(double v, int lane) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                            __builtin_amdgcn_readlane(__double2loint(v), lane));
+}
+
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_mov_d<DPP_XOR1>(v);
+    v += dpp_mov_d<DPP_XOR2>(v);
+    v += dpp_mov_d<DPP_HALF_MIRROR>(v);
+    v += dpp_mov_d<DPP_MIRROR>(v);
+    return (read_lane_d(v, 0) + read_lane_d(v, 16)) + (read_lane_d(v, 32) + read_lane_d(v, 48));
 }
 
 // ---------------------------------------------------------------------------

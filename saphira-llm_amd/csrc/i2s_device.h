@@ -39,16 +39,38 @@ struct act_t {          // layout of sllm_i2s_act (include/saphira_llm/i2s_gemm.
 // wave / block reductions
 // ---------------------------------------------------------------------------
 
+// All-reduce over the 64 lanes of a wave: the four rows of 16 lanes reduce
+// among themselves with DPP moves (xor 1, xor 2, half-row mirror, row
+// mirror: every lane of a row then holds its row's total), and the four row
+// totals are read with v_readlane. No LDS round trip, unlike a ds_bpermute
+// per step. Every lane of the wave must be active.
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f(float v) { return __int_as_float(dpp_mov<CTRL>(__float_as_int(v))); }
+
+__device__ __forceinline__ float lane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_mov_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_mov_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_mov_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_mov_f<DPP_MIRROR>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_mov<DPP_XOR1>(v);
+    v += dpp_mov<DPP_XOR2>(v);
+    v += dpp_mov<DPP_HALF_MIRROR>(v);
+    v += dpp_mov<DPP_MIRROR>(v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
 // Sum over aligned groups of LPR lanes with DPP moves. Every lane of the wave
