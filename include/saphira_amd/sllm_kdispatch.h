@@ -57,6 +57,13 @@ const sllm_kernel_row *sllm_kdispatch_row(size_t i);
 int  sllm_kdispatch_select(const char *name);
 /* The installed row, or NULL. */
 const sllm_kernel_row *sllm_kdispatch_installed(void);
+/* The installed row's name, "none" before any select. The diagnostic the
+ * reference reads as sllm_i2s_dot_isa / sllm_i2s_installed_isa
+ * (include/saphira_llm/i2s_gemm.h:113, :137; printed by bench/tg_bench.c:231
+ * and checked after model load by tests/test_i2s.c:500-537). Pinning one row
+ * without "auto", the reference's sllm_i2s_select_level (i2s_gemm.h:134), is
+ * sllm_kdispatch_select with that row's name. */
+const char            *sllm_kdispatch_installed_name(void);
 /* Forget the installed row (tests). */
 void sllm_kdispatch_reset(void);
 

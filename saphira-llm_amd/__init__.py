@@ -120,6 +120,7 @@ PROTOTYPES = {
     "sllm_kdispatch_row": (POINTER(KernelRow), [c_size_t]),
     "sllm_kdispatch_select": (c_int, [c_char_p]),
     "sllm_kdispatch_installed": (POINTER(KernelRow), []),
+    "sllm_kdispatch_installed_name": (c_char_p, []),
     "sllm_kdispatch_reset": (None, []),
     "sllm_kdispatch_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "sllm_kdispatch_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),

@@ -712,14 +712,14 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
         float xt = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float xi = __shfl(v[i], (int) lt, 64);
+            const float xi = lane_f(v[i], (int) lt);
             xt = lane == (uint32_t) i ? xi : xt;
         }
         float et = 0.0f;
         if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float ei = __shfl(et, i, 64);
+            const float ei = lane_f(et, i);
             if (lane == lt && (uint32_t) i < cnt) v[i] = ei;
         }
     };
@@ -776,7 +776,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                     if ((uint32_t) g == gt) {
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
-                            const float xi = __shfl(v[g][i], (int) lt, 64);
+                            const float xi = lane_f(v[g][i], (int) lt);
                             xt = lane == (uint32_t) i ? xi : xt;
                         }
                     }
@@ -785,7 +785,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const float ei = __shfl(et, i, 64);
+                    const float ei = lane_f(et, i);
 #pragma unroll
                     for (int g = 0; g < RG; ++g) {
                         if ((uint32_t) g == gt && lane == lt && (uint32_t) i < cnt) v[g][i] = ei;
@@ -861,7 +861,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
                 inv = (float) (1.0 / seq);
             }
-            inv = __shfl(inv, 0, 64);
+            inv = lane_f(inv, 0);
         }
         // p of the first round, in place
         const uint32_t n0 = min(npast, PV_RPOS);
@@ -1118,9 +1118,9 @@ sllm_k_dec_lm_head(dec_lm L) {
         if (b == nb - 1) {                                // the row is complete
             float r[8];
 #pragma unroll
-            for (int l = 0; l < 8; ++l) r[l] = acc[l] + __shfl_xor(acc[l], 2, 64);  // acc0 += acc2, acc1 += acc3
+            for (int l = 0; l < 8; ++l) r[l] = acc[l] + dpp_mov_f<DPP_XOR2>(acc[l]);  // acc0 += acc2, acc1 += acc3
 #pragma unroll
-            for (int l = 0; l < 8; ++l) r[l] = r[l] + __shfl_xor(r[l], 1, 64);      // acc0 += acc1
+            for (int l = 0; l < 8; ++l) r[l] = r[l] + dpp_mov_f<DPP_XOR1>(r[l]);      // acc0 += acc1
             const float t0 = r[0] + r[4], t1 = r[1] + r[5], t2 = r[2] + r[6], t3 = r[3] + r[7];
             const float sdot = (t0 + t1) + (t2 + t3);
             const uint32_t row = pass * LM_ROWS + wave * 16 + lane / 4;
@@ -1158,11 +1158,7 @@ sllm_k_dec_lm_head(dec_lm L) {
         }
     }
 
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t other = __shfl_xor(best, o, 64);
-        best = other > best ? other : best;
-    }
+    best = wave_max_u64(best);
     if (lane == 0) red_k[wave] = best;
     __syncthreads();
     if (tid == 0) {
@@ -1183,11 +1179,7 @@ sllm_k_dec_argmax(const uint64_t *__restrict__ partial, uint32_t n, const float 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     uint64_t best = 0;
     for (uint32_t i = tid; i < n; i += 256) best = partial[i] > best ? partial[i] : best;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t other = __shfl_xor(best, o, 64);
-        best = other > best ? other : best;
-    }
+    best = wave_max_u64(best);
     if (lane == 0) red[tid >> 6] = best;
     __syncthreads();
     if (tid != 0) return;
@@ -1516,14 +1508,14 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
         float xt = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float xi = __shfl(v[i], (int) lt, 64);
+            const float xi = lane_f(v[i], (int) lt);
             xt = lane == (uint32_t) i ? xi : xt;
         }
         float et = 0.0f;
         if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float ei = __shfl(et, i, 64);
+            const float ei = lane_f(et, i);
             if (lane == lt && (uint32_t) i < cnt) v[i] = ei;
         }
     };
@@ -1590,7 +1582,7 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
             for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
             inv = (float) (1.0 / seq);
         }
-        inv = __shfl(inv, 0, 64);
+        inv = lane_f(inv, 0);
     }
     // every lane's reads of the row are done (the wave reduced them above)
     if (npast <= 512) {
@@ -1742,11 +1734,7 @@ sllm_k_chk_keys(const float *__restrict__ logits, uint32_t n, uint64_t *__restri
         const uint64_t key = argmax_key(logits[i], i);
         best = key > best ? key : best;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t other = __shfl_xor(best, o, 64);
-        best = other > best ? other : best;
-    }
+    best = wave_max_u64(best);
     if (lane == 0) red[tid >> 6] = best;
     __syncthreads();
     if (tid == 0) {

@@ -64,6 +64,29 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_mov_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t) dpp_mov<CTRL>((int) (uint32_t) v);
+    const uint32_t hi = (uint32_t) dpp_mov<CTRL>((int) (uint32_t) (v >> 32));
+    return ((uint64_t) hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int lane) {
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) v, lane);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (v >> 32), lane);
+    return ((uint64_t) hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_u64(v, dpp_mov_u64<DPP_XOR1>(v));
+    v = max_u64(v, dpp_mov_u64<DPP_XOR2>(v));
+    v = max_u64(v, dpp_mov_u64<DPP_HALF_MIRROR>(v));
+    v = max_u64(v, dpp_mov_u64<DPP_MIRROR>(v));
+    return max_u64(max_u64(lane_u64(v, 0), lane_u64(v, 16)), max_u64(lane_u64(v, 32), lane_u64(v, 48)));
+}
+
 __device__ __forceinline__ int wave_sum(int v) {
     v += dpp_mov<DPP_XOR1>(v);
     v += dpp_mov<DPP_XOR2>(v);

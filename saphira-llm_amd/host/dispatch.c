@@ -79,6 +79,8 @@ int sllm_kdispatch_select(const char *name) {
 
 const sllm_kernel_row *sllm_kdispatch_installed(void) { return g_installed; }
 
+const char *sllm_kdispatch_installed_name(void) { return g_installed ? g_installed->name : "none"; }
+
 void sllm_kdispatch_reset(void) { g_installed = NULL; }
 
 static const sllm_kernel_row *need_row(const char *fn) {

@@ -110,6 +110,7 @@ def test_dispatch_table_rules(amd):
     assert lib.sllm_kdispatch_row(0).contents.name == b"gfx950"
     lib.sllm_kdispatch_reset()
     assert not lib.sllm_kdispatch_installed()
+    assert lib.sllm_kdispatch_installed_name() == b"none"
     # the gfx950 row cannot open here: selection fails, nothing is installed
     assert lib.sllm_kdispatch_select(b"gfx950") == -60
     assert not lib.sllm_kdispatch_installed()
@@ -131,6 +132,7 @@ def test_dispatch_table_rules(amd):
     # "auto" tries gfx950 (priority 100) first, then the stub
     assert lib.sllm_kdispatch_select(b"auto") == 0
     assert lib.sllm_kdispatch_installed().contents.name == b"test-stub"
+    assert lib.sllm_kdispatch_installed_name() == b"test-stub"
     assert lib.sllm_kdispatch_dot(None, None, 256) == 7
     lib.sllm_kdispatch_gemv(None, 3, 384, None, None)
     assert calls[-2:] == [("dot", 256), ("gemv", 3, 384)]
