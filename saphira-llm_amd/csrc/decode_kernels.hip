@@ -302,14 +302,15 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job &j
 #pragma unroll
     for (int w = 0; w < SLAB_WAVES; ++w) asum += S.red_i[w];
 
-    // (5) the row groups, double-buffered (as the slab kernel)
+    // (5) the row groups, double-buffered (as the slab kernel; the load past
+    // the last group goes to the dead offset)
     int32_t *dots = S.dots + wave_row;
     uint32_t t = 0;
     for (uint32_t pair = 0; pair < TT / 2; ++pair) {
-        slab_load<LPR, CPL>(group_rsrc(t + 1), row_bytes, group_row(t + 1), last_row, bufb);
+        slab_load<LPR, CPL>(group_rsrc(t + 1), row_bytes, group_row(t + 1), last_row, bufb, t + 1 < TT);
         slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
         ++t;
-        slab_load<LPR, CPL>(group_rsrc(t + 1), row_bytes, group_row(t + 1), last_row, bufa);
+        slab_load<LPR, CPL>(group_rsrc(t + 1), row_bytes, group_row(t + 1), last_row, bufa, t + 1 < TT);
         slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufb, S.q, dots + t * G);
         ++t;
     }

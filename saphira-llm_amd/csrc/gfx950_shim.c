@@ -614,8 +614,9 @@ uint32_t sllm_shim_slab_group_rows(int variant) { return variant == 0 ? 4 * 64 /
 /* does a job of this shape take the slab kernel (else the streaming one) */
 static int slab_path(size_t n_rows, size_t k) {
     if (g.force_path == 1 || k > SLAB_MAX_K) return 0;
-    /* the slab kernel addresses a tensor with 32-bit offsets */
-    return (uint64_t) n_rows * (k / 4) + 32 <= UINT32_MAX;
+    /* the slab kernel addresses a tensor with 32-bit offsets, and aims the
+     * loads it must not make at 0xFFFF0000, past every slab tensor */
+    return (uint64_t) n_rows * (k / 4) + 32 <= 0xFFFF0000u;
 }
 
 /* Slabs of a job: about slab_kib KiB of weights each, at least one group

@@ -301,7 +301,7 @@ struct slab_shared {
 // it) leaves the compiler unsure how many loads are outstanding where paths
 // meet, and it then waits for all of them, draining the prefetch. Weights
 // are read through a buffer resource bounded by the tensor's size (the host
-// keeps slab tensors below 4 GiB): a chunk slot past the end of the last row
+// keeps slab tensors at or below 0xFFFF0000 bytes): a chunk slot past the end of the last row
 // reads zeros instead of faulting, so lane slot u is simply the lane's
 // offset plus a constant. A lane whose row lies past the slab re-reads the
 // slab's last row (lines already being fetched); slab_dot zeroes what it
@@ -316,12 +316,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tensor_rsrc(const gemv_job &jo
 
 constexpr int CPOL_NT = 2;      // nontemporal: weights are read once
 
+// A load that must not happen (a prefetch past the slab's last group) goes to
+// this offset. The host keeps every slab tensor at or below it, so the
+// resource's range check returns zeros and no memory is read.
+constexpr uint32_t SLAB_DEAD_OFFSET = 0xFFFF0000u;
+
 template <int LPR, int CPL>
 __device__ __forceinline__ void slab_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t row_bytes, uint32_t base,
-                                          uint32_t last_row, u32x4 (&buf)[CPL]) {
+                                          uint32_t last_row, u32x4 (&buf)[CPL], bool live = true) {
     const int lane = threadIdx.x & 63;
     const uint32_t row = min(base + (uint32_t) (lane / LPR), last_row);
-    const uint32_t off = row * row_bytes + (uint32_t) (lane % LPR) * 16u;
+    const uint32_t off = live ? row * row_bytes + (uint32_t) (lane % LPR) * 16u : SLAB_DEAD_OFFSET;
 #pragma unroll
     for (int u = 0; u < CPL; ++u) {
         buf[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int) (off + (uint32_t) (u * LPR * 16)), 0, CPOL_NT);

@@ -140,17 +140,17 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
     }
 
     // (4) the groups, double-buffered: pairs of groups with the next group
-    // always loaded (the last one again past the end) before the current one
-    // is reduced, then a trailing odd group. The loop has one exit and no
-    // load behind a branch, so every wait names exactly the buffer it needs.
-    // Dots of group t go to S.dots[t*G ..].
+    // always loaded before the current one is reduced, then a trailing odd
+    // group. The load past the last group goes to the dead offset (no memory
+    // read). The loop has one exit and no load behind a branch, so every wait
+    // names exactly the buffer it needs. Dots of group t go to S.dots[t*G ..].
     int32_t *dots = S.dots + wave_row;
     uint32_t t = 0;
     for (uint32_t pair = 0; pair < T / 2; ++pair) {
-        slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufb);
+        slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufb, t + 1 < T);
         slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
         ++t;
-        slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufa);
+        slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufa, t + 1 < T);
         slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufb, S.q, dots + t * G);
         ++t;
     }
