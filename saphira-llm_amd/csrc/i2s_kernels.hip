@@ -674,148 +674,20 @@ __device__ __forceinline__ void gemm_place(uint32_t &bx, uint32_t &by) {
     by = t - bx * gy;
 }
 
-// KG K groups: with KG = 2 the workgroup is eight waves, two groups of four
-// over the same tile; group k takes super-steps k, k + 2, k + 4, ... (two
-// waves on every SIMD, one of each group, so that one's waits are covered by
-// the other's MFMAs), and the groups' int32 sums meet in LDS at the end
-// (exact in any order).
-template <int TM, int TN, int STAGES, int KG = 1>
-__device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by) {
+// The end of a direct-load tile (src/i2s_gemm.c:271-290): the K groups'
+// sums meet in LDS, then post = w_scale / act_scale per token and
+// (float)(dot - sum) * post. The tile goes through LDS (S, at least
+// BM (BN + 4) + 2 BM words) so that every store writes whole rows of the
+// output: a lane's accumulators hold rows 16 apart, the store wants four
+// consecutive ones per lane. The caller has drained its copies into S.
+template <int TM, int TN, int KG>
+__device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &V, uint32_t m, uint32_t t0,
+                                                   uint32_t n0, uint32_t wr, uint32_t kgrp, uint32_t wave_all,
+                                                   float ep_ws, act_t ep_at, i32x4v (&c)[TM][TN]) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
-    constexpr uint32_t A_BYTES = BM * 256u, STAGE = A_BYTES + BN * 64u;
-    constexpr int VM = TM + TN;                     // copies per wave per super-step
-    constexpr int D = STAGES / KG;                  // ring depth in iterations
-    static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
-    static_assert(STAGES % KG == 0 && D >= 2 && (D - 2) * VM < 64, "stages");
-    // the epilogue reuses the ring: the tile as BM rows of EP (BN + 4) words,
-    // then post and sum of the BM tokens
-    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = E_TILE + BM * 8u;
-    constexpr uint32_t S_BYTES = STAGES * STAGE > E_BYTES ? STAGES * STAGE : E_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t S[S_BYTES];
+    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wave = wave_all & 3u, kgrp = wave_all >> 2;   // place in the tile, K group
     const uint32_t g = lane >> 4, li = lane & 15u;
-    const uint32_t t0 = by * BM, n0 = V.tile * BN;
-    const uint32_t nsup = k / 256u, kb = k >> 2;
-    // the epilogue's operands, loaded now so that their latency hides behind
-    // the main loop: w_scale, and token t0 + tid's act for the first BM threads
-    float ep_ws = 0.0f;
-    act_t ep_at = { 1.0f, 0 };
-    if (tid < BM) {
-        ep_ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
-        if (V.act != nullptr) ep_at = V.act[min(t0 + tid, m - 1)];
-    }
-    // copy sources: instruction j of this wave fills LDS granules
-    // (4 j + wave) * 64 + lane of the token and the weight block
-    const int8_t *asrc[TM];
-#pragma unroll
-    for (int j = 0; j < TM; ++j) {
-        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
-        const uint32_t t = p >> 4, gr = (p & 15u) ^ (t & 15u);
-        asrc[j] = V.q + (size_t) min(t0 + t, m - 1) * k + gr * 16u;
-    }
-    const uint8_t *bsrc[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
-        const uint32_t r = p >> 2, ch = (p & 3u) ^ ((r >> 2) & 3u);
-        bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb + ch * 16u;
-    }
-    // super-step s lives in slot s % STAGES; past the end the last one is
-    // copied again (never read)
-    auto issue = [&](uint32_t s) {
-        const uint32_t sc = min(s, nsup - 1);
-        uint8_t *base = S + (s % STAGES) * STAGE;
-#pragma unroll
-        for (int j = 0; j < TM; ++j)
-            __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + sc * 256u),
-                                             LDS_PTR(base + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-            __builtin_amdgcn_global_load_lds((const void *) (bsrc[j] + sc * 64u),
-                                             LDS_PTR(base + A_BYTES + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
-    };
-    uint32_t aoff[4];                               // token 16 tm + li (tm * 4096 added), granule of step f
-#pragma unroll
-    for (int f = 0; f < 4; ++f) aoff[f] = li * 256u + (((8u * (g >> 1) + 2u * (uint32_t) f + (g & 1u)) ^ li) * 16u);
-    const uint32_t wr = wave * (16u * TN);          // this wave's first row in the tile
-    const uint32_t boff = A_BYTES + (wr + li) * 64u + ((g ^ ((li >> 2) & 3u)) * 16u);
-    i32x4v c[TM][TN];
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
-    }
-    // iteration it: group k multiplies super-step KG it + k
-    const uint32_t iters = (nsup + KG - 1) / KG;
-#pragma unroll
-    for (int i = 0; i < D - 1; ++i) issue((uint32_t) (KG * i) + kgrp);
-    for (uint32_t it = 0; it < iters; ++it) {
-        const uint32_t s = KG * it + kgrp;
-        // this iteration's copies done (later ones may stay in flight), then everyone's
-        // (near the end, fewer are in flight: wait for all but the next one)
-        const uint32_t ahead = min(iters - 1u - it, (uint32_t) D - 2u);
-        if (ahead == (uint32_t) D - 2u) wait_vmem<(D - 2) * VM>();
-        else if (ahead == 1) wait_vmem<VM>();
-        else wait_vmem<0>();
-        __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's reads of the stage being refilled done
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        issue(s + (uint32_t) (KG * (D - 1)));
-        __builtin_amdgcn_sched_barrier(0);
-        if (KG > 1 && s >= nsup) continue;          // an odd count: the last iteration is group 0's alone
-        const uint8_t *st = S + (s % STAGES) * STAGE;
-        u32x4 raw[TN];
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) raw[tn] = *reinterpret_cast<const u32x4 *>(st + boff + (uint32_t) tn * 1024u);
-        i32x4v a[2][TM], b[2][TN];
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm) a[0][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[0] + (uint32_t) tm * 4096u);
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-#pragma unroll
-            for (int d = 0; d < 4; ++d) b[0][tn][d] = (int32_t) ((raw[tn][d] >> 6u) & 0x03030303u);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            const int cu = f & 1, nx = cu ^ 1;
-            if (f < 3) {
-#pragma unroll
-                for (int tm = 0; tm < TM; ++tm)
-                    a[nx][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[f + 1] + (uint32_t) tm * 4096u);
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) b[nx][tn][d] = (int32_t) ((raw[tn][d] >> (4u - 2u * (uint32_t) f)) & 0x03030303u);
-                }
-            }
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-#pragma unroll
-                for (int tm = 0; tm < TM; ++tm)
-                    c[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[cu][tm], b[cu][tn], c[tm][tn], 0, 0, 0);
-            }
-            if (f < 3) {
-                // each MFMA, then one of the next step's reads and its share of the unpacking
-                constexpr int VPM = (8 * TN + TM * TN - 1) / (TM * TN);
-#pragma unroll
-                for (int i = 0; i < TM * TN; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (i < TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    wait_vmem<0>();                                 // no copy may land after the workgroup leaves
-
-    // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
-    // token, (float)(dot - sum) * post. The tile goes through LDS so that
-    // every store writes whole rows of the output: a lane's accumulators hold
-    // rows 16 apart, the store wants four consecutive ones per lane.
     __syncthreads();                                // every wave done with the ring
     uint32_t *tile = reinterpret_cast<uint32_t *>(S);
     float *post_s = reinterpret_cast<float *>(S + E_TILE);
@@ -891,6 +763,180 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
     };
     if (V.out_i != nullptr) emit(true, reinterpret_cast<uint32_t *>(V.out_i));
     if (V.out != nullptr) emit(false, reinterpret_cast<uint32_t *>(V.out));
+}
+
+// KG K groups: with KG = 2 the workgroup is eight waves, two groups of four
+// over the same tile; group k takes super-steps k, k + 2, k + 4, ... (two
+// waves on every SIMD, one of each group, so that one's waits are covered by
+// the other's MFMAs), and the groups' int32 sums meet in LDS at the end
+// (exact in any order).
+template <int TM, int TN, int STAGES, int KG = 1>
+__device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by) {
+    constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
+    constexpr uint32_t A_BYTES = BM * 256u, STAGE = A_BYTES + BN * 64u;
+    constexpr int VM = TM + TN;                     // copies per wave per super-step
+    constexpr int D = STAGES / KG;                  // ring depth in iterations
+    static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
+    static_assert(STAGES % KG == 0 && D >= 2 && (D - 2) * VM < 64, "stages");
+    // WL (with K groups): the weights of a whole iteration (KG super-steps,
+    // PB bytes of each row) arrive together, 8 rows x 128 bytes or 4 rows x
+    // 256 bytes per copy instruction, whole cache lines where the row is
+    // line-aligned -- 16 rows x 64 bytes per instruction streams at about
+    // 5.1 TB/s on MI355X against 6.0-6.9 for whole lines. LDS then holds
+    // STAGES token slots, then D weight slots of BN rows x PB bytes (the
+    // same total); chunk c of row r of a weight slot sits at slot c ^ (r % 8).
+    constexpr bool WL = KG >= 2;
+    constexpr uint32_t PB = 64u * KG, CR = 4u * KG, A_REGION = STAGES * A_BYTES, WSLOT = BN * PB;
+    // the epilogue reuses the ring: the tile as BM rows of EP (BN + 4) words,
+    // then post and sum of the BM tokens
+    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = E_TILE + BM * 8u;
+    constexpr uint32_t S_BYTES = STAGES * STAGE > E_BYTES ? STAGES * STAGE : E_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t S[S_BYTES];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wave = wave_all & 3u, kgrp = wave_all >> 2;   // place in the tile, K group
+    const uint32_t g = lane >> 4, li = lane & 15u;
+    const uint32_t t0 = by * BM, n0 = V.tile * BN;
+    const uint32_t nsup = k / 256u, kb = k >> 2;
+    // the epilogue's operands, loaded now so that their latency hides behind
+    // the main loop: w_scale, and token t0 + tid's act for the first BM threads
+    float ep_ws = 0.0f;
+    act_t ep_at = { 1.0f, 0 };
+    if (tid < BM) {
+        ep_ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+        if (V.act != nullptr) ep_at = V.act[min(t0 + tid, m - 1)];
+    }
+    // copy sources: instruction j of this wave fills LDS granules
+    // (4 j + wave) * 64 + lane of the token and the weight block
+    const int8_t *asrc[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
+        const uint32_t t = p >> 4, gr = (p & 15u) ^ (t & 15u);
+        asrc[j] = V.q + (size_t) min(t0 + t, m - 1) * k + gr * 16u;
+    }
+    const uint8_t *bsrc[TN];
+    uint32_t bch[TN];                               // WL: the chunk (of CR) each copy lane fetches
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
+        if (WL) {                                   // K group kgrp copies rows [kgrp BN/KG, (kgrp + 1) BN/KG)
+            const uint32_t r = kgrp * (BN / KG) + p / CR;
+            bch[j] = (p % CR) ^ (r & 7u);
+            bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb;
+        } else {
+            const uint32_t r = p >> 2, ch = (p & 3u) ^ ((r >> 2) & 3u);
+            bch[j] = 0;
+            bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb + ch * 16u;
+        }
+    }
+    const uint32_t iters = (nsup + KG - 1) / KG;
+    // super-step s lives in slot s % STAGES (WL: its tokens; its iteration's
+    // weights in weight slot (s / KG) % D); past the end the last one is
+    // copied again (never read), and a WL chunk past the last super-step
+    // copies the iteration's first super-step's instead
+    auto issue = [&](uint32_t s) {
+        const uint32_t sc = min(s, nsup - 1);
+        uint8_t *base = S + (s % STAGES) * (WL ? A_BYTES : STAGE);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+            __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + sc * 256u),
+                                             LDS_PTR(base + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+        if (WL) {
+            const uint32_t it = min(s / KG, iters - 1);
+            uint8_t *wbase = S + A_REGION + ((s / KG) % D) * WSLOT + kgrp * (BN / KG) * PB;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t ch = KG * it + bch[j] / 4u < nsup ? bch[j] : (bch[j] & 3u);
+                __builtin_amdgcn_global_load_lds((const void *) (bsrc[j] + it * PB + ch * 16u),
+                                                 LDS_PTR(wbase + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                __builtin_amdgcn_global_load_lds((const void *) (bsrc[j] + sc * 64u),
+                                                 LDS_PTR(base + A_BYTES + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+        }
+    };
+    uint32_t aoff[4];                               // token 16 tm + li (tm * 4096 added), granule of step f
+#pragma unroll
+    for (int f = 0; f < 4; ++f) aoff[f] = li * 256u + (((8u * (g >> 1) + 2u * (uint32_t) f + (g & 1u)) ^ li) * 16u);
+    const uint32_t wr = wave * (16u * TN);          // this wave's first row in the tile
+    // this lane's weight chunk: row wr + li (+ 16 tn), chunk g of the super-step
+    const uint32_t boff = WL ? A_REGION + (wr + li) * PB + (((4u * kgrp + g) ^ (li & 7u)) * 16u)
+                             : A_BYTES + (wr + li) * 64u + ((g ^ ((li >> 2) & 3u)) * 16u);
+    constexpr uint32_t BROW16 = WL ? 16u * PB : 1024u;   // 16 rows further
+    i32x4v c[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
+    }
+    // iteration it: group k multiplies super-step KG it + k
+#pragma unroll
+    for (int i = 0; i < D - 1; ++i) issue((uint32_t) (KG * i) + kgrp);
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t s = KG * it + kgrp;
+        // this iteration's copies done (later ones may stay in flight), then everyone's
+        // (near the end, fewer are in flight: wait for all but the next one)
+        const uint32_t ahead = min(iters - 1u - it, (uint32_t) D - 2u);
+        if (ahead == (uint32_t) D - 2u) wait_vmem<(D - 2) * VM>();
+        else if (ahead == 1) wait_vmem<VM>();
+        else wait_vmem<0>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's reads of the stage being refilled done
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(s + (uint32_t) (KG * (D - 1)));
+        __builtin_amdgcn_sched_barrier(0);
+        if (KG > 1 && s >= nsup) continue;          // an odd count: the last iteration is group 0's alone
+        const uint8_t *st = S + (s % STAGES) * (WL ? A_BYTES : STAGE);
+        const uint8_t *sw = WL ? S + (it % D) * WSLOT : st;
+        u32x4 raw[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) raw[tn] = *reinterpret_cast<const u32x4 *>(sw + boff + (uint32_t) tn * BROW16);
+        i32x4v a[2][TM], b[2][TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) a[0][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[0] + (uint32_t) tm * 4096u);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) b[0][tn][d] = (int32_t) ((raw[tn][d] >> 6u) & 0x03030303u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const int cu = f & 1, nx = cu ^ 1;
+            if (f < 3) {
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm)
+                    a[nx][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[f + 1] + (uint32_t) tm * 4096u);
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) b[nx][tn][d] = (int32_t) ((raw[tn][d] >> (4u - 2u * (uint32_t) f)) & 0x03030303u);
+                }
+            }
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm)
+                    c[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[cu][tm], b[cu][tn], c[tm][tn], 0, 0, 0);
+            }
+            if (f < 3) {
+                // each MFMA, then one of the next step's reads and its share of the unpacking
+                constexpr int VPM = (8 * TN + TM * TN - 1) / (TM * TN);
+#pragma unroll
+                for (int i = 0; i < TM * TN; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (i < TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wait_vmem<0>();                                 // no copy may land after the workgroup leaves
+    gemm_tile_epilogue<TM, TN, KG>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_at, c);
 }
 
 // the tile of a three-job launch (gemm_args) or of a plan (gemm_table)
