@@ -218,6 +218,34 @@ __device__ __forceinline__ void chunk_dot(const u32x4 wv, const int8_t *__restri
     }
 }
 
+// The slab kernel's form of chunk_dot: field 0 taken as (w ^ 0x80) & 0xC0
+// in one v_bitop3 -- byte values 64 (code - 2), as signed int8 -128, -64, 0
+// -- instead of a shift and a mask. Its accumulator is then 64 (D0 - 2 A0)
+// for D0 the field's true dot and A0 the sum of the activation elements the
+// field covers, which finish_x adds back once per row. No slot is masked:
+// activation bytes past the row are zero, so whatever the weight bytes of a
+// slot past the row hold, it adds nothing.
+__device__ __forceinline__ void chunk_dot_x(const u32x4 wv, const int8_t *__restrict__ a, dot4acc &acc) {
+    const i32x4 q0 = *reinterpret_cast<const i32x4 *>(a);
+    const i32x4 q1 = *reinterpret_cast<const i32x4 *>(a + 32);
+    const i32x4 q2 = *reinterpret_cast<const i32x4 *>(a + 64);
+    const i32x4 q3 = *reinterpret_cast<const i32x4 *>(a + 96);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        acc.f3 = __builtin_amdgcn_sdot4((int) (wv[d] & 0x03030303u), q3[d], acc.f3, false);
+        acc.f2 = __builtin_amdgcn_sdot4((int) (wv[d] & 0x0C0C0C0Cu), q2[d], acc.f2, false);
+        acc.f1 = __builtin_amdgcn_sdot4((int) (wv[d] & 0x30303030u), q1[d], acc.f1, false);
+        // LUT 0x28: (src0 ^ src1) & src2
+        acc.f0 = __builtin_amdgcn_sdot4((int) __builtin_amdgcn_bitop3_b32(wv[d], 0x80808080u, 0xC0C0C0C0u, 0x28),
+                                        q0[d], acc.f0, false);
+    }
+}
+// one lane's share of a row's dot from chunk_dot_x's accumulators; the row's
+// total is the sum over its lanes plus 2 A0
+__device__ __forceinline__ int finish_x(const dot4acc &acc) {
+    return acc.f3 + (acc.f2 >> 2) + (acc.f1 >> 4) + (acc.f0 >> 6);
+}
+
 __device__ __forceinline__ int finish(const dot4acc &acc) {
     // each accumulator is an exact multiple of its field weight
     return acc.f3 + (acc.f2 >> 2) + (acc.f1 >> 4) + (acc.f0 >> 5);
@@ -294,6 +322,7 @@ struct slab_shared {
     int32_t dots[SLAB_MAX_ROWS];
     float   red_f[SLAB_WAVES];
     int     red_i[SLAB_WAVES];
+    int     red_a[SLAB_WAVES];
 };
 
 // Every load of the slab kernel is unconditional: a skipped load (a branch
@@ -358,6 +387,22 @@ __device__ __forceinline__ void slab_dot(uint32_t chunks, uint32_t row0, uint32_
     }
     const int dot = group_sum<LPR>(finish(acc));      // whole wave active here
     if (valid && sub == 0) dots[lane / LPR] = dot;
+}
+
+// slab_dot over chunk_dot_x: a2 = 2 A0 of the activation row; the LDS row
+// must be zero from K to LPR * CPL * 64
+template <int LPR, int CPL>
+__device__ __forceinline__ void slab_dot_x(uint32_t row0, uint32_t n_rows, const u32x4 (&buf)[CPL],
+                                           const int8_t *q_lds, int32_t a2, int32_t *dots) {
+    const int lane = threadIdx.x & 63, sub = lane % LPR;
+    const uint32_t row = row0 + (uint32_t) (lane / LPR);
+    uint32_t lds_lane = (uint32_t) (sub >> 1) * 128u + (uint32_t) (sub & 1) * 16u;
+    asm volatile("" : "+v"(lds_lane));
+    dot4acc acc = { 0, 0, 0, 0 };
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) chunk_dot_x(buf[u], q_lds + lds_lane + (uint32_t) (u * LPR * 64), acc);
+    const int dot = group_sum<LPR>(finish_x(acc)) + a2;   // whole wave active here
+    if (row < n_rows && sub == 0) dots[lane / LPR] = dot;
 }
 
 

@@ -41,7 +41,7 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
     constexpr uint32_t G = SLAB_WAVES * RPW;
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) tid >> 6);
-    const uint32_t k = job.k, chunks = k >> 6, row_bytes = k >> 2;
+    const uint32_t k = job.k, row_bytes = k >> 2;
     const uint32_t n_rows = job.n_rows, last_row = n_rows - 1;
     const __amdgpu_buffer_rsrc_t rsrc = tensor_rsrc(job);
     // this slab's groups: first .. first + T - 1
@@ -59,7 +59,7 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
     f32x4 xv[XV];
     u32x4 qv[QV];
     float scale = 0.0f;
-    int32_t asum = 0;
+    int32_t asum = 0, a2 = 0;       // a2: twice the sum of the row's field-0 elements (slab_dot_x)
     if (QUANT) {
 #pragma unroll
         for (int u = 0; u < XV; ++u) {
@@ -108,7 +108,7 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
 #pragma unroll
         for (int w = 1; w < SLAB_WAVES; ++w) m = fmaxf(m, S.red_f[w]);
         const float s = m > 0.0f ? 127.0f / m : 0.0f;
-        int ls = 0;
+        int ls = 0, la = 0;
 #pragma unroll
         for (int u = 0; u < XV; ++u) {
             const uint32_t i = 4u * (uint32_t) (tid + u * SLAB_THREADS);
@@ -117,26 +117,49 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
                 const int a = quant_one(v[0] * s), b = quant_one(v[1] * s);
                 const int c = quant_one(v[2] * s), d = quant_one(v[3] * s);
                 ls += a + b + c + d;
+                la += ((i >> 5) & 3u) == 0 ? a + b + c + d : 0;     // field 0 of its block
                 *reinterpret_cast<uint32_t *>(S.q + i) =
                     (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) |
                     ((uint32_t) (c & 0xff) << 16) | ((uint32_t) (d & 0xff) << 24);
+            } else {
+                *reinterpret_cast<uint32_t *>(S.q + i) = 0u;       // the dots' slots past the row
             }
         }
         ls = wave_sum(ls);
-        if (lane == 0) S.red_i[wave] = ls;
+        la = wave_sum(la);
+        if (lane == 0) {
+            S.red_i[wave] = ls;
+            S.red_a[wave] = la;
+        }
         __syncthreads();
-        int t = 0;
+        int t = 0, ta = 0;
 #pragma unroll
-        for (int w = 0; w < SLAB_WAVES; ++w) t += S.red_i[w];
+        for (int w = 0; w < SLAB_WAVES; ++w) {
+            t += S.red_i[w];
+            ta += S.red_a[w];
+        }
         scale = s;
         asum = t;
+        a2 = 2 * ta;
     } else {
+        int la = 0;
 #pragma unroll
         for (int u = 0; u < QV; ++u) {
             const uint32_t i = 16u * (uint32_t) (tid + u * SLAB_THREADS);
-            if (i < k) *reinterpret_cast<u32x4 *>(S.q + i) = qv[u];
+            const u32x4 zero = { 0, 0, 0, 0 };
+            if (i < SLAB_MAX_K) *reinterpret_cast<u32x4 *>(S.q + i) = i < k ? qv[u] : zero;
+            if (i < k && ((i >> 5) & 3u) == 0) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) la = __builtin_amdgcn_sdot4((int) qv[u][d], 0x01010101, la, false);
+            }
         }
+        la = wave_sum(la);
+        if (lane == 0) S.red_a[wave] = la;
         __syncthreads();
+        int ta = 0;
+#pragma unroll
+        for (int w = 0; w < SLAB_WAVES; ++w) ta += S.red_a[w];
+        a2 = 2 * ta;
     }
 
     // (4) the groups, double-buffered: pairs of groups with the next group
@@ -148,13 +171,13 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
     uint32_t t = 0;
     for (uint32_t pair = 0; pair < T / 2; ++pair) {
         slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufb, t + 1 < T);
-        slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
+        slab_dot_x<LPR, CPL>(group_row(t), n_rows, bufa, S.q, a2, dots + t * G);
         ++t;
         slab_load<LPR, CPL>(rsrc, row_bytes, group_row(t + 1), last_row, bufa, t + 1 < T);
-        slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufb, S.q, dots + t * G);
+        slab_dot_x<LPR, CPL>(group_row(t), n_rows, bufb, S.q, a2, dots + t * G);
         ++t;
     }
-    if (T & 1u) slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
+    if (T & 1u) slab_dot_x<LPR, CPL>(group_row(t), n_rows, bufa, S.q, a2, dots + t * G);
     __syncthreads();
 
     // (5) raw dots and the epilogue (src/i2s_gemm.c:271-290): post once per
