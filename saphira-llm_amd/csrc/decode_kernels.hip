@@ -190,6 +190,7 @@ struct dec_shared {
     double  lane_d[4];
     float   red_f[SLAB_WAVES];
     int     red_i[SLAB_WAVES];
+    int     red_a[SLAB_WAVES];
 };
 
 template <int MODE>
@@ -207,7 +208,7 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job &j
     constexpr uint32_t G = SLAB_WAVES * RPW;
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t) tid >> 6);
-    const uint32_t k = job0.k, chunks = k >> 6, row_bytes = k >> 2;
+    const uint32_t k = job0.k, row_bytes = k >> 2;
     const uint32_t n_rows = job0.n_rows, last_row = n_rows - 1;
     const __amdgpu_buffer_rsrc_t rs0 = tensor_rsrc(job0), rs1 = tensor_rsrc(job1);
     const uint32_t n_groups = (n_rows + G - 1) / G;
@@ -282,7 +283,7 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job &j
 #pragma unroll
     for (int w = 1; w < SLAB_WAVES; ++w) m = fmaxf(m, S.red_f[w]);
     const float qs = m > 0.0f ? 127.0f / m : 0.0f;
-    int ls = 0;
+    int ls = 0, la = 0;
 #pragma unroll
     for (int u = 0; u < XV; ++u) {
         const uint32_t i = 4u * (uint32_t) (tid + u * SLAB_THREADS);
@@ -290,17 +291,27 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job &j
             const int a = quant_one(xn[u][0] * qs), b = quant_one(xn[u][1] * qs);
             const int c = quant_one(xn[u][2] * qs), e = quant_one(xn[u][3] * qs);
             ls += a + b + c + e;
+            la += ((i >> 5) & 3u) == 0 ? a + b + c + e : 0;     // field 0 of its block
             *reinterpret_cast<uint32_t *>(S.q + i) =
                 (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) |
                 ((uint32_t) (c & 0xff) << 16) | ((uint32_t) (e & 0xff) << 24);
+        } else {
+            *reinterpret_cast<uint32_t *>(S.q + i) = 0u;       // the dots' slots past the row
         }
     }
     ls = wave_sum(ls);
-    if (lane == 0) S.red_i[wave] = ls;
+    la = wave_sum(la);
+    if (lane == 0) {
+        S.red_i[wave] = ls;
+        S.red_a[wave] = la;
+    }
     __syncthreads();
-    int32_t asum = 0;
+    int32_t asum = 0, a2 = 0;       // a2: twice the sum of the row's field-0 elements (slab_dot_x)
 #pragma unroll
-    for (int w = 0; w < SLAB_WAVES; ++w) asum += S.red_i[w];
+    for (int w = 0; w < SLAB_WAVES; ++w) {
+        asum += S.red_i[w];
+        a2 += 2 * S.red_a[w];
+    }
 
     // (5) the row groups, double-buffered (as the slab kernel; the load past
     // the last group goes to the dead offset)
@@ -308,13 +319,13 @@ __device__ __forceinline__ void dec_block(const dec_stage &st, const gemv_job &j
     uint32_t t = 0;
     for (uint32_t pair = 0; pair < TT / 2; ++pair) {
         slab_load<LPR, CPL>(group_rsrc(t + 1), row_bytes, group_row(t + 1), last_row, bufb, t + 1 < TT);
-        slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
+        slab_dot_x<LPR, CPL>(group_row(t), n_rows, bufa, S.q, a2, dots + t * G);
         ++t;
         slab_load<LPR, CPL>(group_rsrc(t + 1), row_bytes, group_row(t + 1), last_row, bufa, t + 1 < TT);
-        slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufb, S.q, dots + t * G);
+        slab_dot_x<LPR, CPL>(group_row(t), n_rows, bufb, S.q, a2, dots + t * G);
         ++t;
     }
-    if (TT & 1u) slab_dot<LPR, CPL>(chunks, group_row(t), n_rows, bufa, S.q, dots + t * G);
+    if (TT & 1u) slab_dot_x<LPR, CPL>(group_row(t), n_rows, bufa, S.q, a2, dots + t * G);
     __syncthreads();
 
     // (6) epilogue (src/forward.c:653-792): (float)(dot - sum) * (w_scale / act_scale);
