@@ -469,6 +469,8 @@ def measure_gemm(amd, dev):
             yd = by.download(np.float32, m * n_rows).reshape(m, n_rows)
             dd = bi.download(np.int32, m * n_rows).reshape(m, n_rows)
             checks.append((ws[0], n_rows, k, x, m, pick, yd[pick], dd[pick], f"gemm {n_rows}x{k} m={m}"))
+            rot = iter(range(1 << 30))
+            settle(dev, lambda: dev.gemm(bws[next(rot) % GEMM_SETS].vp, n_rows, k, bq.vp, ba.vp, m, by.vp))
             dev.events(2)
             reps = 4 * GEMM_SETS
             dev.record(0)
@@ -532,8 +534,7 @@ def measure_gemm_plan(amd, dev, wl, token_counts=(4, 16, 64)):
                 a = (bau if up else bad).ptr + s * m * 8
                 jobs.append((wl.jobs[3 * s + t_].w, n_rows, n, q, a, outs[3 * s + t_].ptr, None))
         plan = dev.gemm_plan(jobs, m)
-        for _ in range(5):
-            dev.gemm_plan_run(plan)
+        settle(dev, lambda: dev.gemm_plan_run(plan), batch=10)
         dev.sync()
         dev.events(2)
         reps = 20
@@ -586,10 +587,11 @@ def measure_gemm_plan(amd, dev, wl, token_counts=(4, 16, 64)):
     return rows
 
 
-def settle(dev, wl, batch=25, max_batches=80, tol=0.005):
-    """Run the headline launch untimed until its duration is steady: batches
-    of `batch` launches (HIP events on the stream) until three batches in a
-    row agree with the one before within `tol`, or `max_batches` batches.
+def settle(dev, launch, batch=25, max_batches=80, tol=0.005, min_ms=25.0):
+    """Run `launch` (one launch of the timed work) untimed until its duration
+    is steady: batches of `batch` launches (HIP events on the stream) until
+    three batches in a row agree with the one before within `tol` and at
+    least `min_ms` of launches have run, or `max_batches` batches.
     From idle clocks the launch starts near 65 us, rises to about 76 us and
     only then comes down to its steady 64 us, about 375 launches (25 ms) in;
     the W warm-up steps alone (5 in the driver's runs) stop inside that ramp.
@@ -600,13 +602,13 @@ def settle(dev, wl, batch=25, max_batches=80, tol=0.005):
     for _ in range(max_batches):
         dev.record(0)
         for _ in range(batch):
-            wl.step()
+            launch()
         dev.record(1)
         dev.sync()
         hist.append(dev.elapsed(0, 1) * 1e3 / batch)
         if len(hist) > 1 and abs(hist[-1] - hist[-2]) <= tol * hist[-1]:
             calm += 1
-            if calm == 3:
+            if calm >= 3 and sum(hist) * batch / 1e3 >= min_ms:
                 break
         else:
             calm = 0
@@ -950,7 +952,7 @@ def main():
     # steady clocks first (the launch's own ramp from idle), then the W
     # warm-up steps; the copy / read calibration runs after the timed steps:
     # its 86 GB of copies leave the launch about 4 % slower for some 100 ms
-    st = settle(dev, wl)
+    st = settle(dev, wl.step)
     log(f"settled after {st['launches']} launches: {st['first_batch_us']} us per launch at first, "
         f"{st['max_batch_us']} at most, {st['last_batch_us']} at the end")
     for _ in range(args.warmup):
