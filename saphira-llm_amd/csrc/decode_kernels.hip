@@ -1022,9 +1022,9 @@ struct dec_lm {
 static_assert(sizeof(dec_lm) == 72, "dec_lm must match decode.c");
 
 constexpr int LM_THREADS = 256;
-constexpr uint32_t LM_ROWS = 64;        // rows per pass: four lanes per row
+constexpr uint32_t LM_ROWS = 32;        // rows per pass: eight lanes per row
 constexpr uint32_t LM_MAX_E = 8192;
-constexpr int LM_UNROLL = 8;            // 32-element steps per load batch
+constexpr int LM_UNROLL = 8;            // 64-element step pairs per load batch
 
 // The argmax key of one logit: ordered like the float, -0 tied with +0, the
 // lower row winning ties; NaN (never greater than anything) is 0.
@@ -1035,11 +1035,18 @@ __device__ __forceinline__ uint64_t argmax_key(float s, uint32_t row) {
     return ((uint64_t) ord << 32) | (uint64_t) (0xffffffffu - row);
 }
 
-// Row . xn as src/ops.c:106-154 orders it: lane j of a row's four holds
-// acc[j][0..7], element 32i + 8j + l going into acc[j][l] by FMA; then
-// acc0 += acc2, acc1 += acc3, acc0 += acc1; t_l = acc0[l] + acc0[l+4];
-// (t0 + t1) + (t2 + t3). n_embd % 32 == 0, so there is no scalar tail.
-// Passes of 64 rows: workgroup w takes pass w first, then passes handed out
+// Row . xn as src/ops.c:106-154 orders it: accumulator j (0..3) holds
+// acc[j][0..7], element 32i + 8j + l going into acc[j][l] by FMA, i in
+// order; then acc0 += acc2, acc1 += acc3, acc0 += acc1; t_l = acc0[l] +
+// acc0[l+4]; (t0 + t1) + (t2 + t3). n_embd % 32 == 0, so there is no scalar
+// tail. Eight lanes per row load its elements 64i' .. 64i' + 63 (steps 2i'
+// and 2i' + 1): one load instruction is whole 128-byte runs of eight rows
+// (sixteen rows x 64 bytes streams near 5 TB/s on MI355X against 6.9 for
+// whole lines). Lane j < 4 holds accumulator j and takes step 2i''s eight
+// elements from its own load and step 2i' + 1's from lane j + 4 (a DPP
+// row shift), so each accumulator still sees its steps in order; lanes 4..7
+// only load.
+// Passes of 32 rows: workgroup w takes pass w first, then passes handed out
 // in order by an atomic counter (the step record's lm_next, which the argmax
 // kernel and the host reset for every token), so that workgroups that stream
 // faster take more passes. Each lane streams its rows in batches of eight
@@ -1057,7 +1064,7 @@ sllm_k_dec_lm_head(dec_lm L) {
     __shared__ uint64_t red_k[LM_THREADS / 64];
     __shared__ uint32_t s_next;
     const uint32_t e = L.n_embd, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t j = lane % 4, steps = e / 32, nb = (steps + LM_UNROLL - 1) / LM_UNROLL;
+    const uint32_t j = lane % 8, steps = e / 32, pairs = (steps + 1) / 2, nb = (pairs + LM_UNROLL - 1) / LM_UNROLL;
     const uint32_t n_pass = (L.n_vocab + LM_ROWS - 1) / LM_ROWS;
     uint32_t *next_ctr = &L.step->lm_next;
 
@@ -1071,10 +1078,15 @@ sllm_k_dec_lm_head(dec_lm L) {
         wv[u] = *G_CAST(const f32x4, L.norm_w + i);
     }
     auto load = [&](uint32_t pass, uint32_t b, u32x4 (&h)[LM_UNROLL]) {
-        const uint32_t row = min(pass * LM_ROWS + wave * 16 + lane / 4, L.n_vocab - 1);
-        const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) row * e) + j;
+        const uint32_t row = min(pass * LM_ROWS + wave * 8 + lane / 8, L.n_vocab - 1);
+        const GLOBAL u32x4 *w = G_CAST(const u32x4, L.embd + (size_t) row * e);
 #pragma unroll
-        for (int u = 0; u < LM_UNROLL; ++u) h[u] = __builtin_nontemporal_load(w + 4 * min(b * LM_UNROLL + u, steps - 1));
+        for (int u = 0; u < LM_UNROLL; ++u) {
+            const uint32_t pr = min(b * LM_UNROLL + u, pairs - 1);
+            // an odd step past the row (n_embd % 64 == 32) reads the even one again
+            const uint32_t jj = 2 * pr + j / 4 < steps ? j : j % 4;
+            h[u] = __builtin_nontemporal_load(w + 8 * pr + jj);
+        }
     };
     u32x4 ha[LM_UNROLL], hb[LM_UNROLL];
     uint32_t p = blockIdx.x;
@@ -1119,12 +1131,16 @@ sllm_k_dec_lm_head(dec_lm L) {
     auto consume = [&](uint32_t pass, uint32_t b, const u32x4 (&h)[LM_UNROLL]) {
 #pragma unroll
         for (int u = 0; u < LM_UNROLL; ++u) {
-            const uint32_t step = b * LM_UNROLL + (uint32_t) u;
-            if (step < steps) {
+            const uint32_t pr = b * LM_UNROLL + (uint32_t) u;
+            if (pr < pairs) {                               // uniform
                 const f32x8 hf = __builtin_convertvector(__builtin_bit_cast(f16x8, h[u]), f32x8);
-                const float *x = xn + 32 * step + 8 * j;
+                const float *x = xn + 64 * pr + 8 * (j % 4);
 #pragma unroll
                 for (int l = 0; l < 8; ++l) acc[l] = fmaf(hf[l], x[l], acc[l]);
+                if (2 * pr + 1 < steps) {                   // uniform
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) acc[l] = fmaf(dpp_mov_f<DPP_ROW_SHL4>(hf[l]), x[32 + l], acc[l]);
+                }
             }
         }
         if (b == nb - 1) {                                // the row is complete
@@ -1135,7 +1151,7 @@ sllm_k_dec_lm_head(dec_lm L) {
             for (int l = 0; l < 8; ++l) r[l] = r[l] + dpp_mov_f<DPP_XOR1>(r[l]);      // acc0 += acc1
             const float t0 = r[0] + r[4], t1 = r[1] + r[5], t2 = r[2] + r[6], t3 = r[3] + r[7];
             const float sdot = (t0 + t1) + (t2 + t3);
-            const uint32_t row = pass * LM_ROWS + wave * 16 + lane / 4;
+            const uint32_t row = pass * LM_ROWS + wave * 8 + lane / 8;
             if (j == 0 && row < L.n_vocab) {
                 G_CAST(float, L.logits)[row] = sdot;
                 const uint64_t key = argmax_key(sdot, row);

@@ -44,7 +44,8 @@ struct act_t {          // layout of sllm_i2s_act (include/saphira_llm/i2s_gemm.
 // mirror: every lane of a row then holds its row's total), and the four row
 // totals are read with v_readlane. No LDS round trip, unlike a ds_bpermute
 // per step. Every lane of the wave must be active.
-enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140,
+             DPP_ROW_SHL4 = 0x104 };   // row_shl:4: lane i takes lane i + 4 of its row of 16
 
 template <int CTRL>
 __device__ __forceinline__ int dpp_mov(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
