@@ -935,6 +935,9 @@ def main():
     ap.add_argument("--inflight", type=int, default=None,
                     help="decode leg: tokens the device greedy loop keeps enqueued ahead of the host "
                          "(default: the library's)")
+    ap.add_argument("--sustain", type=float, default=0.0,
+                    help="after the timed steps, keep the headline launch running this many seconds in "
+                         "batches of 2000 and report each batch's mean (a sustained-clock check; 0: off)")
     ap.add_argument("--legs", default="cfg0,dropin,block,decode,prefill,gemm",
                     help="comma-separated legs to run beside the headline GEMV (cfg0, dropin, block, decode, "
                          "prefill, gemm); for profiling one leg")
@@ -975,6 +978,20 @@ def main():
     achieved = wl.gemv_bytes / (gemv_avg * 1e-3) / 1e9
     log(f"step {ms_per_step * 1e3:.1f} us wall, slab GEMV {gemv_avg * 1e3:.1f} us per launch "
         f"(events on the stream), {achieved:.0f} GB/s")
+    sustained = None
+    if args.sustain > 0:
+        batches, t_end = [], time.perf_counter() + args.sustain
+        while time.perf_counter() < t_end:
+            dev.record(0)
+            for _ in range(2000):
+                wl.step()
+            dev.record(1)
+            dev.sync()
+            batches.append(round(dev.elapsed(0, 1) / 2000 * 1e3, 2))
+        sustained = {"batch_launches": 2000, "batch_us": batches, "mean_us": round(sum(batches) / len(batches), 2),
+                     "GBps_at_mean": round(wl.gemv_bytes / (sum(batches) / len(batches) * 1e-6) / 1e9, 1)}
+        log(f"sustained {args.sustain:.0f} s: {len(batches)} batches of 2000 launches, "
+            f"{min(batches)}..{max(batches)} us per launch, mean {sustained['mean_us']}")
 
     traffic, traffic_note = profiled_traffic()
 
@@ -1030,6 +1047,7 @@ def main():
             "avg_launch_us": round(gemv_avg * 1e3, 2), "bytes_per_launch": wl.gemv_bytes,
         },
         "settle": st,
+        "sustained": sustained,
         "calibration": calib,
         "cfg0": cfg0,
         "dropin": dropin,
