@@ -1277,61 +1277,69 @@ constexpr int CLM_TOK = 4;              // tokens per workgroup
 // silu(gate) * up as src/forward.c:776-778), kept in v_out if asked; RMSNorm
 // (src/ops.c:254-322) with the same mean as the decode step's; then either
 // the normalised row (xn_out) or its quantisation (src/i2s_gemm.c:45-83).
-extern "C" __global__ void __launch_bounds__(CHK_THREADS)
-sllm_k_chk_prep(chk_prep P) {
-    __shared__ __attribute__((aligned(16))) float xs[CHK_MAX_K];
-    __shared__ double red_d[CHK_THREADS / 64], lane_d[4];
-    __shared__ float red_f[CHK_THREADS / 64];
-    __shared__ int red_i[CHK_THREADS / 64];
+// One straight path per input mode and width (CU float4 per thread): every
+// input load is unconditional (addresses clamped inside the row) and goes
+// out before the first is used, so the loads overlap instead of each waiting
+// behind the last one's stores.
+template <uint32_t MODE, int CU>
+__device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, double *red_d, double *lane_d,
+                                              float *red_f, int *red_i) {
     const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = P.k;
     const size_t row = (size_t) t * k;
-    const int32_t token = P.mode == IN_EMBED ? P.tokens[t] : 0;
-    double part = 0.0;
-    // the norm weights of this thread's elements, loaded beside the vector
-    // rather than after the mean (CHK_MAX_K / 4 / CHK_THREADS float4 at most)
-    f32x4 wv[CHK_MAX_K / 4 / CHK_THREADS];
+    const int32_t token = MODE == IN_EMBED ? P.tokens[t] : 0;
+    f32x4 va[CU], vb[CU], wv[CU];
+    u32x2 ha[CU];
 #pragma unroll
-    for (int u = 0; u < (int) (CHK_MAX_K / 4 / CHK_THREADS); ++u) {
-        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
-        wv[u] = i < k ? *G_CAST(const f32x4, P.norm_w + i) : (f32x4) { 0.0f, 0.0f, 0.0f, 0.0f };
-    }
-    for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
-        f32x4 v;
-        if (P.mode == IN_EMBED) {
-            const u32x2 h = *G_CAST(const u32x2, (const uint16_t *) P.a + (size_t) token * k + i);
-            v = (f32x4) { embd_f32(h[0] & 0xffffu), embd_f32(h[0] >> 16), embd_f32(h[1] & 0xffffu),
-                          embd_f32(h[1] >> 16) };
+    for (int u = 0; u < CU; ++u) {
+        const uint32_t i = min(4 * tid + 4 * CHK_THREADS * (uint32_t) u, k - 4);
+        if (MODE == IN_EMBED) {
+            ha[u] = *G_CAST(const u32x2, (const uint16_t *) P.a + (size_t) token * k + i);
         } else {
-            v = *G_CAST(const f32x4, (const float *) P.a + row + i);
-            if (P.mode == IN_RESID) {
-                v = v + *G_CAST(const f32x4, P.b + row + i);
-            } else if (P.mode == IN_SILU) {
-                const f32x4 u = *G_CAST(const f32x4, P.b + row + i);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) v[c] = silu(v[c]) * u[c];
-            }
+            va[u] = *G_CAST(const f32x4, (const float *) P.a + row + i);
+            if (MODE != IN_PLAIN) vb[u] = *G_CAST(const f32x4, P.b + row + i);
         }
-        *reinterpret_cast<f32x4 *>(xs + i) = v;
-        if (P.v_out != nullptr) *G_CAST(f32x4, P.v_out + row + i) = v;
+        // the norm weights beside the vector rather than after the mean
+        wv[u] = *G_CAST(const f32x4, P.norm_w + i);
+    }
+    double part = 0.0;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) part += (double) (v[c] * v[c]);
+    for (int u = 0; u < CU; ++u) {
+        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        if (i < k) {
+            f32x4 v;
+            if (MODE == IN_EMBED) {
+                v = (f32x4) { embd_f32(ha[u][0] & 0xffffu), embd_f32(ha[u][0] >> 16), embd_f32(ha[u][1] & 0xffffu),
+                              embd_f32(ha[u][1] >> 16) };
+            } else if (MODE == IN_RESID) {
+                v = va[u] + vb[u];
+            } else if (MODE == IN_SILU) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = silu(va[u][c]) * vb[u][c];
+            } else {
+                v = va[u];
+            }
+            *reinterpret_cast<f32x4 *>(xs + i) = v;
+            if (P.v_out != nullptr) *G_CAST(f32x4, P.v_out + row + i) = v;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part += (double) (v[c] * v[c]);
+        }
     }
     const float mean = rms_mean(part, k, red_d, lane_d, [&](uint32_t j) { return xs[j]; });
     const float scale = 1.0f / sqrtf(mean + P.eps);
     float m = 0.0f;
 #pragma unroll
-    for (int u = 0; u < (int) (CHK_MAX_K / 4 / CHK_THREADS); ++u) {
+    for (int u = 0; u < CU; ++u) {
         const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
-        if (i >= k) break;
-        f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
-        const f32x4 w = wv[u];
+        if (i < k) {
+            f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            v[c] = (scale * v[c]) * w[c];
-            m = fmaxf(m, fabsf(v[c]));
+            for (int c = 0; c < 4; ++c) {
+                v[c] = (scale * v[c]) * wv[u][c];
+                m = fmaxf(m, fabsf(v[c]));
+            }
+            *reinterpret_cast<f32x4 *>(xs + i) = v;
+            if (P.xn_out != nullptr) *G_CAST(f32x4, P.xn_out + row + i) = v;
         }
-        *reinterpret_cast<f32x4 *>(xs + i) = v;
-        if (P.xn_out != nullptr) *G_CAST(f32x4, P.xn_out + row + i) = v;
     }
     if (P.q_out == nullptr) return;                  // uniform
     m = wave_max(m);
@@ -1342,14 +1350,18 @@ sllm_k_chk_prep(chk_prep P) {
     for (int w = 1; w < CHK_THREADS / 64; ++w) m = fmaxf(m, red_f[w]);
     const float qs = m > 0.0f ? 127.0f / m : 0.0f;
     int ls = 0;
-    for (uint32_t i = 4 * tid; i < k; i += 4 * CHK_THREADS) {
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
-        const int a = quant_one(v[0] * qs), b = quant_one(v[1] * qs);
-        const int c = quant_one(v[2] * qs), e = quant_one(v[3] * qs);
-        ls += a + b + c + e;
-        *G_CAST(uint32_t, P.q_out + row + i) =
-            (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) | ((uint32_t) (c & 0xff) << 16) |
-            ((uint32_t) (e & 0xff) << 24);
+#pragma unroll
+    for (int u = 0; u < CU; ++u) {
+        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        if (i < k) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
+            const int a = quant_one(v[0] * qs), b = quant_one(v[1] * qs);
+            const int c = quant_one(v[2] * qs), e = quant_one(v[3] * qs);
+            ls += a + b + c + e;
+            *G_CAST(uint32_t, P.q_out + row + i) =
+                (uint32_t) (a & 0xff) | ((uint32_t) (b & 0xff) << 8) | ((uint32_t) (c & 0xff) << 16) |
+                ((uint32_t) (e & 0xff) << 24);
+        }
     }
     ls = wave_sum(ls);
     if (lane == 0) red_i[wave] = ls;
@@ -1361,6 +1373,27 @@ sllm_k_chk_prep(chk_prep P) {
         G_CAST(float, P.act_out + t)[0] = qs;
         G_CAST(int32_t, P.act_out + t)[1] = asum;
     }
+}
+
+template <int CU>
+__device__ __forceinline__ void chk_prep_width(const chk_prep &P, float *xs, double *red_d, double *lane_d,
+                                               float *red_f, int *red_i) {
+    switch (P.mode) {
+    case IN_EMBED: chk_prep_body<IN_EMBED, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
+    case IN_RESID: chk_prep_body<IN_RESID, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
+    case IN_SILU:  chk_prep_body<IN_SILU, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
+    default:       chk_prep_body<IN_PLAIN, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(CHK_THREADS)
+sllm_k_chk_prep(chk_prep P) {
+    __shared__ __attribute__((aligned(16))) float xs[CHK_MAX_K];
+    __shared__ double red_d[CHK_THREADS / 64], lane_d[4];
+    __shared__ float red_f[CHK_THREADS / 64];
+    __shared__ int red_i[CHK_THREADS / 64];
+    if (P.k <= 4 * CHK_THREADS * 3) chk_prep_width<3>(P, xs, red_d, lane_d, red_f, red_i);
+    else chk_prep_width<(int) (CHK_MAX_K / 4 / CHK_THREADS)>(P, xs, red_d, lane_d, red_f, red_i);
 }
 
 // Workgroup t: token t's key roped at its position (NeoX, src/ops.c:467-549)
