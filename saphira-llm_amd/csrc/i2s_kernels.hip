@@ -1190,9 +1190,9 @@ sllm_k_gemm_dk2x2(gemm_args G) { gemm_dl_block<2, 2, 4, 2>(G); }
 // of fewer workgroups than CUs (a lone tensor against a few tokens), each
 // group walks a quarter of the super-steps
 extern "C" __global__ void __launch_bounds__(1024)
-sllm_k_gemm_dq1x1(gemm_args G) { gemm_dl_block<1, 1, 8, 4>(G); }
+sllm_k_gemm_dq1x1(gemm_args G) { gemm_dl_block<1, 1, 16, 4>(G); }
 extern "C" __global__ void __launch_bounds__(1024)
-sllm_k_gemm_dq2x1(gemm_args G) { gemm_dl_block<2, 1, 8, 4>(G); }
+sllm_k_gemm_dq2x1(gemm_args G) { gemm_dl_block<2, 1, 12, 4>(G); }
 
 // the same tiles over a plan's table of tensors
 extern "C" __global__ void __launch_bounds__(256)
