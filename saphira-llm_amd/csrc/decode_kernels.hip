@@ -820,8 +820,6 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                             if (s + (uint32_t) i < npast) part += (double) v[g][i];
                         }
                     }
-                    *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[g][0], v[g][1], v[g][2], v[g][3] };
-                    *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[g][4], v[g][5], v[g][6], v[g][7] };
                 }
             }
         } else {
@@ -875,12 +873,25 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
             }
             inv = lane_f(inv, 0);
         }
-        // p of the first round, in place
-        const uint32_t n0 = min(npast, PV_RPOS);
-        for (uint32_t i = 4 * lane; i < n0; i += 256) {
-            f32x4 e4 = *reinterpret_cast<const f32x4 *>(ph + i);
-            e4[0] = e4[0] * inv; e4[1] = e4[1] * inv; e4[2] = e4[2] * inv; e4[3] = e4[3] * inv;
-            *reinterpret_cast<f32x4 *>(ph + i) = e4;
+        // p of the first round: one round, straight from the e still in
+        // registers; else in place over the e written to LDS
+        if (one_round) {
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                const uint32_t s = 512u * (uint32_t) g + 8 * lane;
+                if (s < npast) {
+                    const float (&v)[8] = sv[g];
+                    *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv };
+                    *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv };
+                }
+            }
+        } else {
+            const uint32_t n0 = min(npast, PV_RPOS);
+            for (uint32_t i = 4 * lane; i < n0; i += 256) {
+                f32x4 e4 = *reinterpret_cast<const f32x4 *>(ph + i);
+                e4[0] = e4[0] * inv; e4[1] = e4[1] * inv; e4[2] = e4[2] * inv; e4[3] = e4[3] * inv;
+                *reinterpret_cast<f32x4 *>(ph + i) = e4;
+            }
         }
         if (lane == 0) {
             stat_m[wave] = m;
