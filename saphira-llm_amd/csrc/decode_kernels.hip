@@ -64,7 +64,11 @@ __device__ __forceinline__ float embd_f32(uint32_t h) {
 
 // ggml_v_expf, one lane (src/ops.c:342-379): the lane's value does not depend
 // on its neighbours, and the vector code's all-in-range shortcut returns what
-// the blend gives such a lane.
+// the blend gives such a lane. NONPOS: x is never above zero (a softmax's
+// x - max; NaN allowed), so n <= 0 always holds where it matters and the
+// select of g folds to a constant -- the same bits for every x with the sign
+// bit set and for NaN (tests/test_expf_nonpos.py compares the two forms).
+template <bool NONPOS = false>
 __device__ __forceinline__ float ggml_v_expf(float x) {
     const float r = 0x1.8p23f;
     const float z = fmaf(x, 0x1.715476p+0f, r);
@@ -77,7 +81,7 @@ __device__ __forceinline__ float ggml_v_expf(float x) {
                               fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
                          u, 0x1.ffffecp-1f * b);
     // the three results, then a select: no branch per element
-    const uint32_t g = n <= 0.0f ? 0x82000000u : 0u;
+    const uint32_t g = (NONPOS || n <= 0.0f) ? 0x82000000u : 0u;
     const float s1 = __uint_as_float(g + 0x7f000000u);
     const float s2 = __uint_as_float(e - g);
     const float in_range = fmaf(j, k, k), scaled = fmaf(s2, j, s2) * s1, extreme = s1 * s1;
@@ -710,7 +714,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
     auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
         if (s < nt) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
@@ -810,7 +814,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 if (s < npast) {
                     if (s < nt) {
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) v[g][i] = ggml_v_expf(v[g][i] - m);
+                        for (int i = 0; i < 8; ++i) v[g][i] = ggml_v_expf<true>(v[g][i] - m);
                     }
                     if (s + 8 <= npast) {
                         part += group_sum(v[g]);
@@ -840,7 +844,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                 if (npast > nt && nt - b0 < 512u) tail8(v, (nt - b0) / 8u, m);   // uniform
                 if (s < nt) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+                    for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
                 }
                 if (s + 8 <= npast) {
                     part += group_sum(v);
@@ -940,7 +944,7 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                     if (npast > nt && nt - (base + i0) < 512u) tail8(v, (nt - base - i0) / 8u, m);   // uniform
                     if (base + i < nt) {
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) v[e] = ggml_v_expf(v[e] - m);
+                        for (int e = 0; e < 8; ++e) v[e] = ggml_v_expf<true>(v[e] - m);
                     }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
@@ -1559,7 +1563,7 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
     auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
         if (s < nt) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
@@ -1569,7 +1573,7 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
     auto ggml8 = [&](float (&v)[8], uint32_t s, float m) {
         if (s < nt) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf(v[i] - m);
+            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
         }
     };
     // e of the tail group (npast - nt <= 7 terms, the C library's expf),
