@@ -697,12 +697,15 @@ __device__ __forceinline__ void gemm_place(uint32_t &bx, uint32_t &by) {
     by = t - bx * gy;
 }
 
-// The end of a direct-load tile (src/i2s_gemm.c:271-290): the K groups'
-// sums meet in LDS, then post = w_scale / act_scale per token and
-// (float)(dot - sum) * post. The tile goes through LDS (S, at least
-// BM (BN + 4) + 2 BM words) so that every store writes whole rows of the
-// output: a lane's accumulators hold rows 16 apart, the store wants four
-// consecutive ones per lane. The caller has drained its copies into S.
+// The end of a direct-load tile (src/i2s_gemm.c:271-290): post = w_scale /
+// act_scale per token, then (float)(dot - sum) * post. Each K group writes
+// its int32 sums to a tile of its own in LDS (S, at least KG BM (BN + 4) +
+// 2 BM words) and the stores add the KG tiles up (exact in any order), so
+// one barrier separates the writes from the stores and every wave takes
+// part in both. The tile goes through LDS so that every store writes whole
+// rows of the output: a lane's accumulators hold rows 16 apart, the store
+// wants four consecutive ones per lane. The caller has drained its copies
+// into S.
 template <int TM, int TN, int KG>
 __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &V, uint32_t m, uint32_t t0,
                                                    uint32_t n0, uint32_t wr, uint32_t kgrp, uint32_t wave_all,
@@ -712,34 +715,17 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t g = lane >> 4, li = lane & 15u;
     __syncthreads();                                // every wave done with the ring
-    uint32_t *tile = reinterpret_cast<uint32_t *>(S);
-    float *post_s = reinterpret_cast<float *>(S + E_TILE);
-    int32_t *sum_s = reinterpret_cast<int32_t *>(S + E_TILE + BM * 4u);
-    auto tile_at = [&](int tm, int tn, int r) -> uint32_t & {
-        return tile[(16u * (uint32_t) tm + 4u * g + (uint32_t) r) * EP + wr + 16u * (uint32_t) tn + li];
-    };
-    // the other groups' sums into group 0's, one group at a time
+    uint32_t *mine = reinterpret_cast<uint32_t *>(S + kgrp * E_TILE);
+    float *post_s = reinterpret_cast<float *>(S + KG * E_TILE);
+    int32_t *sum_s = reinterpret_cast<int32_t *>(S + KG * E_TILE + BM * 4u);
 #pragma unroll
-    for (uint32_t k2 = 1; k2 < (uint32_t) KG; ++k2) {
-        if (kgrp == k2) {
+    for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
+        for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) tile_at(tm, tn, r) = (uint32_t) c[tm][tn][r];
-        }
-        __syncthreads();
-        if (kgrp == 0) {
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) c[tm][tn][r] += (int32_t) tile_at(tm, tn, r);
-        }
-        __syncthreads();
-    }
+            for (int r = 0; r < 4; ++r)
+                mine[(16u * (uint32_t) tm + 4u * g + (uint32_t) r) * EP + wr + 16u * (uint32_t) tn + li] =
+                    (uint32_t) c[tm][tn][r];
     if (tid < BM) {
         post_s[tid] = ep_ws / ep_at.scale;
         sum_s[tid] = ep_at.sum;
@@ -748,44 +734,37 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
     constexpr uint32_t LPT = BN / 4u;               // lanes per tile row in the stores
     constexpr uint32_t RPS = 64u / LPT;             // tile rows per store instruction
     const uint32_t srow = lane / LPT, scol = 4u * (lane % LPT);
-    auto emit = [&](bool raw, uint32_t *dst) {
-        if (kgrp == 0) {
+    const bool vec_i = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out_i & 15u) == 0;
+    const bool vec_f = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out & 15u) == 0;
+    // streaming stores: written through as the tiles finish rather than left
+    // dirty in L2 for the end-of-kernel writeback
+    auto put = [&](bool vec, GLOBAL uint32_t *o, uint32_t n, u32x4 v) {
+        if (vec) {
+            __builtin_nontemporal_store(v, reinterpret_cast<GLOBAL u32x4 *>(o));
+        } else {
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t row = 16u * (uint32_t) tm + 4u * g + (uint32_t) r;
-                    const float post = post_s[row];
-                    const int32_t sum = sum_s[row];
-#pragma unroll
-                    for (int tn = 0; tn < TN; ++tn) {
-                        const int32_t d = c[tm][tn][r];
-                        tile_at(tm, tn, r) = raw ? (uint32_t) d : __float_as_uint((float) (d - sum) * post);
-                    }
-                }
-            }
+            for (uint32_t e = 0; e < 4u; ++e) if (n + e < V.n_rows) __builtin_nontemporal_store(v[e], o + e);
         }
-        __syncthreads();
-        const bool vec = (V.n_rows & 3u) == 0 && ((uintptr_t) dst & 15u) == 0;
-        for (uint32_t row0 = wave_all * RPS; row0 < BM; row0 += 4u * KG * RPS) {
-            const uint32_t row = row0 + srow, t = t0 + row, n = n0 + scol;
-            if (t < m && n < V.n_rows) {
-                const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + row * EP + scol);
-                GLOBAL uint32_t *o = G_CAST(uint32_t, dst) + (size_t) t * V.n_rows + n;
-                // streaming stores: written through as the tiles finish
-                // rather than left dirty in L2 for the end-of-kernel writeback
-                if (vec) {
-                    __builtin_nontemporal_store(v, reinterpret_cast<GLOBAL u32x4 *>(o));
-                } else {
-#pragma unroll
-                    for (uint32_t e = 0; e < 4u; ++e) if (n + e < V.n_rows) __builtin_nontemporal_store(v[e], o + e);
-                }
-            }
-        }
-        __syncthreads();                            // before the tile is written again
     };
-    if (V.out_i != nullptr) emit(true, reinterpret_cast<uint32_t *>(V.out_i));
-    if (V.out != nullptr) emit(false, reinterpret_cast<uint32_t *>(V.out));
+    for (uint32_t row0 = wave_all * RPS; row0 < BM; row0 += 4u * KG * RPS) {
+        const uint32_t row = row0 + srow, t = t0 + row, n = n0 + scol;
+        if (t < m && n < V.n_rows) {
+            i32x4v d = *reinterpret_cast<const i32x4v *>(S + (row * EP + scol) * 4u);
+#pragma unroll
+            for (uint32_t k2 = 1; k2 < (uint32_t) KG; ++k2)
+                d += *reinterpret_cast<const i32x4v *>(S + k2 * E_TILE + (row * EP + scol) * 4u);
+            const size_t at = (size_t) t * V.n_rows + n;
+            if (V.out_i != nullptr) put(vec_i, G_CAST(uint32_t, V.out_i) + at, n, (u32x4) d);
+            if (V.out != nullptr) {
+                const float post = post_s[row];
+                const int32_t sum = sum_s[row];
+                u32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = __float_as_uint((float) (d[e] - sum) * post);
+                put(vec_f, G_CAST(uint32_t, V.out) + at, n, v);
+            }
+        }
+    }
 }
 
 // KG K groups: with KG = 2 the workgroup is eight waves, two groups of four
@@ -810,9 +789,9 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
     // same total); chunk c of row r of a weight slot sits at slot c ^ (r % 8).
     constexpr bool WL = KG >= 2;
     constexpr uint32_t PB = 64u * KG, CR = 4u * KG, A_REGION = STAGES * A_BYTES, WSLOT = BN * PB;
-    // the epilogue reuses the ring: the tile as BM rows of EP (BN + 4) words,
+    // the epilogue reuses the ring: KG tiles of BM rows of EP (BN + 4) words,
     // then post and sum of the BM tokens
-    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = E_TILE + BM * 8u;
+    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = KG * E_TILE + BM * 8u;
     constexpr uint32_t S_BYTES = STAGES * STAGE > E_BYTES ? STAGES * STAGE : E_BYTES;
     __shared__ __attribute__((aligned(1024))) uint8_t S[S_BYTES];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
