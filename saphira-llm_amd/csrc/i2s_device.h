@@ -291,6 +291,17 @@ __device__ __forceinline__ uint32_t xcd_slot(uint32_t n_wg) {
     return (blockIdx.x & 7u) * (n_wg >> 3) + (blockIdx.x >> 3);
 }
 
+// 0 in a VGPR the compiler cannot see through. A load indexed by it is a
+// vector load (counted by vmcnt) even where its address is uniform: a
+// uniform load of read-only memory would otherwise be a scalar load, and
+// the next wait on any scalar load (lgkmcnt, which cannot tell them apart)
+// would stall on its trip to HBM.
+__device__ __forceinline__ uint32_t vzero() {
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // w_scale, the f32 after the packed codes (src/quant.c:102-106)
 __device__ __forceinline__ float tensor_scale(const gemv_job &job) {
     return *G_CAST(const float, job.w + (size_t) job.n_rows * (job.k >> 2));

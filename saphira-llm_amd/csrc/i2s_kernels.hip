@@ -83,7 +83,7 @@ __device__ __forceinline__ void slab_block(const gemv_job &job, uint32_t slab, u
     // w_scale for the epilogue; without one, read row 0 instead of a tail
     // the caller need not have given (no branch around the load)
     const uint8_t *ws_at = job.out_f != nullptr ? job.w + (size_t) job.n_rows * row_bytes : job.w;
-    const float ws = *G_CAST(const float, ws_at);
+    const float ws = G_CAST(const float, ws_at)[vzero()];   // a vector load
     // keep the scheduler from moving activation loads behind the weight loads
     __builtin_amdgcn_sched_barrier(0);
 
@@ -472,7 +472,7 @@ __device__ __forceinline__ void gemm_block(const gemm_args &G) {
 
     // epilogue (src/i2s_gemm.c:271-290): post = w_scale / act_scale per
     // token, (float)(dot - sum) * post
-    const float ws = *G_CAST(const float, V.w + (size_t) V.n_rows * (G.k >> 2));
+    const float ws = G_CAST(const float, V.w + (size_t) V.n_rows * (G.k >> 2))[vzero()];
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
@@ -628,7 +628,7 @@ __device__ __forceinline__ void gemm_lds_block(const gemm_args &G) {
         }
     }
 
-    const float ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+    const float ws = G_CAST(const float, V.w + (size_t) V.n_rows * kb)[vzero()];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
 #pragma unroll
@@ -805,7 +805,13 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
     float ep_ws = 0.0f;
     act_t ep_at = { 1.0f, 0 };
     if (tid < BM) {
-        ep_ws = *G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+        // the sixteen-wave tiles (a few tokens, one token tile): a vector
+        // load, so that the first wait on the scalar loads does not stall on
+        // it; the others (weight tiles shared in L2 by several token tiles)
+        // measured faster with the scalar load
+        const GLOBAL float *wsp = G_CAST(const float, V.w + (size_t) V.n_rows * kb);
+        if (KG == 4) ep_ws = wsp[vzero()];
+        else ep_ws = *wsp;
         if (V.act != nullptr) ep_at = V.act[min(t0 + tid, m - 1)];
     }
     // copy sources: instruction j of this wave fills LDS granules
