@@ -642,7 +642,7 @@ def host_cpu():
     """The host's CPU model, the logical CPUs this process may run on and the
     physical cores among them (distinct (package, core) pairs in
     /proc/cpuinfo), and the thread counts the CPU baselines use: 1, 4 and
-    all (at most 16, the GPU box's CPU share)."""
+    all (at most 16: the host's share of CPUs per GPU)."""
     try:
         allowed = sorted(os.sched_getaffinity(0))
     except AttributeError:
