@@ -79,6 +79,22 @@ def test_every_tile_shape_gives_the_same_bits(amd, orc, dev, tile):
     _check(orc, w, n_rows, n, x, m, y, d, q, act, f"tile {tile}")
 
 
+@pytest.mark.parametrize("tile", list(range(1, 16)))
+@pytest.mark.parametrize("n", [768, 6912])
+def test_every_tile_shape_with_an_odd_count_of_super_steps(amd, orc, dev, tile, n):
+    """K = 768 and 6912 are 3 and 27 super-steps of 256: the K-group tiles
+    split them unevenly (two groups: the last iteration is group 0's alone;
+    four groups: 27 = 6 x 4 + 3), and the partial sums still meet exactly."""
+    n_rows, m = 320, 19
+    w, x = _case(amd, 4, n_rows, n, m)
+    dev.set_gemm_tile(tile)
+    try:
+        y, d, q, act = _run(amd, dev, w, n_rows, n, x, m)
+    finally:
+        dev.set_gemm_tile(0)
+    _check(orc, w, n_rows, n, x, m, y, d, q, act, f"tile {tile} K {n}")
+
+
 @pytest.mark.parametrize("tile", [0, 1, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15])
 @pytest.mark.parametrize("m", [37, 512])
 def test_several_tensors_in_one_launch(amd, orc, dev, tile, m):
