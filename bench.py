@@ -398,6 +398,10 @@ def measure_decode(amd, dev, tokens=128, warm=8, graph=True, inflight=None):
 
 PREFILL_TOKENS = 512
 PREFILL_CHECK = 16
+# positions whose logits the reference's own chunked forward checks: one in
+# every eight-token scores block, the offset inside the block advancing by
+# one from block to block (positions 0, 9, 18, ..., 511)
+PREFILL_CHECK_POS = tuple(8 * i + i % 8 for i in range(PREFILL_TOKENS // 8))
 
 
 def measure_prefill(amd, dev, model, reps=5):
@@ -407,7 +411,8 @@ def measure_prefill(amd, dev, model, reps=5):
     head for the last token only (a prompt's prefill), and for every token
     (sllm_forward_chunk's full output, its copy to host memory included).
     Rows 0..PREFILL_CHECK-1 of the full output go to the CPU leg's bit-exact
-    check."""
+    check against the oracle, and the rows at PREFILL_CHECK_POS to its check
+    against the reference's own chunked forward over the same 512 tokens."""
     cfg = dict(amd.BITNET_2B)
     n = PREFILL_TOKENS
     toks = [int(t) for t in np.random.default_rng(90).integers(0, cfg["n_vocab"], n)]
@@ -429,7 +434,9 @@ def measure_prefill(amd, dev, model, reps=5):
     g.reset()
     full = g.forward_chunk(toks, 0, logits=True)
     g.close()
-    check = {"model": model, "tokens": toks[:PREFILL_CHECK], "logits": full[:PREFILL_CHECK].copy()}
+    check = {"model": model, "tokens": toks, "logits": full[:PREFILL_CHECK].copy(),
+             "strided": full[list(PREFILL_CHECK_POS)].copy()}
+    del full
     return check, {
         "workload": (f"random-init BitNet-b1.58-2B, one chunk of {n} tokens at positions 0..{n - 1} "
                      f"(sllm_gfx950_forward_chunk), batch 1"),
@@ -737,39 +744,58 @@ def cpu_decode(dec_check, seconds=10.0, thread_counts=(16,)):
 
 def cpu_prefill(pre_check, seconds=10.0, thread_counts=(16,)):
     """Parity: rows 0..15 of the chunk's logits against the oracle's
-    token-by-token logits, bit for bit. Baseline: the reference's own
-    sllm_forward_prefill_chunked (oracle/_ref) on the same model and tokens,
-    chunks of 16, as many chunks as fit in about `seconds`, at each thread
-    count of this host."""
+    token-by-token logits, and the rows at PREFILL_CHECK_POS (one in every
+    eight-token scores block, 511 included) against the reference's own
+    sllm_forward_chunk (oracle/_ref) over the same 512 tokens, bit for bit.
+    Baseline: that reference chunked forward, chunks of 16 from position 0 --
+    at the highest thread count over all 512 tokens (the run the strided
+    check reads), at the others as many chunks as fit in about `seconds`."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     c = pre_check
     model = c["model"]
     o = orc.Decoder(model, PREFILL_CHECK + 8)
-    want = np.stack([o.forward(t, p) for p, t in enumerate(c["tokens"])])
+    want = np.stack([o.forward(t, p) for p, t in enumerate(c["tokens"][:PREFILL_CHECK])])
     o.close()
     if not np.array_equal(want.view(np.uint32), np.ascontiguousarray(c["logits"], np.float32).view(np.uint32)):
         raise SystemExit("bench: the GPU chunk's logits differ from the oracle")
     log(f"prefill chunk: logits of positions 0..{PREFILL_CHECK - 1} match the oracle bit for bit")
     if not orc.ref_available():
-        return {"checked": True, "cpu": None}
-    toks = np.asarray(c["tokens"] * (PREFILL_TOKENS // PREFILL_CHECK), np.int32)
+        return {"checked": True, "strided": False, "cpu": None}
+    toks = np.asarray(c["tokens"], np.int32)
+    pos = list(PREFILL_CHECK_POS)
     runs = []
-    for threads in thread_counts:
+    for threads in sorted(thread_counts, reverse=True):
+        whole = threads == max(thread_counts)
         r = orc.RefDecoder(model, PREFILL_TOKENS + 8, threads=threads)
+        rows = {}
         done, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds and done + 16 <= PREFILL_TOKENS:
-            r.forward_chunk(toks[done:done + 16], done)
+        while done + 16 <= PREFILL_TOKENS and (whole or time.perf_counter() - t0 < seconds):
+            lg = r.forward_chunk(toks[done:done + 16], done)
+            if whole:
+                for p_ in pos:
+                    if done <= p_ < done + 16:
+                        rows[p_] = lg[p_ - done].copy()
             done += 16
         dt = time.perf_counter() - t0
         r.close()
         runs.append({"threads": threads, "tokens_per_s": round(done / dt, 2), "tokens": done, "seconds": round(dt, 1)})
         log(f"reference chunked prefill, {threads} threads: {done / dt:.2f} tokens/s")
+        if whole:
+            ref_rows = np.stack([rows[p_] for p_ in pos])
+            got = np.ascontiguousarray(c["strided"], np.float32)
+            if not np.array_equal(ref_rows.view(np.uint32), got.view(np.uint32)):
+                bad = [p_ for i, p_ in enumerate(pos) if not np.array_equal(ref_rows[i].view(np.uint32),
+                                                                           got[i].view(np.uint32))]
+                raise SystemExit(f"bench: the GPU chunk's logits differ from the reference's at positions {bad[:8]}")
+            log(f"prefill chunk: logits of {len(pos)} positions (one per eight-token block, 0..511) match the "
+                "reference's own chunked forward bit for bit")
     best = max(runs, key=lambda r_: r_["tokens_per_s"])
-    return {"checked": True, "cpu": dict(best, kind="reference", runs=runs,
-                                         sample="sllm_forward_chunk, chunks of 16 from position 0, every token's "
-                                                f"logits, at {', '.join(str(r_['threads']) for r_ in runs)} threads; "
-                                                "the fastest")}
+    return {"checked": True, "strided": True,
+            "cpu": dict(best, kind="reference", runs=runs,
+                        sample="sllm_forward_chunk, chunks of 16 from position 0, every token's logits; at "
+                               f"{max(thread_counts)} threads all {PREFILL_TOKENS} tokens, at the others as many "
+                               "chunks as fit in the time allowed; the fastest")}
 
 
 def cpu_gemm_check(checks):
@@ -1070,7 +1096,11 @@ def main():
             out["decode"]["cpu_baseline"] = dec["cpu"]
         if pre_check is not None:
             pre = cpu_prefill(pre_check, seconds=args.cpu_seconds, thread_counts=host["thread_counts"])
-            out["prefill"]["parity"] = f"logits of positions 0..{PREFILL_CHECK - 1} bit-identical to the oracle"
+            out["prefill"]["parity"] = (f"logits of positions 0..{PREFILL_CHECK - 1} bit-identical to the oracle"
+                                        + (f"; of {len(PREFILL_CHECK_POS)} positions, one per eight-token block "
+                                           f"(0, 9, 18, ..., {PREFILL_CHECK_POS[-1]}), bit-identical to the "
+                                           "reference's own chunked forward over the same tokens"
+                                           if pre["strided"] else ""))
             out["prefill"]["cpu_baseline"] = pre["cpu"]
     print(json.dumps(out), flush=True)
 

@@ -182,6 +182,41 @@ def test_full_2b_chunk_is_bit_exact(amd, orc, dev):
     assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
 
 
+@pytest.mark.parametrize("prefix", [0, 1024])
+def test_2b_width_512_token_chunk_every_position(amd, orc, dev, prefix):
+    """One chunk of 512 tokens -- the device's largest, twice the reference's
+    cap -- at BitNet-2B widths (20 x 128 query heads over 5 KV heads, FFN
+    6912; two blocks and a 512-row vocabulary keep the oracle to seconds),
+    from position 0 as the prefill benchmark runs it, and after a restored
+    1024-position cache (rows up to 1536 positions). Every token's scores
+    workgroup of eight, every p.V chain length from 1 to 512 (and 1025 to
+    1536): every position's logits against the oracle's token-by-token
+    logits, bit for bit."""
+    cfg = dict(amd.BITNET_2B, n_layer=2, n_vocab=512)
+    model = amd.synth_model(cfg, 93)
+    toks = _tokens(512, cfg["n_vocab"], 94 + prefix)
+    n_ctx = prefix + 512 + 8
+    caches = None
+    if prefix:
+        hd = cfg["n_embd"] // cfg["n_head"]
+        rng = np.random.default_rng(95)
+        shape = (cfg["n_layer"], cfg["n_head_kv"], prefix, hd)
+        caches = (rng.standard_normal(shape).astype(np.float16).astype(np.float32),
+                  rng.standard_normal(shape).astype(np.float16).astype(np.float32))
+    print(f"[chunk] 2B widths: oracle, 512 tokens after {prefix} positions", flush=True)
+    want = _oracle_logits(orc, model, n_ctx, toks, prefix, caches)
+    g = amd.DeviceDecoder(dev, model, n_ctx)
+    try:
+        if caches is not None:
+            g.kv_load(caches[0], caches[1], prefix)
+        print("[chunk] device chunk of 512", flush=True)
+        got = g.forward_chunk(toks, prefix)
+        assert g.n_past() == prefix + 512
+    finally:
+        g.close()
+    assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
 def test_chunk_refuses_what_the_reference_refuses(amd, dev):
     cfg = dict(TINY, n_layer=1)
     model = amd.synth_model(cfg, 77)
