@@ -115,6 +115,8 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 
 /* kernel constants (decode_kernels.hip) */
 #define ATT_THREADS 256
+#define PV_THREADS  512
+#define PV_HPW      2
 #define ATT_POS     64
 #define PV_SLICE    8
 #define LM_THREADS  256
@@ -579,6 +581,8 @@ static int launch_token(sllm_gfx950_ctx *c) {
     int st = SLLM_GFX950_OK;
     const uint32_t kv_chunks = (uint32_t) ((c->n_ctx + ATT_POS - 1) / ATT_POS);
     const uint32_t slices = (uint32_t) (m->hd / PV_SLICE);
+    /* p.V workgroups per (KV head, slice): two query heads each */
+    const uint32_t pv_wpk = (uint32_t) ((m->n_head / m->n_head_kv + PV_HPW - 1) / PV_HPW);
     for (int32_t il = 0; il < m->n_layer && st == SLLM_GFX950_OK; ++il) {
         for (int s = 0; s < N_STAGE && st == SLLM_GFX950_OK; ++s) {
             k_dec_gemv_args *A = &c->gargs[(size_t) il * N_STAGE + s];
@@ -588,7 +592,7 @@ static int launch_token(sllm_gfx950_ctx *c) {
                 void *aargs[] = { &c->attn_args[il] };
                 st = sllm_shim_launch(c->f_scores, (uint32_t) m->n_head_kv, kv_chunks, ATT_THREADS, 0, aargs);
                 if (st == SLLM_GFX950_OK) {
-                    st = sllm_shim_launch(c->f_pv, (uint32_t) m->n_head_kv, slices, ATT_THREADS, 0, aargs);
+                    st = sllm_shim_launch(c->f_pv, (uint32_t) m->n_head_kv * slices * pv_wpk, 1, PV_THREADS, 0, aargs);
                 }
             }
         }

@@ -432,7 +432,12 @@ constexpr uint32_t PV_SLICE = 8;       // head dimensions per p.V workgroup
 constexpr uint32_t PV_RPOS = 1536;      // positions of p (LDS) and V (registers) per round
 constexpr uint32_t PV_SUB = 192;        // positions per product sub-round
 constexpr uint32_t PV_XSTRIDE = PV_SUB + 4;                // LDS product row: rows 4 banks apart
-constexpr int PV_PTHREADS = ATT_THREADS - 64;              // producer threads (waves 1..3)
+constexpr int PV_THREADS = 512;                            // p.V workgroup: eight waves
+constexpr int PV_WAVES = PV_THREADS / 64;
+constexpr uint32_t PV_HPW = 2;                             // query heads per p.V workgroup
+constexpr int PV_WPH = PV_WAVES / (int) PV_HPW;            // waves per head
+constexpr uint32_t PV_SPAN = 512u * PV_WPH;                // positions of one pass: a group per lane
+constexpr int PV_PTHREADS = 128;                           // producer threads: waves 3 and 7
 constexpr int PV_VLOADS = (int) (PV_RPOS * PV_SLICE / 4 / PV_PTHREADS);   // float4 of V per producer
 constexpr int PV_VSUB = (int) (PV_SUB * PV_SLICE / 4 / PV_PTHREADS);      // of them per sub-round
 constexpr uint32_t PV_G4 = PV_SLICE / 4;                   // float4 per position of a slice
@@ -440,6 +445,7 @@ static_assert(ATT_MAX_GRP * PV_SLICE <= 64, "one chain wave");
 static_assert(PV_VLOADS * PV_PTHREADS * 4 == (int) (PV_RPOS * PV_SLICE), "whole float4 per producer");
 static_assert(PV_VSUB * PV_PTHREADS * 4 == (int) (PV_SUB * PV_SLICE) && PV_RPOS % PV_SUB == 0, "sub-rounds");
 static_assert(PV_PTHREADS % PV_G4 == 0, "a producer keeps its dimensions");
+static_assert(PV_SPAN >= PV_RPOS && PV_HPW * PV_SLICE <= 64, "one group per lane; one chain wave");
 
 // NeoX RoPE (src/ops.c:467-549) of element d of a head vector: pairs
 // (e, e + half) rotate by angle e, x[e] -> x[e] c - x[e+half] s and
@@ -660,65 +666,98 @@ sllm_k_chk_scores(dec_attn A, uint32_t n_tok) { chk_scores_body<8>(A, n_tok); }
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_chk_scores4(dec_attn A, uint32_t n_tok) { chk_scores_body<4>(A, n_tok); }
 
-// Softmax and p . V: workgroup (KV head, 16 head dimensions), four waves.
-//  - The slice of V for the first 1536 positions is loaded first, all of it
-//    in flight (24 float4 per thread).
-//  - Wave w takes the softmax of query head w of the KV head
-//    (src/ops.c:386-422): the max; ggml_v_expf over whole groups of eight,
-//    the C library's expf over the rest; the double sum with each group
-//    added as ((t0 + t1) + t2) + t3 of t_j = e_j + e_{j+4}, in any order,
-//    checked, in the reference's order when the check cannot decide;
-//    inv = 1/sum narrowed to f32; p = e * inv. Each lane holds groups of
-//    eight consecutive scores, so a group's sum never leaves its lane, and
-//    the first round's e go to LDS in the same pass.
+// Softmax and p . V: workgroup (two query heads of a KV head, 8 head
+// dimensions), eight waves.
+//  - The softmax of each head's row (src/ops.c:386-422), on waves 4h ..
+//    4h + 3: lane i of them holds the eight consecutive scores at 8i of each
+//    span of 2048 positions; the max; ggml_v_expf over whole groups of eight, the C
+//    library's expf over the rest (the tail group's wave, one term per
+//    lane); the double sum with each group added as ((t0 + t1) + t2) + t3
+//    of t_j = e_j + e_{j+4}, the groups in any order, checked, in the
+//    reference's order when the check cannot decide; inv = 1/sum narrowed to
+//    f32; p = e * inv. A head's waves meet in LDS for the max and for the
+//    sum. For rows of at most 1536 positions the scores are loaded first,
+//    one group per lane, and stay in registers. One wave issues a VALU
+//    instruction every five or six cycles, so the exponentials of a row are
+//    spread over the lanes, and a workgroup takes two query heads, not the
+//    four of a KV head: the workgroups of one KV head share its slice of V
+//    (they run on one XCD, where its L2 serves the repeat), not the
+//    exponentials.
+//  - The slice of V for the first 1536 positions is loaded by the two
+//    producer waves, 3 and 7, 24 float4 per thread, once the scores are in.
+//    In a row of at most 1536 positions those waves hold no scores: a wave
+//    waits on its loads in the order it issued them, so a softmax wave with
+//    V loads in flight would wait for them at its next use of a score.
 //  - Per round of 1536 positions, p in LDS and the slice of V in the
-//    registers of waves 1..3 (32 float4 per thread, issued before the
-//    softmax). In sub-rounds of 192 positions those waves form the products
-//    p_s * v_s of every (head, dimension) into one of two LDS buffers, while
-//    wave 0, one lane per (head, dimension), adds the previous sub-round's
+//    producers' registers. In sub-rounds of 192 positions the producers form
+//    the products p_s * v_s of every (head, dimension) into one of two LDS
+//    buffers, while wave 0, one lane per (head, dimension), adds the previous sub-round's
 //    products to its accumulator in order of s (src/forward.c:706-726) --
 //    the chain wave issues adds and reads only.
-template <bool CHUNK>
 __device__ __forceinline__ void pv_body(const dec_attn &A) {
-    __shared__ __attribute__((aligned(16))) float P[ATT_MAX_GRP][PV_RPOS];
-    __shared__ __attribute__((aligned(16))) float X[2][ATT_MAX_GRP * PV_SLICE][PV_XSTRIDE];
-    __shared__ float stat_inv[ATT_MAX_GRP], stat_m[ATT_MAX_GRP];
+    __shared__ __attribute__((aligned(16))) float P[PV_HPW][PV_RPOS];
+    __shared__ __attribute__((aligned(16))) float X[2][PV_HPW * PV_SLICE][PV_XSTRIDE];
+    __shared__ float stat_inv[PV_HPW], red_m[PV_WAVES];
+    __shared__ double red_s[PV_WAVES];
     __shared__ uint64_t tab[32];          // the expf table, next to the lanes that index it
-    const uint32_t kvh = blockIdx.x, d0 = blockIdx.y * PV_SLICE, tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
-    const uint32_t t = CHUNK ? blockIdx.z : 0u;
-    const uint32_t npast = (CHUNK ? A.chunk_base + t : (uint32_t) A.step->pos) + 1;
-    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
-    const float *scores = A.scores + (size_t) t * A.n_head * ss;
-    const uint32_t nb = npast / 8, nt = nb * 8;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride, slices = hd / PV_SLICE;
+    const uint32_t wpk = (grp + PV_HPW - 1) / PV_HPW;      // workgroups per (KV head, slice)
+    // workgroup -> (KV head, slice, its first query head): the workgroups of
+    // one (KV head, slice) on one XCD (workgroups go to the eight XCDs in
+    // turn) when the grid allows
+    uint32_t kvh, slice, j;
+    {
+        const uint32_t total = A.n_kv * slices * wpk, L = blockIdx.x;
+        uint32_t p;
+        if (total % (8 * wpk) == 0) {
+            const uint32_t per = total / 8, x = L % 8, r = L / 8;
+            p = x * (per / wpk) + r / wpk;
+            j = r % wpk;
+        } else {
+            p = L / wpk;
+            j = L % wpk;
+        }
+        kvh = p / slices;
+        slice = p % slices;
+    }
+    const uint32_t d0 = slice * PV_SLICE, qh0 = kvh * grp + j * PV_HPW;
+    const uint32_t nh = min(PV_HPW, grp - j * PV_HPW);     // heads of this workgroup
+    const uint32_t head = wave / PV_WPH, hw = wave % PV_WPH;
+    const bool soft = head < nh;                          // uniform per wave
+    const float *sc = A.scores + (size_t) (qh0 + min(head, nh - 1)) * ss;
     // this workgroup's slice of V: dimensions d0 .. d0 + 7 of every position, contiguous
-    const float *vc = A.v_cache + ((size_t) kvh * A.n_ctx * hd + (size_t) blockIdx.y * A.n_ctx * PV_SLICE);
-
-    auto group_sum = [](const float (&e)[8]) {
-        const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
-        const double t2 = (double) e[2] + (double) e[6], t3 = (double) e[3] + (double) e[7];
-        return ((t0 + t1) + t2) + t3;
-    };
-    // eight scores from position s of a row (clamped inside the row: only
+    const float *vc = A.v_cache + ((size_t) kvh * A.n_ctx * hd + (size_t) slice * A.n_ctx * PV_SLICE);
+    const uint32_t lpos = 8 * (hw * 64 + lane);         // the lane's first position in a span
+    // eight scores from position s of the row (clamped inside the row: only
     // groups wholly past npast move)
-    auto load8 = [&](const float *sc, uint32_t s, float (&v)[8]) {
+    auto load8 = [&](uint32_t s, float (&v)[8]) {
         const uint32_t at = min(s, ss - 8);
         const f32x4 a = *G_CAST(const f32x4, sc + at), b = *G_CAST(const f32x4, sc + at + 4);
         v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
         v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
     };
-    // e of the group at s: ggml_v_expf for a whole group, the C library's
-    // expf for the tail group (s and nt are multiples of eight, so a group
-    // lies wholly on one side; a branch, so that only the tail's lane runs
-    // the double-precision path)
-    auto exps8 = [&](float (&v)[8], uint32_t s, float m) {
-        if (s < nt) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = sllm_libm_expf(v[i] - m, tab);
-        }
+
+    // (1) the loads that do not wait for the position, issued ahead of its
+    // load: the lane's group of the first round (waves past it have none)
+    // and the expf table
+    const bool first_round_lane = soft && lpos < PV_RPOS;   // uniform per wave
+    float sv[8];
+    if (first_round_lane) load8(lpos, sv);
+    const uint64_t tab_e = c_expf_tab[tid & 31u];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t npast = (uint32_t) A.step->pos + 1;
+    const uint32_t nb = npast / 8, nt = nb * 8;
+    const bool one_round = npast <= PV_RPOS;
+    // the tail group (positions nt .. npast - 1, if any): its span, wave of
+    // the head's and lane
+    const bool has_tail = npast > nt;
+    const uint32_t t_span = nt / PV_SPAN, t_hw = (nt % PV_SPAN) / 512, t_lane = (nt % 512) / 8;
+
+    auto group_sum = [](const float (&e)[8]) {
+        const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
+        const double t2 = (double) e[2] + (double) e[6], t3 = (double) e[3] + (double) e[7];
+        return ((t0 + t1) + t2) + t3;
     };
     // e of the tail group (npast - nt <= 7 terms, the C library's expf),
     // held by lane lt: one term per lane, so that the wave evaluates expf
@@ -739,21 +778,28 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
             if (lane == lt && (uint32_t) i < cnt) v[i] = ei;
         }
     };
-    // one round (npast <= 1536): each softmax wave's scores are loaded
-    // first, all at once, ahead of V, and stay in registers
-    constexpr int RG = (int) (PV_RPOS / 512);
-    const bool one_round = npast <= PV_RPOS;
-    float sv[RG][8];
-    if (one_round && wave < grp) {
-        const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
+    // e and the partial sum of the lane's group at s (whole groups through
+    // ggml_v_expf; the tail group's terms already in v)
+    auto exps_sum = [&](float (&v)[8], uint32_t s, float m, double &part) {
+        if (s < nt) {
 #pragma unroll
-        for (int g = 0; g < RG; ++g) load8(sc, 512u * (uint32_t) g + 8 * lane, sv[g]);
-    }
+            for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
+        }
+        if (s + 8 <= npast) {
+            part += group_sum(v);
+        } else if (s < npast) {                       // the tail, from the lane's own registers
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (s + (uint32_t) i < npast) part += (double) v[i];
+            }
+        }
+    };
 
-    // producer pt = tid - 64 holds float4 f = pt + 192 u of a round:
-    // position f / G4, dimensions 4 (pt % G4) .. + 3 of the slice (G4 =
-    // float4 per position); its float4 G4 j .. G4 j + G4 - 1 are sub-round j
-    const uint32_t pt = tid - 64u;
+    // producer pt holds float4 f = pt + 128 u of a round: position f / G4,
+    // dimensions 4 (pt % G4) .. + 3 of the slice; its float4 3j .. 3j + 2
+    // are sub-round j
+    const bool producer = (wave & 3u) == 3;
+    const uint32_t pt = (wave >> 2) * 64 + lane;
     f32x4 vr[PV_VLOADS];
     auto load_v = [&](uint32_t base) {
 #pragma unroll
@@ -763,168 +809,140 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
             vr[u] = *G_CAST(const f32x4, vc + (size_t) sp * PV_SLICE + 4 * (f % PV_G4));
         }
     };
-    if (wave > 0) load_v(0);
-    if (tid < 32) tab[tid] = c_expf_tab[tid];
-    __syncthreads();
 
-    if (wave < grp) {
-        const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
-        float *ph = P[wave];
-        float m = -INFINITY;
-        double part = 0.0;
+    // (2) the max of each head's row
+    float m = -INFINITY;
+    if (soft) {
         if (one_round) {
-            float (&v)[RG][8] = sv;
+            if (first_round_lane) {
 #pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                const uint32_t s = 512u * (uint32_t) g + 8 * lane;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[g][i] : -INFINITY);
-            }
-            m = wave_max(m);
-            // the tail group's C-library expf (npast - nt <= 7 terms): one
-            // term per lane, so that the wave evaluates it once rather than
-            // the tail's lane eight times over
-            if (npast > nt) {                     // uniform
-                const uint32_t gt = nt / 512u, lt = (nt % 512u) / 8u, cnt = npast - nt;
-                float xt = 0.0f;
-#pragma unroll
-                for (int g = 0; g < RG; ++g) {
-                    if ((uint32_t) g == gt) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const float xi = lane_f(v[g][i], (int) lt);
-                            xt = lane == (uint32_t) i ? xi : xt;
-                        }
-                    }
-                }
-                float et = 0.0f;
-                if (lane < cnt) et = sllm_libm_expf(xt - m, tab);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float ei = lane_f(et, i);
-#pragma unroll
-                    for (int g = 0; g < RG; ++g) {
-                        if ((uint32_t) g == gt && lane == lt && (uint32_t) i < cnt) v[g][i] = ei;
-                    }
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                const uint32_t s = 512u * (uint32_t) g + 8 * lane;
-                if (s < npast) {
-                    if (s < nt) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) v[g][i] = ggml_v_expf<true>(v[g][i] - m);
-                    }
-                    if (s + 8 <= npast) {
-                        part += group_sum(v[g]);
-                    } else {                      // the tail, from the lane's own registers
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            if (s + (uint32_t) i < npast) part += (double) v[g][i];
-                        }
-                    }
-                }
+                for (int i = 0; i < 8; ++i) m = fmaxf(m, lpos + (uint32_t) i < npast ? sv[i] : -INFINITY);
             }
         } else {
-            for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
+            for (uint32_t b0 = 0; b0 < npast; b0 += PV_SPAN) {
                 float v[8];
-                const uint32_t s = b0 + 8 * lane;
-                load8(sc, s, v);
+                const uint32_t s = b0 + lpos;
+                load8(s, v);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
             }
-            m = wave_max(m);
-            // e (of the first round into LDS) and the sum of whole groups; the
-            // tail positions, one lane each
-            for (uint32_t b0 = 0; b0 < npast; b0 += 512) {
-                float v[8];
-                const uint32_t s = b0 + 8 * lane;
-                load8(sc, s, v);
-                if (npast > nt && nt - b0 < 512u) tail8(v, (nt - b0) / 8u, m);   // uniform
-                if (s < nt) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
-                }
-                if (s + 8 <= npast) {
-                    part += group_sum(v);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        if (s + (uint32_t) i < npast) part += (double) v[i];
-                    }
-                }
-                if (s < PV_RPOS) {
-                    *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0], v[1], v[2], v[3] };
-                    *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4], v[5], v[6], v[7] };
-                }
-            }
         }
-        const double sum = wave_sum_d(part);
-        const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
-        float inv = (float) (1.0 / (sum - bound));
-        if (inv != (float) (1.0 / (sum + bound))) {   // uniform over the wave
-            if (lane == 0) {
-                double seq = 0.0;
-                for (uint32_t s = 0; s < nt; s += 8) {
-                    float v[8];
-                    load8(sc, s, v);
-                    exps8(v, s, m);
-                    seq += group_sum(v);
-                }
-                for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
-                inv = (float) (1.0 / seq);
-            }
-            inv = lane_f(inv, 0);
-        }
-        // p of the first round: one round, straight from the e still in
-        // registers; else in place over the e written to LDS
+    }
+    m = wave_max(m);
+    if (lane == 0) red_m[wave] = m;
+    if (tid < 32) tab[tid] = tab_e;
+    __syncthreads();                                 // red_m and the expf table visible
+
+    // the producers' V (in a row of at most 1536 positions the producers
+    // hold no scores)
+    if (producer && one_round) load_v(0);
+
+    // (3) e and the double sum of whole groups; the tail terms one lane each
+    const uint32_t hb = min(head, PV_HPW - 1) * PV_WPH;  // the head's first wave
+    m = red_m[hb];
+#pragma unroll
+    for (int w = 1; w < PV_WPH; ++w) m = fmaxf(m, red_m[hb + w]);
+    double part = 0.0;
+    if (soft) {
         if (one_round) {
-#pragma unroll
-            for (int g = 0; g < RG; ++g) {
-                const uint32_t s = 512u * (uint32_t) g + 8 * lane;
-                if (s < npast) {
-                    const float (&v)[8] = sv[g];
-                    *reinterpret_cast<f32x4 *>(ph + s) = (f32x4) { v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv };
-                    *reinterpret_cast<f32x4 *>(ph + s + 4) = (f32x4) { v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv };
-                }
+            if (first_round_lane) {
+                if (has_tail && t_hw == hw) tail8(sv, t_lane, m);     // uniform: the tail group's wave
+                exps_sum(sv, lpos, m, part);
             }
         } else {
-            const uint32_t n0 = min(npast, PV_RPOS);
-            for (uint32_t i = 4 * lane; i < n0; i += 256) {
-                f32x4 e4 = *reinterpret_cast<const f32x4 *>(ph + i);
-                e4[0] = e4[0] * inv; e4[1] = e4[1] * inv; e4[2] = e4[2] * inv; e4[3] = e4[3] * inv;
-                *reinterpret_cast<f32x4 *>(ph + i) = e4;
+            for (uint32_t b0 = 0; b0 < npast; b0 += PV_SPAN) {
+                float v[8];
+                const uint32_t s = b0 + lpos;
+                load8(s, v);
+                if (has_tail && b0 == t_span * PV_SPAN && t_hw == hw) tail8(v, t_lane, m);   // uniform
+                exps_sum(v, s, m, part);
+                if (s < PV_RPOS) {                   // e of the first round, for p in place below
+                    *reinterpret_cast<f32x4 *>(&P[head][s]) = (f32x4) { v[0], v[1], v[2], v[3] };
+                    *reinterpret_cast<f32x4 *>(&P[head][s + 4]) = (f32x4) { v[4], v[5], v[6], v[7] };
+                }
             }
         }
-        if (lane == 0) {
-            stat_m[wave] = m;
-            stat_inv[wave] = inv;
+    }
+    part = wave_sum_d(part);
+    if (lane == 0) red_s[wave] = part;
+    if (producer && !one_round) load_v(0);           // after this path's own score loads
+    __syncthreads();                                 // red_s (and the first round's e) visible
+
+    // (4) inv of each head, checked; p of the first round: from the e in
+    // registers (one round), else in place over the e in LDS.
+    // The reference's sum S lies within s (1 -+ b) of this order's s, b =
+    // bound_f; its inv is (float) fl(1/S), and fl(1/S) lies within
+    // r (1 -+ (b + 2^-50)) of r = fl(1/s). When both ends of that interval
+    // narrow to one f32 -- the narrowing is monotone -- that f32 is the
+    // reference's. One division per lane: lanes 32h .. 32h + 31 take head h.
+    const double bound_f = (double) (nb + (npast - nt) + 8) * 0x1p-52;
+    float inv_l;
+    bool ok_l;
+    {
+        const uint32_t h = min(lane >> 5, PV_HPW - 1);
+        double sum = red_s[h * PV_WPH];
+#pragma unroll
+        for (int w = 1; w < PV_WPH; ++w) sum += red_s[h * PV_WPH + w];
+        const double r = 1.0 / sum, dr = r * (bound_f + 0x1p-50);
+        inv_l = (float) (r - dr);
+        ok_l = inv_l == (float) (r + dr) || h >= nh;
+    }
+    const bool ok_all = __builtin_amdgcn_readfirstlane((uint32_t) ok_l) != 0 &&
+                        __builtin_amdgcn_readlane((uint32_t) ok_l, 32) != 0;    // uniform over the workgroup
+    float inv = lane_f(inv_l, (int) (32 * min(head, PV_HPW - 1)));
+    if (!ok_all) {
+        // the reference's own order, one thread per head whose check cannot decide
+        const bool mine = __builtin_amdgcn_readlane((uint32_t) ok_l, (int) (32 * min(head, PV_HPW - 1))) == 0;
+        if (soft && mine && hw == 0 && lane == 0) {
+            double seq = 0.0;
+            for (uint32_t s = 0; s < nt; s += 8) {
+                float v[8];
+                load8(s, v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
+                seq += group_sum(v);
+            }
+            for (uint32_t s = nt; s < npast; ++s) seq += (double) sllm_libm_expf(sc[s] - m, tab);
+            stat_inv[head] = (float) (1.0 / seq);
+        }
+        __syncthreads();
+        if (mine) inv = stat_inv[min(head, PV_HPW - 1)];
+    }
+    if (one_round) {
+        if (first_round_lane && lpos < npast) {
+            float *ph = &P[head][lpos];
+            *reinterpret_cast<f32x4 *>(ph) = (f32x4) { sv[0] * inv, sv[1] * inv, sv[2] * inv, sv[3] * inv };
+            *reinterpret_cast<f32x4 *>(ph + 4) = (f32x4) { sv[4] * inv, sv[5] * inv, sv[6] * inv, sv[7] * inv };
+        }
+    } else if (first_round_lane) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 4) {
+            f32x4 e4 = *reinterpret_cast<const f32x4 *>(&P[head][lpos + i]);
+            e4[0] = e4[0] * inv; e4[1] = e4[1] * inv; e4[2] = e4[2] * inv; e4[3] = e4[3] * inv;
+            *reinterpret_cast<f32x4 *>(&P[head][lpos + i]) = e4;
         }
     }
 
-    // rounds of 1536 positions, sub-rounds of 192
-    const bool chain = wave == 0 && lane < grp * PV_SLICE;
+    // (5) rounds of 1536 positions, sub-rounds of 192
+    const bool chain = wave == 0 && lane < nh * PV_SLICE;
     const uint32_t d4 = 4u * (pt % PV_G4);
     // products of sub-round j (positions 192 j ..) into X[buf]
     auto produce = [&](uint32_t j, int buf) {
-        float pw[PV_VSUB][ATT_MAX_GRP];           // every p read first, then the products
+        float pw[PV_VSUB][PV_HPW];                // every p read first, then the products
 #pragma unroll
         for (int u = 0; u < PV_VSUB; ++u) {
             const uint32_t sl = (pt + (uint32_t) u * PV_PTHREADS) / PV_G4;
 #pragma unroll
-            for (int h = 0; h < (int) ATT_MAX_GRP; ++h) pw[u][h] = P[min((uint32_t) h, grp - 1)][PV_SUB * j + sl];
+            for (int h = 0; h < (int) PV_HPW; ++h) pw[u][h] = P[h][PV_SUB * j + sl];
         }
 #pragma unroll
         for (int u = 0; u < PV_VSUB; ++u) {
             const f32x4 v = vr[(int) (PV_VSUB * j) + u];     // j is a constant after unrolling
             const uint32_t sl = (pt + (uint32_t) u * PV_PTHREADS) / PV_G4;
 #pragma unroll
-            for (int h = 0; h < (int) ATT_MAX_GRP; ++h) {
-                if ((uint32_t) h < grp) {
+            for (int h = 0; h < (int) PV_HPW; ++h) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) X[buf][(uint32_t) h * PV_SLICE + d4 + (uint32_t) e][sl] = pw[u][h] * v[e];
-                }
+                for (int e = 0; e < 4; ++e) X[buf][(uint32_t) h * PV_SLICE + d4 + (uint32_t) e][sl] = pw[u][h] * v[e];
             }
         }
     };
@@ -932,30 +950,29 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
     for (uint32_t base = 0; base < npast; base += PV_RPOS) {
         const uint32_t n = min(PV_RPOS, npast - base);
         if (base > 0) {
-            __syncthreads();                      // stat_* visible; the last round's products read
-            if (wave > 0) load_v(base);
-            if (wave < grp) {                     // p of this round, recomputed (the same bits)
-                const float *sc = scores + (size_t) (kvh * grp + wave) * ss;
-                const float m = stat_m[wave], inv = stat_inv[wave];
-                for (uint32_t i0 = 0; i0 < n; i0 += 512) {
+            __syncthreads();                      // the last round's products read
+            if (producer) load_v(base);
+            if (soft) {                           // p of this round, recomputed (the same bits)
+                for (uint32_t i0 = 0; i0 < n; i0 += PV_SPAN) {
+                    const uint32_t i = i0 + lpos;
                     float v[8];
-                    const uint32_t i = i0 + 8 * lane;
-                    load8(sc, base + i, v);
-                    if (npast > nt && nt - (base + i0) < 512u) tail8(v, (nt - base - i0) / 8u, m);   // uniform
+                    load8(base + i, v);
+                    const uint32_t r = nt - (base + i0);       // the tail group's offset in this pass
+                    if (has_tail && r < PV_SPAN && r / 512 == hw) tail8(v, (r % 512) / 8, m);   // whole wave
                     if (base + i < nt) {
 #pragma unroll
                         for (int e = 0; e < 8; ++e) v[e] = ggml_v_expf<true>(v[e] - m);
                     }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        if (i + (uint32_t) e < n) P[wave][i + (uint32_t) e] = v[e] * inv;
+                        if (i + (uint32_t) e < n) P[head][i + (uint32_t) e] = v[e] * inv;
                     }
                 }
             }
         }
         __syncthreads();                          // this round's p in LDS
         const uint32_t n_sub = (n + PV_SUB - 1) / PV_SUB;
-        if (wave > 0) produce(0, 0);
+        if (producer) produce(0, 0);
         __syncthreads();
         // unrolled whole, so that the producers' register indices are constants
 #pragma unroll
@@ -1006,17 +1023,17 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
                     }
                     for (; s < cnt; ++s) acc = acc + x[s];
                 }
-            } else if (j + 1 < n_sub) {
+            } else if (producer && j + 1 < n_sub) {
                 produce(j + 1, (int) ((j + 1) & 1u));
             }
             __syncthreads();
         }
     }
-    if (chain) A.out[(size_t) t * A.n_head * hd + (size_t) (kvh * grp + lane / PV_SLICE) * hd + d0 + lane % PV_SLICE] = acc;
+    if (chain) A.out[(size_t) (qh0 + lane / PV_SLICE) * hd + d0 + lane % PV_SLICE] = acc;
 }
 
-extern "C" __global__ void __launch_bounds__(ATT_THREADS)
-sllm_k_dec_pv(dec_attn A) { pv_body<false>(A); }
+extern "C" __global__ void __launch_bounds__(PV_THREADS)
+sllm_k_dec_pv(dec_attn A) { pv_body(A); }
 
 // ---------------------------------------------------------------------------
 // output: x = a + b, RMSNorm with output_norm, the F16 rows
