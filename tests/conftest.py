@@ -30,7 +30,12 @@ def load_package():
 
 @pytest.fixture(scope="session")
 def amd():
-    return load_package()
+    mod = load_package()
+    # SLLM_TEST_LIB: run the tests against another build of the library's C
+    # sources (the sanitizer build of tests/fakehip, tests/test_sanitizers.py)
+    if os.environ.get("SLLM_TEST_LIB"):
+        mod.LIB_PATH = os.environ["SLLM_TEST_LIB"]
+    return mod
 
 
 @pytest.fixture(scope="session")

@@ -33,7 +33,9 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 FAKE_DIR = os.path.join(ROOT, "tests", "fakehip")
-FAKE = os.path.join(FAKE_DIR, "libsllm_gfx950_fakehip.so")
+# SLLM_FAKEHIP_SAN=1: the ASan + UBSan build of the same sources (tests/test_sanitizers.py)
+FAKE_NAME = "libsllm_gfx950_fakehip_san.so" if os.environ.get("SLLM_FAKEHIP_SAN") else "libsllm_gfx950_fakehip.so"
+FAKE = os.path.join(FAKE_DIR, FAKE_NAME)
 
 HIP_INVALID_VALUE, HIP_OUT_OF_MEMORY = 1, 2          # hipErrorInvalidValue, hipErrorOutOfMemory
 NOMEM, UNSUPPORTED, NO_DEVICE, HIP = -2, -4, -60, -61
@@ -47,7 +49,7 @@ def _build():
     # one build at a time when test workers run side by side
     with open(os.path.join(FAKE_DIR, ".build.lock"), "w") as lock:
         fcntl.flock(lock, fcntl.LOCK_EX)
-        r = subprocess.run(["make", "-s", "-C", FAKE_DIR], capture_output=True, text=True)
+        r = subprocess.run(["make", "-s", "-C", FAKE_DIR, FAKE_NAME], capture_output=True, text=True)
     if r.returncode != 0:
         pytest.fail(f"building the fake-HIP library failed:\n{r.stdout}\n{r.stderr}")
 
