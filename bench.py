@@ -13,9 +13,13 @@ before the timed region.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
-Beside the headline line the JSON carries:
+Beside the headline line the JSON carries (each GPU figure also as the
+median and best of several batches or runs):
+  batches  the headline launch in ten batches of 100;
   cfg0     one 2560 x 2560 GEMV per launch, hot and rotated over 192 tensors,
            and the 192 as one launch;
+  ffn_sets the headline workload one weight set per launch (gate + up +
+           down), the 32 sets rotated;
   dropin   the same FFN workload through the host-pointer row that a patched
            reference forward.c calls (sllm_kdispatch_*), each call copying
            across PCIe and waiting: what the drop-in costs per GEMV;
@@ -174,6 +178,7 @@ def measure_block_plan(amd, dev, layers=30, steps=200):
     dev.sync()
     wall_us = (time.perf_counter() - t0) * 1e6 / steps
     ev_us = dev.elapsed(0, 1) * 1e3 / steps
+    bt = timed_batches(dev, lambda: dev.plan_run(plan), 10, steps // 10)
     dev.plan_destroy(plan)
     for b in bufs:
         b.free()
@@ -182,7 +187,8 @@ def measure_block_plan(amd, dev, layers=30, steps=200):
                         "down 2560x6912), 210 GEMVs in one launch, f32 inputs quantised in-kernel",
             "weight_bytes": w_bytes, "bytes_per_launch": total, "us_per_launch": round(ev_us, 2),
             "GBps": round(total / (ev_us * 1e-6) / 1e9, 1), "wall_us_per_launch": round(wall_us, 2),
-            "frac_of_peak": round(total / (ev_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "steps": steps}
+            "frac_of_peak": round(total / (ev_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "steps": steps,
+            "batches": with_rate(bt, total)}
 
 
 CFG0_N = 2560
@@ -216,7 +222,13 @@ def measure_cfg0(amd, dev, calls=2000):
             dev.linear(bws[i % rot].vp, n, n, bx.at(4 * n * (i % rot)), bq.vp, ba.vp, by.at(4 * n * (i % rot)))
         dev.record(1)
         us = dev.elapsed(0, 1) * 1e3 / calls
-        res[label] = {"us_per_call": round(us, 2), "GBps": round(per_call / us / 1e3, 1)}
+        it = iter(range(1 << 40))
+
+        def call():
+            i = next(it) % rot
+            dev.linear(bws[i].vp, n, n, bx.at(4 * n * i), bq.vp, ba.vp, by.at(4 * n * i))
+        res[label] = {"us_per_call": round(us, 2), "GBps": round(per_call / us / 1e3, 1),
+                      "batches": with_rate(timed_batches(dev, call, 10, calls // 10), per_call)}
         log(f"cfg0 2560x2560 {label}: {us:.2f} us per call, {per_call / us / 1e3:.1f} GB/s")
     checks = []
     for i in (0, CFG0_COPIES - 1):
@@ -232,12 +244,14 @@ def measure_cfg0(amd, dev, calls=2000):
         dev.plan_run(plan)
     dev.record(1)
     us = dev.elapsed(0, 1) * 1e3 / reps
+    bt = timed_batches(dev, lambda: dev.plan_run(plan), 10, reps // 10)
     dev.plan_destroy(plan)
     for b in bws + [bx, bq, ba, by]:
         b.free()
     total = per_call * CFG0_COPIES
     res["batched"] = {"us_per_launch": round(us, 2), "GBps": round(total / us / 1e3, 1),
-                      "frac_of_peak": round(total / us / 1e3 / PEAK_HBM_GBS, 4), "gemvs_per_launch": CFG0_COPIES}
+                      "frac_of_peak": round(total / us / 1e3 / PEAK_HBM_GBS, 4), "gemvs_per_launch": CFG0_COPIES,
+                      "batches": with_rate(bt, total)}
     log(f"cfg0 2560x2560, {CFG0_COPIES} rotated GEMVs in one launch: {us:.2f} us, {total / us / 1e3:.1f} GB/s")
     return checks, (ws, xs), dict(res, workload=(f"I2_S GEMV 2560x2560 batch 1, uniform ternary, per-tensor scale U(0.5,2), "
                                        f"f32 N(0,1) activation int8-absmax quantised in-kernel, f32 output; one "
@@ -343,18 +357,20 @@ def decode_bytes_per_token(cfg, npast):
     return i2s + lm + norms + kv, {"i2s": i2s, "lm_head": lm, "norms": norms, "kv": kv}
 
 
-def measure_decode(amd, dev, tokens=128, warm=8, graph=True, inflight=None):
+def measure_decode(amd, dev, tokens=128, warm=8, graph=True, inflight=None, runs=3):
     """The decode step at BitNet-2B shape on the device's own greedy loop
-    (one HIP graph per token, the output kernel feeding the next token): the
+    (one HIP graph per token, the argmax kernel feeding the next token): the
     first token after the prefix is traced for the CPU leg's bit-exact check,
-    then `warm` untimed and `tokens` timed tokens. Every generated id is kept
-    for the CPU leg's token witness. inflight: tokens the loop keeps enqueued
-    ahead of the host (the library's default when None)."""
+    then `warm` untimed tokens and `runs` timed runs of `tokens` tokens each,
+    one after the other (tokens/s: the median run, and the best). Every
+    generated id is kept for the CPU leg's token witness. inflight: tokens
+    the loop keeps enqueued ahead of the host (the library's default when
+    None)."""
     cfg = dict(amd.BITNET_2B)
     t0 = time.perf_counter()
     model = amd.synth_model(cfg, 0)
     k, v = decode_prefix(amd, cfg, DECODE_PREFIX)
-    g = amd.DeviceDecoder(dev, model, DECODE_PREFIX + 1 + warm + tokens + 8)
+    g = amd.DeviceDecoder(dev, model, DECODE_PREFIX + 1 + warm + runs * tokens + 8)
     g.kv_load(k, v, DECODE_PREFIX)
     log(f"decode model and {DECODE_PREFIX}-position prefix ready in {time.perf_counter() - t0:.1f}s")
     tok0 = 128000 % cfg["n_vocab"]
@@ -367,31 +383,42 @@ def measure_decode(amd, dev, tokens=128, warm=8, graph=True, inflight=None):
         g.set_inflight(inflight)
     warm_ids = g.generate([], warm)
     dev.events(2)
-    dev.sync()
-    t0 = time.perf_counter()
-    dev.record(0)
-    ids = g.generate([], tokens)
-    dev.record(1)
-    wall = time.perf_counter() - t0
-    ms = dev.elapsed(0, 1)
+    ids, run_ms, walls = [], [], []
+    for _ in range(runs):
+        dev.sync()
+        t0 = time.perf_counter()
+        dev.record(0)
+        ids += list(g.generate([], tokens))
+        dev.record(1)
+        walls.append(time.perf_counter() - t0)
+        run_ms.append(dev.elapsed(0, 1))
     g.close()
+    ms = float(np.median(run_ms))
     tok_s = tokens / (ms * 1e-3)
+    wall = float(np.median(walls))
     pos_first = DECODE_PREFIX + 1 + warm
-    npast_mean = pos_first + 1 + (tokens - 1) / 2
+    npast_mean = pos_first + 1 + (runs * tokens - 1) / 2
     bpt, parts = decode_bytes_per_token(cfg, npast_mean)
+    # the same token with a binary16 KV cache (the bytes BASELINE's 6,360
+    # tokens/s roofline is quoted on): parity needs the f32 cache
+    bpt16 = bpt - parts["kv"] // 2
     check = {"model": model, "k": k, "v": v, "token": tok0, "logits": logits0, "dots": dots0, "acts": acts0,
              "ids": [int(x) for x in warm_ids] + [int(x) for x in ids]}
     return check, {
         "workload": (f"random-init BitNet-b1.58-2B (30 blocks, 2560/6912, 20x128 heads, 5 KV heads, F16 128256 x 2560 "
                      f"output), KV cache of {DECODE_PREFIX} binary16 N(0,1) positions, greedy decode at positions "
-                     f"{pos_first}..{pos_first + tokens - 1}, batch 1, "
+                     f"{pos_first}..{pos_first + runs * tokens - 1} ({runs} runs of {tokens}), batch 1, "
                      + ("one HIP graph per token" if graph else "the token's launches enqueued one by one")
                      + ("" if inflight is None else f", at most {inflight} token(s) enqueued ahead")),
         "tokens_per_s": round(tok_s, 1), "us_per_token": round(ms * 1e3 / tokens, 1),
-        "wall_tokens_per_s": round(tokens / wall, 1), "tokens": tokens,
+        "tokens_per_s_best": round(tokens / (min(run_ms) * 1e-3), 1),
+        "run_tokens_per_s": [round(tokens / (r_ * 1e-3), 1) for r_ in run_ms],
+        "wall_tokens_per_s": round(tokens / wall, 1), "tokens": tokens, "runs": runs,
         "bytes_per_token": int(bpt), "bytes_parts": {a: int(b) for a, b in parts.items()},
         "effective_GBps": round(bpt * tok_s / 1e9, 1), "roofline_tokens_per_s": round(PEAK_HBM_GBS * 1e9 / bpt, 1),
         "frac_of_roofline": round(tok_s * bpt / (PEAK_HBM_GBS * 1e9), 4),
+        "roofline_f16kv_tokens_per_s": round(PEAK_HBM_GBS * 1e9 / bpt16, 1),
+        "frac_of_f16kv_roofline": round(tok_s * bpt16 / (PEAK_HBM_GBS * 1e9), 4),
         "launches_per_token": 6 * cfg["n_layer"] + 2,
     }
 
@@ -417,9 +444,9 @@ def measure_prefill(amd, dev, model, reps=5):
     n = PREFILL_TOKENS
     toks = [int(t) for t in np.random.default_rng(90).integers(0, cfg["n_vocab"], n)]
     g = amd.DeviceDecoder(dev, model, n + 8)
-    res = {}
+    res, med = {}, {}
     for label, logits in (("last", False), ("all", True)):
-        best = None
+        times = []
         for _ in range(reps):
             g.reset()
             dev.events(2)
@@ -428,9 +455,8 @@ def measure_prefill(amd, dev, model, reps=5):
             g.forward_chunk(toks, 0, logits=logits)
             dev.record(1)
             dev.sync()
-            ms = dev.elapsed(0, 1)
-            best = ms if best is None or ms < best else best
-        res[label] = best
+            times.append(dev.elapsed(0, 1))
+        res[label], med[label] = min(times), float(np.median(times))
     g.reset()
     full = g.forward_chunk(toks, 0, logits=True)
     g.close()
@@ -441,9 +467,10 @@ def measure_prefill(amd, dev, model, reps=5):
         "workload": (f"random-init BitNet-b1.58-2B, one chunk of {n} tokens at positions 0..{n - 1} "
                      f"(sllm_gfx950_forward_chunk), batch 1"),
         "tokens": n,
-        "ms_last_logits": round(res["last"], 3),
+        "ms_last_logits": round(res["last"], 3), "ms_last_logits_median": round(med["last"], 3), "reps": reps,
         "tokens_per_s": round(n / (res["last"] * 1e-3), 1),
         "ms_all_logits_incl_host_copy": round(res["all"], 3),
+        "ms_all_logits_incl_host_copy_median": round(med["all"], 3),
         "all_logits_tokens_per_s": round(n / (res["all"] * 1e-3), 1),
     }
 
@@ -478,24 +505,16 @@ def measure_gemm(amd, dev):
             checks.append((ws[0], n_rows, k, x, m, pick, yd[pick], dd[pick], f"gemm {n_rows}x{k} m={m}"))
             rot = iter(range(1 << 30))
             settle(dev, lambda: dev.gemm(bws[next(rot) % GEMM_SETS].vp, n_rows, k, bq.vp, ba.vp, m, by.vp))
-            dev.events(2)
-            reps = 4 * GEMM_SETS
-            dev.record(0)
-            for i in range(reps):
-                dev.gemm(bws[i % GEMM_SETS].vp, n_rows, k, bq.vp, ba.vp, m, by.vp)
-            dev.record(1)
-            mfma_us = dev.elapsed(0, 1) * 1e3 / reps
+            bt_m = timed_batches(dev, lambda: dev.gemm(bws[next(rot) % GEMM_SETS].vp, n_rows, k, bq.vp, ba.vp, m, by.vp),
+                           8, GEMM_SETS)
+            mfma_us = bt_m["median_us"]
             plans = [dev.plan([amd.GemvJob(bws[i].ptr, n_rows, k, bx.ptr + 4 * k * t, None, None, by.ptr + 4 * n_rows * t,
                                            None) for t in range(m)]) for i in range(GEMM_SETS)]
             for p in plans:
                 dev.plan_run(p)
             dev.sync()
-            reps_g = 2 * GEMM_SETS
-            dev.record(0)
-            for i in range(reps_g):
-                dev.plan_run(plans[i % GEMM_SETS])
-            dev.record(1)
-            gemv_us = dev.elapsed(0, 1) * 1e3 / reps_g
+            bt_g = timed_batches(dev, lambda: dev.plan_run(plans[next(rot) % GEMM_SETS]), 4, GEMM_SETS)
+            gemv_us = bt_g["median_us"]
             for p in plans:
                 dev.plan_destroy(p)
             for b in (bx, bq, ba, by, bi):
@@ -506,6 +525,8 @@ def measure_gemm(amd, dev):
                          "mfma_TOPS": round(ops / mfma_us / 1e6, 1),
                          "mfma_frac_int8_peak": round(ops / mfma_us / 1e6 / PEAK_INT8_TOPS, 4),
                          "mfma_GBps": round(byts / mfma_us / 1e3, 1), "gemv_plan_us": round(gemv_us, 2),
+                         "mfma_best_us": bt_m["best_us"], "mfma_batch_us": bt_m["batch_us"],
+                         "gemv_plan_best_us": bt_g["best_us"],
                          "faster": "mfma" if mfma_us < gemv_us else "gemv"})
             log(f"gemm {n_rows}x{k} m={m}: mfma {mfma_us:.2f} us ({ops / mfma_us / 1e6:.1f} TOPS), gemv plan {gemv_us:.2f} us")
         for b in bws:
@@ -542,14 +563,8 @@ def measure_gemm_plan(amd, dev, wl, token_counts=(4, 16, 64)):
                 jobs.append((wl.jobs[3 * s + t_].w, n_rows, n, q, a, outs[3 * s + t_].ptr, None))
         plan = dev.gemm_plan(jobs, m)
         settle(dev, lambda: dev.gemm_plan_run(plan), batch=10)
-        dev.sync()
-        dev.events(2)
-        reps = 20
-        dev.record(0)
-        for _ in range(reps):
-            dev.gemm_plan_run(plan)
-        dev.record(1)
-        plan_us = dev.elapsed(0, 1) * 1e3 / reps
+        bt_p = timed_batches(dev, lambda: dev.gemm_plan_run(plan), 8, 10)
+        plan_us = bt_p["median_us"]
         # the same tensors one sllm_gfx950_gemm at a time, for the check
         ref = dev.alloc(4 * m * N_FF)
         for s in (0, wl.sets - 1):
@@ -573,13 +588,8 @@ def measure_gemm_plan(amd, dev, wl, token_counts=(4, 16, 64)):
                                              outs[3 * s + t_].ptr + 4 * t * n_rows, None))
         gplan = dev.plan(gjobs)
         dev.plan_run(gplan)
-        dev.sync()
-        greps = 3
-        dev.record(0)
-        for _ in range(greps):
-            dev.plan_run(gplan)
-        dev.record(1)
-        gemv_us = dev.elapsed(0, 1) * 1e3 / greps
+        bt_g = timed_batches(dev, lambda: dev.plan_run(gplan), 3, 1)
+        gemv_us = bt_g["median_us"]
         dev.plan_destroy(gplan)
         for b in [bxu, bxd, bqu, bqd, bau, bad] + outs:
             b.free()
@@ -588,7 +598,10 @@ def measure_gemm_plan(amd, dev, wl, token_counts=(4, 16, 64)):
         ops = 2.0 * m * sum(n_rows * n for _, n_rows, n in SHAPES) * wl.sets
         rows.append({"tokens": m, "tensors": len(jobs), "plan_us": round(plan_us, 2),
                      "plan_GBps": round(byts / plan_us / 1e3, 1), "plan_TOPS": round(ops / plan_us / 1e6, 1),
-                     "gemv_plan_us": round(gemv_us, 2), "faster": "mfma" if plan_us < gemv_us else "gemv"})
+                     "plan_best_us": bt_p["best_us"], "plan_GBps_best": round(byts / bt_p["best_us"] / 1e3, 1),
+                     "plan_batch_us": bt_p["batch_us"], "bytes": byts,
+                     "gemv_plan_us": round(gemv_us, 2), "gemv_plan_best_us": bt_g["best_us"],
+                     "faster": "mfma" if plan_us < gemv_us else "gemv"})
         log(f"gemm plan, 96 tensors x {m} tokens: {plan_us:.1f} us ({byts / plan_us / 1e3:.0f} GB/s), "
             f"GEMV plan {gemv_us:.1f} us")
     return rows
@@ -623,6 +636,50 @@ def settle(dev, launch, batch=25, max_batches=80, tol=0.005, min_ms=25.0):
             "last_batch_us": round(hist[-1], 2)}
 
 
+def timed_batches(dev, run, n_batches, per_batch):
+    """Microseconds per call of `run`: n_batches batches of per_batch
+    back-to-back calls, HIP events on the library stream at each batch's
+    edges. Returns median, best and every batch's mean (the reference's
+    tgbench reports best / median / spread the same way,
+    bench/tg_bench.c:256-333)."""
+    dev.events(2)
+    us = []
+    for _ in range(n_batches):
+        dev.sync()
+        dev.record(0)
+        for _ in range(per_batch):
+            run()
+        dev.record(1)
+        dev.sync()
+        us.append(dev.elapsed(0, 1) * 1e3 / per_batch)
+    return {"median_us": round(float(np.median(us)), 2), "best_us": round(min(us), 2),
+            "batch_us": [round(u, 2) for u in us], "per_batch": per_batch}
+
+
+def with_rate(b, byts):
+    """A timed_batches() record with GB/s at its median and best."""
+    return dict(b, GBps_median=round(byts / b["median_us"] / 1e3, 1), GBps_best=round(byts / b["best_us"] / 1e3, 1))
+
+
+def measure_ffn_sets(amd, dev, wl):
+    """Config 1 in its per-set form: one launch per weight set (gate, up and
+    down of one set as a three-job plan, gate and up sharing the quantised
+    input), the 32 sets rotated launch after launch, many back-to-back
+    launches. Bytes per launch: one set's share of the headline's."""
+    plans = [dev.plan(wl.jobs[3 * s_:3 * s_ + 3]) for s_ in range(wl.sets)]
+    rot = iter(range(1 << 40))
+    run = lambda: dev.plan_run(plans[next(rot) % wl.sets])  # noqa: E731
+    st = settle(dev, run)
+    b = timed_batches(dev, run, 10, 10 * wl.sets)
+    for p_ in plans:
+        dev.plan_destroy(p_)
+    per_set = wl.step_bytes // wl.sets
+    return dict(with_rate(b, per_set), bytes_per_launch=per_set, settle=st,
+                frac_of_peak_median=round(per_set / b["median_us"] / 1e3 / PEAK_HBM_GBS, 4),
+                workload=("the FFN workload one set per launch: gate + up (shared int8 input) + down of one of the "
+                          f"{wl.sets} sets, sets rotated, {10 * wl.sets} launches per batch"))
+
+
 def measure_copy_bandwidth(dev, nbytes=2 << 30, reps=20):
     """Plain device copy and read-only checksum of known size: the achievable
     HBM figure beside the GEMV."""
@@ -654,7 +711,7 @@ def host_cpu():
         allowed = sorted(os.sched_getaffinity(0))
     except AttributeError:
         allowed = list(range(os.cpu_count() or 1))
-    model, cores = "", set()
+    model, cores, ident, flags = "", set(), {}, set()
     try:
         for block in open("/proc/cpuinfo").read().split("\n\n"):
             d = {}
@@ -665,12 +722,18 @@ def host_cpu():
             if "processor" not in d or int(d["processor"]) not in allowed:
                 continue
             model = model or d.get("model name", "")
+            if not ident:
+                ident = {k_: d.get(k_) for k_ in ("vendor_id", "cpu family", "model", "stepping", "microcode",
+                                                  "cache size", "cpu MHz")}
+                flags = set(d.get("flags", "").split())
             cores.add((d.get("physical id", "0"), d.get("core id", d["processor"])))
     except OSError:
         pass
     top = min(16, len(allowed))
-    return {"cpu": model, "logical_cpus": len(allowed), "physical_cores": len(cores) or None,
-            "thread_counts": sorted({1, min(4, top), top})}
+    # the ISA the reference's dot selects on (src/i2s_gemm.c:292-363)
+    isa = [f for f in ("avx2", "fma", "f16c", "avx_vnni", "avx512f", "avx512_vnni", "avx512_bf16") if f in flags]
+    return {"cpu": model, "cpu_id": ident, "isa": isa, "logical_cpus": len(allowed),
+            "physical_cores": len(cores) or None, "thread_counts": sorted({1, min(4, top), top})}
 
 
 def cpu_decode(dec_check, seconds=10.0, thread_counts=(16,)):
@@ -964,8 +1027,8 @@ def main():
     ap.add_argument("--sustain", type=float, default=0.0,
                     help="after the timed steps, keep the headline launch running this many seconds in "
                          "batches of 2000 and report each batch's mean (a sustained-clock check; 0: off)")
-    ap.add_argument("--legs", default="cfg0,dropin,block,decode,prefill,gemm",
-                    help="comma-separated legs to run beside the headline GEMV (cfg0, dropin, block, decode, "
+    ap.add_argument("--legs", default="cfg0,sets,dropin,block,decode,prefill,gemm",
+                    help="comma-separated legs to run beside the headline GEMV (cfg0, sets, dropin, block, decode, "
                          "prefill, gemm); for profiling one leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1019,6 +1082,9 @@ def main():
         log(f"sustained {args.sustain:.0f} s: {len(batches)} batches of 2000 launches, "
             f"{min(batches)}..{max(batches)} us per launch, mean {sustained['mean_us']}")
 
+    # the same launch in ten batches of 100, for its median and best
+    head_batches = with_rate(timed_batches(dev, wl.step, 10, 100), wl.gemv_bytes)
+    log(f"headline in batches of 100: median {head_batches['median_us']} us, best {head_batches['best_us']} us")
     traffic, traffic_note = profiled_traffic()
 
     checks = wl.outputs([0, wl.sets - 1])
@@ -1029,6 +1095,11 @@ def main():
     dropin_checks, dropin = [], None
     if "cfg0" in legs:
         cfg0_checks, cfg0_host, cfg0 = measure_cfg0(amd, dev)
+    ffn_sets = None
+    if "sets" in legs:
+        ffn_sets = measure_ffn_sets(amd, dev, wl)
+        log(f"FFN sets one per launch: median {ffn_sets['median_us']} us ({ffn_sets['GBps_median']} GB/s), "
+            f"best {ffn_sets['best_us']} us ({ffn_sets['GBps_best']} GB/s)")
     if "dropin" in legs:
         dropin_checks, dropin = measure_dropin(amd, wl)
         dropin["device_resident_us_per_set"] = round(gemv_avg * 1e3 / SETS, 2)
@@ -1073,7 +1144,9 @@ def main():
             "avg_launch_us": round(gemv_avg * 1e3, 2), "bytes_per_launch": wl.gemv_bytes,
         },
         "settle": st,
+        "batches": head_batches,
         "sustained": sustained,
+        "ffn_sets": ffn_sets,
         "calibration": calib,
         "cfg0": cfg0,
         "dropin": dropin,

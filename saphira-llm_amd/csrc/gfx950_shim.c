@@ -108,6 +108,7 @@ struct sllm_gfx950_plan {
     uint32_t   slab_wg;        /* multiple of 8 (empty descriptors pad it) */
     uint32_t   st_wg, st_lds, st_threads;
     int        st_lpr_idx;
+    uint64_t   slab_target;    /* bytes of packed weights per slab */
 };
 
 static struct {
@@ -619,10 +620,11 @@ static int slab_path(size_t n_rows, size_t k) {
     return (uint64_t) n_rows * (k / 4) + 32 <= 0xFFFF0000u;
 }
 
-/* Slabs of a job: about slab_kib KiB of weights each, at least one group
+/* Slabs of a job: about `target` bytes of weights each, at least one group
  * each, and few enough groups per slab for its dots to fit in LDS. */
-static uint32_t slab_count(size_t n_rows, size_t k, int variant) {
-    const uint64_t target = (uint64_t) (g.slab_kib ? g.slab_kib : SLAB_DEFAULT_KIB) * 1024u;
+static uint64_t slab_default_target(void) { return (uint64_t) (g.slab_kib ? g.slab_kib : SLAB_DEFAULT_KIB) * 1024u; }
+
+static uint32_t slab_count(size_t n_rows, size_t k, int variant, uint64_t target) {
     const uint64_t group = 4u * (uint64_t) (64 / k_slab_geom[variant].lpr);
     const uint64_t n_groups = (n_rows + group - 1) / group;
     const uint64_t max_groups = SLAB_MAX_ROWS / group;
@@ -724,10 +726,10 @@ static size_t plan_scratch_bytes(const sllm_gfx950_gemv_job *jobs, size_t n_jobs
 }
 
 /* workgroups a job takes (streaming: and the rows each one owns) */
-static uint32_t job_workgroups(const k_gemv_job *kj, int slab, uint32_t *rows) {
+static uint32_t job_workgroups(const k_gemv_job *kj, int slab, uint32_t *rows, uint64_t target) {
     if (slab) {
         *rows = 0;
-        return slab_count(kj->n_rows, kj->k, (int) kj->variant);
+        return slab_count(kj->n_rows, kj->k, (int) kj->variant, target);
     }
     *rows = stream_shape_for().rows_per_wg;
     return (kj->n_rows + *rows - 1) / *rows;
@@ -779,8 +781,22 @@ static int plan_layout(const sllm_gfx950_gemv_job *jobs, size_t n_jobs, sllm_gfx
             j->act = kq[e].act;
             j->x = NULL;
         }
+    }
+    /* Slabs of the default size fill the chip with a batch of 35 MB and up;
+     * a smaller batch (one FFN set, 13 MB) gets slabs sized so that its
+     * workgroups still cover every CU once. */
+    uint64_t slab_bytes = 0;
+    for (size_t i = 0; i < n_jobs; ++i) {
+        if (is_slab[i]) slab_bytes += (uint64_t) kj[i].n_rows * (kj[i].k / 4);
+    }
+    p->slab_target = slab_default_target();
+    if (g.slab_kib == 0 && slab_bytes > 0 && slab_bytes < p->slab_target * (uint64_t) g.cu) {
+        p->slab_target = (slab_bytes + (uint64_t) g.cu - 1) / (uint64_t) g.cu;
+    }
+    for (size_t i = 0; i < n_jobs; ++i) {
+        k_gemv_job *j = &kj[i];
         uint32_t rows;
-        const uint64_t wg = job_workgroups(j, is_slab[i], &rows);
+        const uint64_t wg = job_workgroups(j, is_slab[i], &rows, p->slab_target);
         if (is_slab[i]) {
             slab_wg += wg;
         } else {
@@ -807,7 +823,7 @@ static void plan_descriptors(const sllm_gfx950_plan *p, const k_gemv_job *kj, co
     uint32_t ns = 0, nt = 0;
     for (uint32_t i = 0; i < p->n_jobs; ++i) {
         uint32_t rows;
-        const uint32_t wg = job_workgroups(&kj[i], is_slab[i], &rows);
+        const uint32_t wg = job_workgroups(&kj[i], is_slab[i], &rows, p->slab_target);
         for (uint32_t w = 0; w < wg; ++w) {
             if (is_slab[i]) {
                 sd[ns++] = (k_wg_desc) { i, w, wg, w == 0 ? WG_PUBLISH : 0 };
@@ -1017,7 +1033,7 @@ static int single_launch(const sllm_gfx950_gemv_job *j) {
     if (slab_path(kj.n_rows, kj.k)) {
         kj.variant = (uint32_t) slab_variant_for(kj.k);
         uint32_t rows, flags = 0;
-        uint32_t wg = job_workgroups(&kj, 1, &rows);
+        uint32_t wg = job_workgroups(&kj, 1, &rows, slab_default_target());
         if (g.slab_kib == 0) {
             /* The slab size targets batches, whose many jobs fill the chip;
              * a launch of its own spreads over one group of rows per
@@ -1041,7 +1057,7 @@ static int single_launch(const sllm_gfx950_gemv_job *j) {
     }
     const stream_shape ss = stream_shape_for();
     uint32_t rows;
-    const uint32_t wg = job_workgroups(&kj, 0, &rows);
+    const uint32_t wg = job_workgroups(&kj, 0, &rows, slab_default_target());
     void *args[] = { (void *) &no_jobs, (void *) &no_descs, &zero, &kj, &rows };
     return launch(g.k_stream[ss.lpr_idx], wg, (uint32_t) (64 * ss.waves), kj.k, args);
 }
@@ -1409,7 +1425,9 @@ static int pinned_reserve(uint8_t **host, uint8_t **dev, size_t *cap, size_t byt
     *host = *dev = NULL;
     *cap = 0;
     bytes = (bytes + 4095u) & ~(size_t) 4095u;
-    HIP_TRY(hipHostMalloc((void **) host, bytes, hipHostMallocDefault));
+    /* coherent (fine-grained) whatever HIP_HOST_COHERENT says: the host
+     * spins on a completion word the device stores into this memory */
+    HIP_TRY(hipHostMalloc((void **) host, bytes, hipHostMallocCoherent));
     HIP_TRY(hipHostGetDevicePointer((void **) dev, *host, 0));
     *cap = bytes;
     return SLLM_GFX950_OK;

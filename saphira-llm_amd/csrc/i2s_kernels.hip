@@ -1070,6 +1070,10 @@ sllm_k_quant_host(const float *__restrict__ x, uint32_t n, int8_t *__restrict__ 
     }
     sum = wave_sum(sum);
     if (lane == 0) red_i[wave] = sum;
+    // every wave makes its q stores visible to the host itself (a
+    // system-scope release of its own), before the barrier after which
+    // thread 0 publishes `done`: the host reads q as soon as it sees it
+    __threadfence_system();
     __syncthreads();
     if (tid == 0) {
         int t = 0;
@@ -1079,7 +1083,6 @@ sllm_k_quant_host(const float *__restrict__ x, uint32_t n, int8_t *__restrict__ 
         G_CAST(int32_t, act_dev)[1] = t;
         G_CAST(float, act_host)[0] = s;
         G_CAST(int32_t, act_host)[1] = t;
-        // every wave's q stores precede the barrier above
         __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
