@@ -320,6 +320,17 @@ int sllm_gfx950_set_tuning(int path, int variant, int lanes_per_row, int waves, 
  * A range that overlaps a registered one otherwise is refused (-1). */
 int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n);
 int sllm_gfx950_tensor_unregister(const void *packed);
+/* The kernel row's own upload on first use, standing in for a registration
+ * at load: the first sllm_gemv of a whole matrix (src/forward.c:196-205)
+ * acquires it -- uploaded as register does, unless a registered or acquired
+ * tensor already covers its n_rows*n/4 + 32 bytes (then nothing happens).
+ * A range that overlaps one otherwise is refused (-1). Acquired copies are
+ * not counted per model: release_acquired drops them all (a model still in
+ * use acquires its tensors again on its next GEMV), which the row does when
+ * a model is freed (sllm_model_free, src/forward.c:457). Registered ranges
+ * are left as they are. */
+int sllm_gfx950_tensor_acquire(const void *packed, size_t n_rows, size_t n);
+int sllm_gfx950_tensor_release_acquired(void);
 /* The device copy of a registered host address (inside any tensor), or NULL. */
 const void *sllm_gfx950_tensor_device(const void *host);
 

@@ -39,6 +39,11 @@ typedef struct sllm_kernel_row {
     int32_t (*dot)(const uint8_t *w, const int8_t *q, size_t n);
     /* include/saphira_llm/i2s_gemm.h:81-82 */
     void    (*gemv)(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q, int32_t *rows_out);
+    /* Drop what the row holds for freed models (the gfx950 row: the device
+     * copies its GEMVs uploaded), or NULL. No counterpart in the reference,
+     * whose CPU rows hold nothing: sllm_model_free (src/forward.c:457)
+     * calls it through sllm_kdispatch_release. */
+    void    (*release)(void);
 } sllm_kernel_row;
 
 #define SLLM_KDISPATCH_MAX_ROWS 8
@@ -74,6 +79,9 @@ int32_t sllm_kdispatch_dot(const uint8_t *w, const int8_t *q, size_t n);
  * takes the whole matrix in one call; there is no CPU row split here. */
 void    sllm_kdispatch_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
                             int32_t *rows_out);
+/* The installed row's release hook, where it has one (sllm_model_free,
+ * src/forward.c:457); nothing before any select. */
+void    sllm_kdispatch_release(void);
 
 #ifdef __cplusplus
 }

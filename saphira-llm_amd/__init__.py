@@ -48,7 +48,8 @@ class KernelRow(ctypes.Structure):
                 ("open", ctypes.CFUNCTYPE(c_int)),
                 ("quant_act", ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_void_p, c_void_p)),
                 ("dot", ctypes.CFUNCTYPE(c_int32, c_void_p, c_void_p, c_size_t)),
-                ("gemv", ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p))]
+                ("gemv", ctypes.CFUNCTYPE(None, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p)),
+                ("release", ctypes.CFUNCTYPE(None))]
 
 
 class LayerDesc(ctypes.Structure):
@@ -111,6 +112,8 @@ PROTOTYPES = {
     "sllm_gfx950_set_tuning": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "sllm_gfx950_tensor_register": (c_int, [c_void_p, c_size_t, c_size_t]),
     "sllm_gfx950_tensor_unregister": (c_int, [c_void_p]),
+    "sllm_gfx950_tensor_acquire": (c_int, [c_void_p, c_size_t, c_size_t]),
+    "sllm_gfx950_tensor_release_acquired": (c_int, []),
     "sllm_gfx950_tensor_device": (c_void_p, [c_void_p]),
     "sllm_gfx950_i2s_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "sllm_gfx950_i2s_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),
@@ -125,6 +128,7 @@ PROTOTYPES = {
     "sllm_kdispatch_quant_act": (None, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "sllm_kdispatch_dot": (c_int32, [c_void_p, c_void_p, c_size_t]),
     "sllm_kdispatch_gemv": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "sllm_kdispatch_release": (None, []),
     "sllm_gfx950_gemm": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "sllm_gfx950_linear_batch": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p, c_void_p,
                                          c_void_p, c_void_p]),

@@ -81,6 +81,7 @@ typedef struct reg_tensor {
     size_t         bytes;    /* n_rows*n/4 + 32 */
     uint8_t       *dev;
     size_t         refs;     /* registrations of this exact range */
+    int            acquired; /* the kernel row uploaded it on first use */
 } reg_tensor;
 
 /* One row for the list quantiser (mirror of quant_job in i2s_kernels.hip). */
@@ -1340,30 +1341,13 @@ static ptrdiff_t reg_find(const void *host) {
     return -1;
 }
 
-int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n) {
-    NEED_OPEN();
-    if (packed == NULL) return fail(SLLM_GFX950_ERR_ARG, "register: NULL tensor");
-    if (n % SLLM_GFX950_QK != 0 || n == 0) return fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "register: K=%zu is not a positive multiple of 128", n);
-    const size_t bytes = n_rows * (n / 4) + 32;
-    pthread_mutex_lock(&g_mtx);
-    int st = SLLM_GFX950_OK;
-    const uint8_t *h = packed;
-    size_t pos = 0;
-    while (pos < g.n_regs && g.regs[pos].host < h) ++pos;
-    if (pos < g.n_regs && g.regs[pos].host == h && g.regs[pos].bytes == bytes) {
-        /* a second model over the same image: share the device copy */
-        g.regs[pos].refs++;
-        goto out;
-    }
-    if ((pos < g.n_regs && g.regs[pos].host < h + bytes) ||
-        (pos > 0 && g.regs[pos - 1].host + g.regs[pos - 1].bytes > h)) {
-        st = fail(SLLM_GFX950_ERR_ARG, "register: tensor overlaps a registered one");
-        goto out;
-    }
+/* Upload [h, h + bytes) into a new registry entry at sorted position pos
+ * (g_mtx held). */
+static int reg_insert(const uint8_t *h, size_t bytes, size_t pos, size_t refs, int acquired) {
     if (g.n_regs == g.cap_regs) {
         const size_t cap = g.cap_regs ? 2 * g.cap_regs : 256;
         reg_tensor *r = realloc(g.regs, cap * sizeof *r);
-        if (r == NULL) { st = fail(SLLM_GFX950_ERR_NOMEM, "register: registry"); goto out; }
+        if (r == NULL) return fail(SLLM_GFX950_ERR_NOMEM, "register: registry");
         g.regs = r;
         g.cap_regs = cap;
     }
@@ -1372,15 +1356,83 @@ int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n) {
     if (e == hipSuccess) e = hipMemcpy(dev, h, bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         if (dev) hipFree(dev);
-        st = hip_fail(e, "register: upload");
-        goto out;
+        return hip_fail(e, "register: upload");
     }
     memmove(&g.regs[pos + 1], &g.regs[pos], (g.n_regs - pos) * sizeof *g.regs);
-    g.regs[pos] = (reg_tensor) { h, bytes, dev, 1 };
+    g.regs[pos] = (reg_tensor) { h, bytes, dev, refs, acquired };
     g.n_regs++;
-out:
+    return SLLM_GFX950_OK;
+}
+
+/* the sorted position of h, and whether [h, h + bytes) overlaps an entry */
+static size_t reg_pos(const uint8_t *h, size_t bytes, int *overlap) {
+    size_t pos = 0;
+    while (pos < g.n_regs && g.regs[pos].host < h) ++pos;
+    *overlap = (pos < g.n_regs && g.regs[pos].host < h + bytes) ||
+               (pos > 0 && g.regs[pos - 1].host + g.regs[pos - 1].bytes > h);
+    return pos;
+}
+
+int sllm_gfx950_tensor_register(const void *packed, size_t n_rows, size_t n) {
+    NEED_OPEN();
+    if (packed == NULL) return fail(SLLM_GFX950_ERR_ARG, "register: NULL tensor");
+    if (n % SLLM_GFX950_QK != 0 || n == 0) return fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "register: K=%zu is not a positive multiple of 128", n);
+    const size_t bytes = n_rows * (n / 4) + 32;
+    pthread_mutex_lock(&g_mtx);
+    int st = SLLM_GFX950_OK, overlap;
+    const uint8_t *h = packed;
+    const size_t pos = reg_pos(h, bytes, &overlap);
+    if (pos < g.n_regs && g.regs[pos].host == h && g.regs[pos].bytes == bytes) {
+        /* a second model over the same image: share the device copy */
+        g.regs[pos].refs++;
+    } else if (overlap) {
+        st = fail(SLLM_GFX950_ERR_ARG, "register: tensor overlaps a registered one");
+    } else {
+        st = reg_insert(h, bytes, pos, 1, 0);
+    }
     pthread_mutex_unlock(&g_mtx);
     return st;
+}
+
+int sllm_gfx950_tensor_acquire(const void *packed, size_t n_rows, size_t n) {
+    NEED_OPEN();
+    if (packed == NULL) return fail(SLLM_GFX950_ERR_ARG, "acquire: NULL tensor");
+    if (n % SLLM_GFX950_QK != 0 || n == 0) return fail(SLLM_GFX950_ERR_TENSOR_SHAPE, "acquire: K=%zu is not a positive multiple of 128", n);
+    const size_t bytes = n_rows * (n / 4) + 32;
+    const uint8_t *h = packed;
+    pthread_mutex_lock(&g_mtx);
+    int st = SLLM_GFX950_OK;
+    const ptrdiff_t i = reg_find(h);
+    if (i >= 0 && h + bytes <= g.regs[i].host + g.regs[i].bytes) {
+        /* already on the device: registered, or acquired by an earlier GEMV */
+    } else {
+        int overlap;
+        const size_t pos = reg_pos(h, bytes, &overlap);
+        st = overlap ? fail(SLLM_GFX950_ERR_ARG, "acquire: tensor overlaps a registered one")
+                     : reg_insert(h, bytes, pos, 0, 1);
+    }
+    pthread_mutex_unlock(&g_mtx);
+    return st;
+}
+
+int sllm_gfx950_tensor_release_acquired(void) {
+    NEED_OPEN();
+    pthread_mutex_lock(&g_mtx);
+    /* kernels reading a copy may still be in flight: wait, then free */
+    const hipError_t e = hipStreamSynchronize(g.stream);
+    size_t keep = 0;
+    for (size_t i = 0; i < g.n_regs; ++i) {
+        reg_tensor r = g.regs[i];
+        if (r.acquired && r.refs == 0) {
+            hipFree(r.dev);
+            continue;
+        }
+        r.acquired = 0;               /* registered as well: it stays, as registered */
+        g.regs[keep++] = r;
+    }
+    g.n_regs = keep;
+    pthread_mutex_unlock(&g_mtx);
+    return e != hipSuccess ? hip_fail(e, "release_acquired") : SLLM_GFX950_OK;
 }
 
 int sllm_gfx950_tensor_unregister(const void *packed) {
@@ -1390,8 +1442,9 @@ int sllm_gfx950_tensor_unregister(const void *packed) {
     int st = SLLM_GFX950_OK;
     if (i < 0 || g.regs[i].host != (const uint8_t *) packed) {
         st = fail(SLLM_GFX950_ERR_NOT_REGISTERED, "unregister: %p is not a registered tensor", packed);
-    } else if (--g.regs[i].refs == 0) {
-        /* the copy goes either way; a failed wait is still reported */
+    } else if (--g.regs[i].refs == 0 && !g.regs[i].acquired) {
+        /* the copy goes either way; a failed wait is still reported
+         * (an acquired copy stays until release_acquired) */
         const hipError_t e = hipStreamSynchronize(g.stream);
         hipFree(g.regs[i].dev);
         memmove(&g.regs[i], &g.regs[i + 1], (g.n_regs - (size_t) i - 1) * sizeof *g.regs);

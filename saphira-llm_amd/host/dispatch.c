@@ -19,9 +19,30 @@
 
 static int gfx950_open(void) { return sllm_gfx950_open(SLLM_GFX950_DEVICE); }
 
+/* sllm_gemv hands over whole matrices (src/forward.c:196-205): the first call
+ * on a matrix uploads it, so the loader need not register anything */
+static void gfx950_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q, int32_t *rows_out) {
+    if (w != NULL && q != NULL && rows_out != NULL && n_rows > 0 && n >= SLLM_GFX950_QK) {
+        const int st = sllm_gfx950_tensor_acquire(w, n_rows, n);
+        if (st != SLLM_GFX950_OK) {
+            fprintf(stderr, "sllm_kdispatch_gemv: the gfx950 row cannot take the weights at %p (%d): %s\n",
+                    (const void *) w, st, sllm_gfx950_last_error());
+            abort();
+        }
+    }
+    sllm_gfx950_i2s_gemv(w, n_rows, n, q, rows_out);
+}
+
+static void gfx950_release(void) {
+    const int st = sllm_gfx950_tensor_release_acquired();
+    if (st != SLLM_GFX950_OK && st != SLLM_GFX950_ERR_NO_DEVICE) {
+        fprintf(stderr, "sllm_kdispatch_release: %s\n", sllm_gfx950_last_error());
+    }
+}
+
 static const sllm_kernel_row k_gfx950_row = {
     "gfx950", 100, gfx950_open,
-    sllm_gfx950_i2s_quant_act, sllm_gfx950_i2s_dot, sllm_gfx950_i2s_gemv,
+    sllm_gfx950_i2s_quant_act, sllm_gfx950_i2s_dot, gfx950_gemv, gfx950_release,
 };
 
 static sllm_kernel_row g_rows[SLLM_KDISPATCH_MAX_ROWS] = { k_gfx950_row };
@@ -103,4 +124,8 @@ int32_t sllm_kdispatch_dot(const uint8_t *w, const int8_t *q, size_t n) {
 void sllm_kdispatch_gemv(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
                          int32_t *rows_out) {
     need_row("sllm_kdispatch_gemv")->gemv(w, n_rows, n, q, rows_out);
+}
+
+void sllm_kdispatch_release(void) {
+    if (g_installed != NULL && g_installed->release != NULL) g_installed->release();
 }

@@ -125,6 +125,7 @@ def test_dispatch_table_rules(amd):
     row.quant_act = row._fields_[3][1](lambda x, n, q, a: calls.append(("quant", n)))
     row.dot = row._fields_[4][1](lambda w, q, n: calls.append(("dot", n)) or 7)
     row.gemv = row._fields_[5][1](lambda w, r, n, q, o: calls.append(("gemv", r, n)))
+    row.release = row._fields_[6][1](lambda: calls.append(("release",)))
     test_dispatch_table_rules._keep = row      # callbacks must outlive the table
     if lib.sllm_kdispatch_count() == 1:
         assert lib.sllm_kdispatch_register(ctypes.byref(row)) == 0
@@ -135,8 +136,11 @@ def test_dispatch_table_rules(amd):
     assert lib.sllm_kdispatch_installed_name() == b"test-stub"
     assert lib.sllm_kdispatch_dot(None, None, 256) == 7
     lib.sllm_kdispatch_gemv(None, 3, 384, None, None)
-    assert calls[-2:] == [("dot", 256), ("gemv", 3, 384)]
+    lib.sllm_kdispatch_release()
+    assert calls[-3:] == [("dot", 256), ("gemv", 3, 384), ("release",)]
     lib.sllm_kdispatch_reset()
+    lib.sllm_kdispatch_release()                   # nothing installed: nothing happens
+    assert calls[-1] == ("release",) and len([c for c in calls if c == ("release",)]) == 1
 
 
 # ---------------------------------------------------------------------------

@@ -68,14 +68,18 @@ def test_patch_only_inserts_conditional_lines():
 
 
 def test_patch_touches_the_documented_sites():
-    """Row selection at load, seven registrations, the GEMV, four quantiser
-    calls, release in both error paths and in sllm_model_free."""
+    """Row selection at load, the GEMV, four quantiser calls and the release
+    hook in sllm_model_free: nothing in the loader (the row uploads each
+    matrix on its first GEMV)."""
     body = "\n".join("\n".join(lines) for _, lines in _hunks())
     assert body.count('sllm_kdispatch_select("gfx950")') == 1
-    assert body.count("sllm_gfx950_tensor_register(") == 7
     assert body.count("sllm_kdispatch_gemv(") == 1
     assert body.count("sllm_kdispatch_quant_act(") == 4
-    assert body.count("gfx950_release(m);") == 3
+    assert body.count("sllm_kdispatch_release();") == 1
+    assert "sllm_gfx950_tensor_register" not in body and "gfx950_release" not in body
+    # eight sites: the include / layout check, the GEMV, the select, sllm_model_free
+    # (two hunks) and the four quantisers (two hunks each)
+    assert len(_hunks()) == 13
 
 
 def test_patched_reference_refuses_without_a_device(amd, orc):

@@ -236,6 +236,11 @@ def scenarios(E):
     # the device copy goes even when the wait before freeing it fails
     add("tensor_unregister", lambda: st(L.sllm_gfx950_tensor_unregister(P(E.w_host))),
         prepare=lambda: L.sllm_gfx950_tensor_register(P(E.w_host), nr, n), freed=1)
+    # the kernel row's upload on first use, and the release hook
+    add("tensor_acquire", lambda: st(L.sllm_gfx950_tensor_acquire(P(E.w_host), nr, n)),
+        cleanup=lambda _: L.sllm_gfx950_tensor_release_acquired())
+    add("tensor_release_acquired", lambda: st(L.sllm_gfx950_tensor_release_acquired()),
+        prepare=lambda: L.sllm_gfx950_tensor_acquire(P(E.w_host), nr, n), freed=1)
 
     # decode
     def upload():
@@ -344,8 +349,8 @@ def test_every_failed_allocation_returns_nomem(env):
         points[name] = (_sweep(env.L, name, *s, "hipMalloc", HIP_OUT_OF_MEMORY, NOMEM) +
                         _sweep(env.L, name, *s, "hipHostMalloc", HIP_OUT_OF_MEMORY, NOMEM))
     # the calls that allocate were driven through their allocations
-    for name in ("malloc", "plan_create", "gemv_batch", "tensor_register", "model_upload", "model_load_gguf",
-                 "ctx_new", "gemm_plan_create"):
+    for name in ("malloc", "plan_create", "gemv_batch", "tensor_register", "tensor_acquire", "model_upload",
+                 "model_load_gguf", "ctx_new", "gemm_plan_create"):
         assert points[name] > 0, name
 
 
@@ -431,6 +436,8 @@ calls = {{
   "gemm_plan_run": lambda: L.sllm_gfx950_gemm_plan_run(None),
   "tensor_register": lambda: L.sllm_gfx950_tensor_register(None, 1, 128),
   "tensor_unregister": lambda: L.sllm_gfx950_tensor_unregister(None),
+  "tensor_acquire": lambda: L.sllm_gfx950_tensor_acquire(None, 1, 128),
+  "tensor_release_acquired": lambda: L.sllm_gfx950_tensor_release_acquired(),
   "device_info": lambda: L.sllm_gfx950_device_info(None, 0, None, None),
   "model_upload": lambda: L.sllm_gfx950_model_upload(None, ctypes.byref(p)),
   "model_load_gguf": lambda: L.sllm_gfx950_model_load_gguf(image.ctypes.data_as(V), image.size, ctypes.byref(p)),

@@ -1,11 +1,10 @@
 """The reference's own forward pass with the gfx950 row installed.
 
 oracle/gfx950_forward.patch is the integration a maintainer applies to the
-reference's src/forward.c: select the row at model load (after :334),
-register each I2_S tensor where the loader accepts it (after :399-423),
-send sllm_gemv (:196-205) and the four quantiser calls (:651, :737, :763,
-:788) through sllm_kdispatch_*, and release the device copies in the load's
-error paths and sllm_model_free. The oracle recipe applies it to a copy of
+reference's src/forward.c: select the row at model load (after :334), send
+sllm_gemv (:196-205) and the four quantiser calls (:651, :737, :763, :788)
+through sllm_kdispatch_*, and let sllm_model_free (:457) call the row's
+release hook. The row uploads each matrix on its first GEMV. The oracle recipe applies it to a copy of
 forward.c and builds oracle/_ref/libsllm_ref_gfx950.so beside the unpatched
 oracle/_ref/libsllm_ref.so. Both run the reference's own sllm_forward; one
 reaches its CPU kernels, the other the GPU row. The row returns the CPU
@@ -95,40 +94,55 @@ def test_patched_forward_matches_reference_2b_block(amd, orc, patched):
         gpu.close()
 
 
-def test_patched_load_registers_shares_and_releases(amd, orc, patched):
-    """The patched load uploads every I2_S tensor; a second model over the
-    same image shares the device copies; closing one model leaves the other
-    whole; closing the last drops them."""
+def test_row_uploads_on_first_gemv_and_releases_with_the_model(amd, orc, patched):
+    """The patched load uploads nothing; the first forward step's GEMVs
+    upload every I2_S tensor of the model (the row's first whole-matrix
+    sllm_gemv); a second model over the same image uses the same copies;
+    freeing one model drops the row's copies and the other, still open,
+    uploads its tensors again on its next GEMV, its logits still the
+    reference's bit for bit; freeing the last leaves nothing on the device."""
     from oracle.gguf_synth import gguf_image
     model = amd.synth_model(TINY, 46)
     image = np.frombuffer(gguf_image(model), np.uint8)
     weights = _weights(amd, image)
     assert len(weights) == 7 * TINY["n_layer"]
     dev_of = amd.lib().sllm_gfx950_tensor_device
-    assert not any(dev_of(ctypes.c_void_p(w)) for w in weights)
+    on_device = lambda: [bool(dev_of(ctypes.c_void_p(w))) for w in weights]  # noqa: E731
+    assert not any(on_device())
     st = ctypes.c_int()
     r1 = patched.ref_model_open(orc._p(image), image.nbytes, ctypes.byref(st))
     assert r1, st.value
-    r2 = None
+    r2 = c1 = c2 = None
+    cpu = orc.RefDecoder(model, 16)
+    toks = _tokens(4, TINY["n_vocab"], 47)
+
+    def step(r, c, pos):
+        got = np.empty(TINY["n_vocab"], np.float32)
+        assert patched.ref_forward(r, c, toks[pos], pos, orc._p(got)) == 0
+        return got
     try:
-        assert all(dev_of(ctypes.c_void_p(w)) for w in weights)
+        assert not any(on_device())                  # the load registers nothing
+        c1 = patched.ref_ctx_new(r1, 16)
+        want0 = cpu.forward(toks[0], 0)
+        assert np.array_equal(bits(step(r1, c1, 0)), bits(want0))
+        assert all(on_device())                      # the first step's GEMVs uploaded every tensor
         r2 = patched.ref_model_open(orc._p(image), image.nbytes, ctypes.byref(st))
         assert r2, st.value
+        c2 = patched.ref_ctx_new(r2, 16)
+        assert np.array_equal(bits(step(r2, c2, 0)), bits(want0))
+        patched.ref_ctx_free(c1)
+        c1 = None
         patched.ref_model_close(r1)
         r1 = None
-        assert all(dev_of(ctypes.c_void_p(w)) for w in weights)
-        c = patched.ref_ctx_new(r2, 16)
-        cpu = orc.RefDecoder(model, 16)
-        try:
-            for pos, t in enumerate(_tokens(4, TINY["n_vocab"], 47)):
-                got = np.empty(TINY["n_vocab"], np.float32)
-                assert patched.ref_forward(r2, c, t, pos, orc._p(got)) == 0
-                assert np.array_equal(bits(got), bits(cpu.forward(t, pos))), pos
-        finally:
-            patched.ref_ctx_free(c)
-            cpu.close()
+        assert not any(on_device())                  # freeing a model drops the row's copies
+        for pos in range(1, len(toks)):
+            assert np.array_equal(bits(step(r2, c2, pos)), bits(cpu.forward(toks[pos], pos))), pos
+        assert all(on_device())                      # uploaded again for the model still open
     finally:
-        for r in (r1, r2):
+        cpu.close()
+        for c, r in ((c1, r1), (c2, r2)):
+            if c:
+                patched.ref_ctx_free(c)
             if r:
                 patched.ref_model_close(r)
-    assert not any(dev_of(ctypes.c_void_p(w)) for w in weights)
+    assert not any(on_device())
