@@ -940,16 +940,23 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         /* l_out of the layer below (cproj + cffn_inp), or the embedding; attn_norm */
         st = il == 0 ? prep(c, n, IN_EMBED, m->tok_embd, NULL, B->x, L->attn_norm, (uint32_t) e, 1, NULL)
                      : prep(c, n, IN_RESID, B->proj, B->fi, B->x, L->attn_norm, (uint32_t) e, 1, NULL);
-        if (st == SLLM_GFX950_OK) {
-            const sllm_gfx950_gemm_job qkv[3] = { { L->w[P_Q], e, B->q, NULL }, { L->w[P_K], g, B->k, NULL },
-                                                  { L->w[P_V], g, B->v, NULL } };
-            st = sllm_gfx950_gemm_multi(qkv, 3, e, B->q8, B->act, (size_t) n);
-        }
         k_dec_attn A = c->attn_args[il];
         A.q = B->q; A.k = B->k; A.v = B->v; A.scores = B->scores; A.out = B->attn;
         A.chunk_base = (uint32_t) base;
+        /* Q, K, V; where the GEMM's row tiles hold whole heads its epilogue
+         * also ropes the queries and stores the keys and values, else
+         * sllm_k_chk_kv_store does */
+        int store = 1;
+        if (st == SLLM_GFX950_OK) {
+            const sllm_gfx950_gemm_job qkv[3] = { { L->w[P_Q], e, B->q, NULL }, { L->w[P_K], g, B->k, NULL },
+                                                  { L->w[P_V], g, B->v, NULL } };
+            const k_gemm_rope R = { A.rope, A.k_cache, A.v_cache, A.n_ctx, A.hd, A.half, (uint32_t) base };
+            st = sllm_shim_gemm_qkv_rope(qkv, e, B->q8, B->act, (size_t) n, &R);
+            if (st == SLLM_SHIM_NOT_FUSED) st = sllm_gfx950_gemm_multi(qkv, 3, e, B->q8, B->act, (size_t) n);
+            else store = 0;
+        }
         void *aargs[] = { &A };
-        if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_kvs, (uint32_t) n, 1, ATT_THREADS, 0, aargs);
+        if (st == SLLM_GFX950_OK && store) st = sllm_shim_launch(c->f_kvs, (uint32_t) n, 1, ATT_THREADS, 0, aargs);
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;
             void *sargs[] = { &A, &n_tok };

@@ -125,6 +125,7 @@ static struct {
     hipFunction_t  k_copy;
     hipFunction_t  k_gemm[15];
     hipFunction_t  k_gemm_t[5];
+    hipFunction_t  k_gemm_rope[2];       /* dk2x2, dk4x4 with the chunk's cache store */
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -245,6 +246,8 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[12], g.mod, "sllm_k_gemm_dk2x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[13], g.mod, "sllm_k_gemm_dq1x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[14], g.mod, "sllm_k_gemm_dq2x1"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_rope[0], g.mod, "sllm_k_gemm_dk2x2_rope"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_rope[1], g.mod, "sllm_k_gemm_dk4x4_rope"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[0], g.mod, "sllm_k_gemm_tdl1x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[1], g.mod, "sllm_k_gemm_tdl2x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[2], g.mod, "sllm_k_gemm_tdk2x2"));
@@ -1122,9 +1125,12 @@ int sllm_gfx950_set_gemm_tile(int tile) {
     return SLLM_GFX950_OK;
 }
 
-int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t n, const int8_t *q,
-                           const sllm_gfx950_act *act, size_t m) {
-    NEED_OPEN();
+/* The launch of a GEMM over 1 to 3 jobs: arguments checked, tile shape
+ * chosen, gemm_args filled. SLLM_GFX950_OK with *gx == 0: nothing to do. */
+static int gemm_prepare(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t n, const int8_t *q,
+                        const sllm_gfx950_act *act, size_t m, k_gemm_args *a, int *tile_out, uint64_t *gx_out,
+                        uint64_t *gy_out) {
+    *gx_out = 0;
     if (jobs == NULL || n_jobs < 1 || n_jobs > 3) return fail(SLLM_GFX950_ERR_ARG, "gemm: 1 to 3 jobs");
     if (m == 0) return SLLM_GFX950_OK;
     if (q == NULL || ((uintptr_t) q & 15u) != 0) return fail(SLLM_GFX950_ERR_ARG, "gemm: q must be given and 16-byte aligned");
@@ -1156,24 +1162,57 @@ int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size
     }
     if (tile >= 3 && n % 256 != 0) tile = 2;
     const uint32_t rows_per_wg = k_gemm_rows[tile], tok_per_wg = k_gemm_tokens[tile];
-    k_gemm_args a;
-    memset(&a, 0, sizeof a);
+    memset(a, 0, sizeof *a);
     uint64_t gx = 0;
     for (size_t j = 0; j < 3; ++j) {
         const size_t jj = j < n_jobs ? j : n_jobs - 1;      /* unused slots repeat the last job, no tiles */
-        a.w[j] = jobs[jj].w;
-        a.out[j] = jobs[jj].out;
-        a.out_i[j] = jobs[jj].rows_out;
-        a.n_rows[j] = (uint32_t) jobs[jj].n_rows;
-        a.tiles[j] = j < n_jobs ? (uint32_t) ((jobs[j].n_rows + rows_per_wg - 1) / rows_per_wg) : 0u;
-        gx += a.tiles[j];
+        a->w[j] = jobs[jj].w;
+        a->out[j] = jobs[jj].out;
+        a->out_i[j] = jobs[jj].rows_out;
+        a->n_rows[j] = (uint32_t) jobs[jj].n_rows;
+        a->tiles[j] = j < n_jobs ? (uint32_t) ((jobs[j].n_rows + rows_per_wg - 1) / rows_per_wg) : 0u;
+        gx += a->tiles[j];
     }
-    a.q = q; a.act = act; a.k = (uint32_t) n; a.m = (uint32_t) m; a.n_jobs = (uint32_t) n_jobs;
+    a->q = q; a->act = act; a->k = (uint32_t) n; a->m = (uint32_t) m; a->n_jobs = (uint32_t) n_jobs;
     const uint64_t gy = (m + tok_per_wg - 1) / tok_per_wg;
-    if (gx == 0) return SLLM_GFX950_OK;
     if (gx > INT32_MAX || gy > 65535) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm: grid too large");
+    *tile_out = tile;
+    *gx_out = gx;
+    *gy_out = gy;
+    return SLLM_GFX950_OK;
+}
+
+int sllm_gfx950_gemm_multi(const sllm_gfx950_gemm_job *jobs, size_t n_jobs, size_t n, const int8_t *q,
+                           const sllm_gfx950_act *act, size_t m) {
+    NEED_OPEN();
+    k_gemm_args a;
+    int tile = 0;
+    uint64_t gx, gy;
+    const int st = gemm_prepare(jobs, n_jobs, n, q, act, m, &a, &tile, &gx, &gy);
+    if (st != SLLM_GFX950_OK || gx == 0) return st;
     void *args[] = { &a };
     HIP_TRY(hipModuleLaunchKernel(g.k_gemm[tile], (uint32_t) gx, (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
+                                  g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
+int sllm_shim_gemm_qkv_rope(const sllm_gfx950_gemm_job jobs[3], size_t n, const int8_t *q,
+                            const sllm_gfx950_act *act, size_t m, const k_gemm_rope *r) {
+    NEED_OPEN();
+    k_gemm_args a;
+    int tile = 0;
+    uint64_t gx, gy;
+    const int st = gemm_prepare(jobs, 3, n, q, act, m, &a, &tile, &gx, &gy);
+    if (st != SLLM_GFX950_OK || gx == 0) return st;
+    const int which = tile == 12 ? 0 : (tile == 9 ? 1 : -1);
+    if (which < 0 || r->hd == 0 || k_gemm_rows[tile] % r->hd != 0 || r->half == 0 || r->half % 4 != 0 ||
+        2 * r->half > r->hd || r->hd % 8 != 0)
+        return SLLM_SHIM_NOT_FUSED;
+    for (int j = 0; j < 3; ++j)
+        if (jobs[j].out == NULL || jobs[j].rows_out != NULL || jobs[j].n_rows % r->hd != 0) return SLLM_SHIM_NOT_FUSED;
+    k_gemm_rope rr = *r;
+    void *args[] = { &a, &rr };
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm_rope[which], (uint32_t) gx, (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
                                   g.stream, args, NULL));
     return SLLM_GFX950_OK;
 }

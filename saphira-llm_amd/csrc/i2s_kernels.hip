@@ -349,7 +349,22 @@ struct gemm_view {
     uint32_t       n_rows, tile;
     const int8_t  *q;
     const act_t   *act;
+    uint32_t       job;
 };
+
+// A chunk's Q + K + V launch (jobs 0, 1, 2 of gemm_args) that also does the
+// attention's cache store (src/forward.c:668-690): queries and keys roped
+// at their positions (NeoX, src/ops.c:467-549), the queries in place in
+// out[0], the keys into the key cache, the values into the value cache.
+// Token t of the launch sits at position pos0 + t. The host uses it only
+// where a row tile holds whole heads (BN % hd == 0) and half % 4 == 0.
+struct gemm_rope {
+    const float *rope;          // [n_ctx][half] (cos, sin)
+    float       *k_cache;       // [n_kv][n_ctx][hd]
+    float       *v_cache;       // [n_kv][hd / 8][n_ctx][8]
+    uint32_t     n_ctx, hd, half, pos0;
+};
+static_assert(sizeof(gemm_rope) == 40, "gemm_rope must match gfx950_shim.c");
 
 // One tensor of a GEMM plan (gemm_table): its own token rows, K and
 // outputs; tile0 is its first row tile in the plan (mirrored in
@@ -376,7 +391,7 @@ __device__ __forceinline__ gemm_view gemm_pick(const gemm_args &G, uint32_t b = 
              j == 0 ? G.out[0] : (j == 1 ? G.out[1] : G.out[2]),
              j == 0 ? G.out_i[0] : (j == 1 ? G.out_i[1] : G.out_i[2]),
              j == 0 ? G.n_rows[0] : (j == 1 ? G.n_rows[1] : G.n_rows[2]),
-             b - (j == 0 ? 0u : (j == 1 ? t0 : t01)), G.q, G.act };
+             b - (j == 0 ? 0u : (j == 1 ? t0 : t01)), G.q, G.act, j };
 }
 
 template <int TM, int TN>
@@ -706,10 +721,11 @@ __device__ __forceinline__ void gemm_place(uint32_t &bx, uint32_t &by) {
 // rows of the output: a lane's accumulators hold rows 16 apart, the store
 // wants four consecutive ones per lane. The caller has drained its copies
 // into S.
-template <int TM, int TN, int KG>
+template <int TM, int TN, int KG, bool ROPE = false>
 __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &V, uint32_t m, uint32_t t0,
                                                    uint32_t n0, uint32_t wr, uint32_t kgrp, uint32_t wave_all,
-                                                   float ep_ws, act_t ep_at, i32x4v (&c)[TM][TN]) {
+                                                   float ep_ws, act_t ep_at, i32x4v (&c)[TM][TN],
+                                                   const gemm_rope *R) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
     constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -734,6 +750,69 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
     constexpr uint32_t LPT = BN / 4u;               // lanes per tile row in the stores
     constexpr uint32_t RPS = 64u / LPT;             // tile rows per store instruction
     const uint32_t srow = lane / LPT, scol = 4u * (lane % LPT);
+    if constexpr (ROPE) {
+        // the tile's rows are whole heads of one job (n0 and BN multiples of
+        // hd): values go straight to the value cache; query and key floats
+        // go back into LDS (over K group 0's tile) so that each dimension
+        // finds its rotary partner, then out to the q rows / the key cache
+        constexpr uint32_t NP = BM / (4u * KG * RPS);  // rows of this lane
+        const uint32_t hd = R->hd, half = R->half;
+        const uint32_t dd = (n0 + scol) % hd;          // the lane's first dimension (of four)
+        const uint32_t e0 = dd < half ? dd : (dd < 2u * half ? dd - half : 0u);
+        float fr[NP][4];
+        f32x4 csa[NP][2];                              // (cos, sin) of dimensions dd .. dd + 3
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            const uint32_t row = wave_all * RPS + p * 4u * KG * RPS + srow, t = t0 + row, n = n0 + scol;
+            const GLOBAL float *cs = G_CAST(const float, R->rope) +
+                                     ((size_t) (R->pos0 + min(t, m - 1)) * half + e0) * 2u;
+            csa[p][0] = *reinterpret_cast<const GLOBAL f32x4 *>(cs);
+            csa[p][1] = *reinterpret_cast<const GLOBAL f32x4 *>(cs + 4);
+            i32x4v d = *reinterpret_cast<const i32x4v *>(S + (row * EP + scol) * 4u);
+#pragma unroll
+            for (uint32_t k2 = 1; k2 < (uint32_t) KG; ++k2)
+                d += *reinterpret_cast<const i32x4v *>(S + k2 * E_TILE + (row * EP + scol) * 4u);
+            const float post = post_s[row];
+            const int32_t sum = sum_s[row];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) fr[p][e] = (float) (d[e] - sum) * post;
+            if (V.job == 2 && t < m && n < V.n_rows) {
+                // slice-major: [KV head][dimension / 8][position][dimension % 8]
+                GLOBAL float *o = G_CAST(float, R->v_cache) +
+                                  (((size_t) (n / hd) * (hd / 8u) + dd / 8u) * R->n_ctx + R->pos0 + t) * 8u + dd % 8u;
+                *reinterpret_cast<GLOBAL f32x4 *>(o) = (f32x4) { fr[p][0], fr[p][1], fr[p][2], fr[p][3] };
+            }
+        }
+        if (V.job == 2) return;                         // uniform
+        __syncthreads();                                // every read of the int32 tiles done
+        float *F = reinterpret_cast<float *>(S);
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            const uint32_t row = wave_all * RPS + p * 4u * KG * RPS + srow;
+            *reinterpret_cast<f32x4 *>(F + row * EP + scol) = (f32x4) { fr[p][0], fr[p][1], fr[p][2], fr[p][3] };
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            const uint32_t row = wave_all * RPS + p * 4u * KG * RPS + srow, t = t0 + row, n = n0 + scol;
+            if (t < m && n < V.n_rows) {
+                f32x4 o;
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) {
+                    const uint32_t de = dd + e, col = scol + e, hb = col - de;
+                    const uint32_t partner = de < half ? de + half : (de < 2u * half ? de - half : de);
+                    const float x = F[row * EP + col], y = F[row * EP + hb + partner];
+                    const float cc = csa[p][e / 2u][2u * (e % 2u)], ss = csa[p][e / 2u][2u * (e % 2u) + 1u];
+                    o[e] = de < half ? x * cc - y * ss : (de < 2u * half ? y * ss + x * cc : x);
+                }
+                GLOBAL float *dst = V.job == 0
+                    ? G_CAST(float, V.out) + (size_t) t * V.n_rows + n
+                    : G_CAST(float, R->k_cache) + ((size_t) (n / hd) * R->n_ctx + R->pos0 + t) * hd + dd;
+                *reinterpret_cast<GLOBAL f32x4 *>(dst) = o;
+            }
+        }
+        return;
+    }
     const bool vec_i = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out_i & 15u) == 0;
     const bool vec_f = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out & 15u) == 0;
     // streaming stores: written through as the tiles finish rather than left
@@ -772,8 +851,9 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
 // waves on every SIMD, one of each group, so that one's waits are covered by
 // the other's MFMAs), and the groups' int32 sums meet in LDS at the end
 // (exact in any order).
-template <int TM, int TN, int STAGES, int KG = 1>
-__device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by) {
+template <int TM, int TN, int STAGES, int KG = 1, bool ROPE = false>
+__device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by,
+                                             const gemm_rope *R = nullptr) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
     constexpr uint32_t A_BYTES = BM * 256u, STAGE = A_BYTES + BN * 64u;
     constexpr int VM = TM + TN;                     // copies per wave per super-step
@@ -944,15 +1024,15 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
         }
     }
     wait_vmem<0>();                                 // no copy may land after the workgroup leaves
-    gemm_tile_epilogue<TM, TN, KG>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_at, c);
+    gemm_tile_epilogue<TM, TN, KG, ROPE>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_at, c, R);
 }
 
 // the tile of a three-job launch (gemm_args) or of a plan (gemm_table)
-template <int TM, int TN, int STAGES, int KG = 1>
-__device__ __forceinline__ void gemm_dl_block(const gemm_args &G) {
+template <int TM, int TN, int STAGES, int KG = 1, bool ROPE = false>
+__device__ __forceinline__ void gemm_dl_block(const gemm_args &G, const gemm_rope *R = nullptr) {
     uint32_t bx, by;
     gemm_place(bx, by);
-    gemm_dl_tile<TM, TN, STAGES, KG>(gemm_pick(G, bx), G.k, G.m, by);
+    gemm_dl_tile<TM, TN, STAGES, KG, ROPE>(gemm_pick(G, bx), G.k, G.m, by, R);
 }
 
 template <int TM, int TN, int STAGES, int KG = 1>
@@ -960,7 +1040,7 @@ __device__ __forceinline__ void gemm_dl_table(const gemm_table &T) {
     uint32_t bx, by;
     gemm_place(bx, by);
     const gemm_tjob &J = T.jobs[T.tile_job[bx]];
-    const gemm_view V = { J.w, J.out, J.out_i, J.n_rows, bx - J.tile0, J.q, J.act };
+    const gemm_view V = { J.w, J.out, J.out_i, J.n_rows, bx - J.tile0, J.q, J.act, 0u };
     gemm_dl_tile<TM, TN, STAGES, KG>(V, J.k, T.m, by);
 }
 
@@ -1174,6 +1254,11 @@ extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_dk2x4(gemm_args G) { gemm_dl_block<2, 4, 4, 2>(G); }
 extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_dk2x2(gemm_args G) { gemm_dl_block<2, 2, 4, 2>(G); }
+// a chunk's Q + K + V with the cache store in the epilogue (gemm_rope)
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk2x2_rope(gemm_args G, gemm_rope R) { gemm_dl_block<2, 2, 4, 2, true>(G, &R); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk4x4_rope(gemm_args G, gemm_rope R) { gemm_dl_block<4, 4, 4, 2, true>(G, &R); }
 // sixteen waves in four K groups over a 16 x 64 / 32 x 64 tile: for grids
 // of fewer workgroups than CUs (a lone tensor against a few tokens), each
 // group walks a quarter of the super-steps

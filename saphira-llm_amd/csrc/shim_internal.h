@@ -67,6 +67,23 @@ SLLM_HIDDEN int         sllm_shim_launch(hipFunction_t f, uint32_t gx, uint32_t 
 SLLM_HIDDEN int         sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz,
                                             uint32_t block, uint32_t lds, void **args);
 
+/* A chunk's Q + K + V GEMM (jobs 0, 1, 2, each with an f32 output) with the
+ * attention's cache store in its epilogue (mirror of gemm_rope in
+ * i2s_kernels.hip): queries roped in place in jobs[0].out, keys roped into
+ * k_cache, values into the slice-major v_cache, token t at position
+ * pos0 + t; jobs[1].out and jobs[2].out are not written.
+ * SLLM_SHIM_NOT_FUSED (nothing launched) where the chosen tile does not
+ * hold whole heads: the caller then runs the plain GEMM and its own store. */
+typedef struct k_gemm_rope {
+    const float *rope;
+    float       *k_cache, *v_cache;
+    uint32_t     n_ctx, hd, half, pos0;
+} k_gemm_rope;
+_Static_assert(sizeof(k_gemm_rope) == 40, "k_gemm_rope must match gemm_rope in i2s_kernels.hip");
+#define SLLM_SHIM_NOT_FUSED 1
+SLLM_HIDDEN int         sllm_shim_gemm_qkv_rope(const sllm_gfx950_gemm_job jobs[3], size_t n, const int8_t *q,
+                                                const sllm_gfx950_act *act, size_t m, const k_gemm_rope *r);
+
 /* noalloc.hip: the address on `device` (current) of the static array behind
  * sllm_gfx950_gemv_batch_noalloc; 0 or the HIP error */
 SLLM_HIDDEN int         sllm_noalloc_resolve(int device, void **out);

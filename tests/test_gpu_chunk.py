@@ -9,8 +9,9 @@ oracle's logits at that position, bit for bit. Shapes: chunk sizes from 2
 to 64 over a 70-token sequence (later chunks attend to keys earlier ones
 wrote), chunks over a restored 1024-position cache at tiny and BitNet-2B
 widths, chunks of 200 and 150 tokens (the scores' eight-token workgroups),
-the full 30-block 2B model in one 100-token chunk, and decode / greedy
-generation carrying on after a chunk.
+the full 30-block 2B model in one 100-token chunk, 512-token chunks at 2B
+widths, the cache store folded into the Q + K + V GEMM (forced tiles), and
+decode / greedy generation carrying on after a chunk.
 """
 import numpy as np
 import pytest
@@ -140,10 +141,7 @@ def test_chunks_above_128_tokens(amd, orc, dev):
     assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
 
 
-@pytest.mark.parametrize("widths", ["tiny", "2b"])
-def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
-    """40 tokens at positions 1024..1063 over a restored cache: every query's
-    softmax spans its own KV rows past the prefix."""
+def _prefix_case(amd, orc, dev, widths):
     cfg = dict(TINY) if widths == "tiny" else dict(amd.BITNET_2B, n_layer=2, n_vocab=512)
     model = amd.synth_model(cfg, 73)
     n_pos, n_ctx = 1024, 1072
@@ -162,6 +160,60 @@ def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
     finally:
         g.close()
     assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
+@pytest.mark.parametrize("widths", ["tiny", "2b"])
+def test_chunk_over_a_1024_position_prefix(amd, orc, dev, widths):
+    """40 tokens at positions 1024..1063 over a restored cache: every query's
+    softmax spans its own KV rows past the prefix."""
+    _prefix_case(amd, orc, dev, widths)
+
+
+@pytest.mark.parametrize("tile", [10, 13])
+def test_cache_store_in_the_qkv_epilogue(amd, orc, dev, tiny, tile):
+    """Where the Q + K + V GEMM's row tiles hold whole heads (the 64 x 256 and
+    32 x 128 tiles, forced here: set_gemm_tile 10 and 13) its epilogue ropes
+    the queries and writes the keys and values into the caches itself, in
+    place of sllm_k_chk_kv_store. Forced at sizes where the automatic choice
+    takes other tiles: the tiny model in chunks of 7 and 64 (two or four
+    64-wide heads per tile, K and V tiles past their 128 rows), the narrow
+    rotary width (n_rot 48 of 64), 2B widths over a 1024-position cache
+    (one or two 128-wide heads per tile); then greedy decoding from the
+    caches the chunks wrote, against token-by-token decoding."""
+    model, toks, want = tiny
+    print(f"[chunk] cache store in the QKV epilogue, tile {tile}", flush=True)
+    dev.set_gemm_tile(tile)
+    try:
+        for chunk in (7, 64):
+            g = amd.DeviceDecoder(dev, model, 80)
+            try:
+                got = g.prefill_chunked(toks, chunk)
+            finally:
+                g.close()
+            assert np.array_equal(bits(got), bits(want)), f"chunk {chunk}: " + _first_diff(got, want)
+        cfg = dict(TINY, n_layer=3, n_embd=512, n_ff=1024, n_head=8, n_head_kv=2, n_rot=48, n_vocab=777)
+        m2 = amd.synth_model(cfg, 78)
+        t2 = _tokens(51, cfg["n_vocab"], 79)
+        w2 = _oracle_logits(orc, m2, 64, t2)
+        g = amd.DeviceDecoder(dev, m2, 64)
+        try:
+            got = g.prefill_chunked(t2, 23)
+        finally:
+            g.close()
+        assert np.array_equal(bits(got), bits(w2)), "narrow rotary: " + _first_diff(got, w2)
+        _prefix_case(amd, orc, dev, "2b")
+        g = amd.DeviceDecoder(dev, model, 80)
+        u = amd.DeviceDecoder(dev, model, 80)
+        try:
+            assert g.forward_chunk(toks[:40], 0, logits=False) is None
+            for p, t in enumerate(toks[:40]):
+                u.forward(t, p, logits=False)
+            assert np.array_equal(g.generate([], 12), u.generate([], 12))
+        finally:
+            g.close()
+            u.close()
+    finally:
+        dev.set_gemm_tile(0)
 
 
 def test_full_2b_chunk_is_bit_exact(amd, orc, dev):
