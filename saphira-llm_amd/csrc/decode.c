@@ -128,6 +128,8 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define CLM_TOK      4    /* tokens per chunk output-head workgroup */
 #define CS_TOK       8    /* tokens per chunk scores workgroup (half that up to CS_SMALL tokens) */
 #define CS_SMALL     128
+#define CSW_THREADS  1024 /* the one-wave-unit scores kernel: sixteen waves per CU */
+#define CSW_LDS_PAD  98304u   /* its (unused) LDS: more than half a CU's, one workgroup per CU */
 #define CP_TOK       4    /* tokens per chunk p.V workgroup */
 #define CP_THREADS   512  /* threads per chunk p.V workgroup: two waves per query head */
 #define CSM_ROWS     4    /* softmax rows (one wave each) per chunk softmax workgroup */
@@ -316,7 +318,7 @@ struct sllm_gfx950_ctx {
     k_dec_lm      lm_args;
     size_t        kv_per_layer;    /* floats */
     hipFunction_t f_gemv, f_scores, f_pv, f_lm, f_argmax;
-    hipFunction_t f_prep, f_kvs, f_cscores, f_cscores4, f_csoft, f_cpv, f_clm, f_keys;
+    hipFunction_t f_prep, f_kvs, f_cscores, f_cscores4, f_cscores_w, f_csoft, f_cpv, f_clm, f_keys;
     uint32_t      sc_stride;
     chunk_bufs    chk;
     int           graph_on, graph_ready;
@@ -514,6 +516,7 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
             (st = sllm_shim_decode_function("sllm_k_chk_kv_store", &c->f_kvs)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_scores", &c->f_cscores)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_scores4", &c->f_cscores4)) == SLLM_GFX950_OK &&
+            (st = sllm_shim_decode_function("sllm_k_chk_scores_w", &c->f_cscores_w)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_softmax", &c->f_csoft)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_pv", &c->f_cpv)) == SLLM_GFX950_OK &&
             (st = sllm_shim_decode_function("sllm_k_chk_lm_head", &c->f_clm)) == SLLM_GFX950_OK &&
@@ -877,6 +880,11 @@ int sllm_gfx950_ctx_trace(sllm_gfx950_ctx *c, int32_t *dots, sllm_gfx950_act *ac
 /* chunks of tokens                                                    */
 /* ------------------------------------------------------------------ */
 
+static uint32_t cu_count(void) {
+    const int cu = sllm_shim_cu();
+    return (uint32_t) (cu > 0 ? cu : 256);
+}
+
 /* the chunk buffers for at least n tokens (kept, grown on demand) */
 static int chunk_reserve(sllm_gfx950_ctx *c, int32_t n) {
     if (n <= c->chk.cap) return SLLM_GFX950_OK;
@@ -960,11 +968,19 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;
             void *sargs[] = { &A, &n_tok };
-            /* eight tokens per workgroup, four for small chunks (measured: the grid
-             * of a 64-token chunk is too small at eight) */
-            const int tok = n > CS_SMALL ? CS_TOK : CS_TOK / 2;
-            st = sllm_shim_launch_3d(n > CS_SMALL ? c->f_cscores : c->f_cscores4, (uint32_t) m->n_head_kv, pos_blocks,
-                                     (uint32_t) ((n + tok - 1) / tok), ATT_THREADS, 0, sargs);
+            if (n > CS_SMALL && m->hd % 32 == 0) {
+                /* units of one wave dealt evenly over one workgroup per CU
+                 * (measured: the workgroups of 8 tokens x 64 positions take
+                 * 1.4 rounds of the CUs at 512 tokens, and the dispatcher
+                 * leaves some CUs with twice the others' share) */
+                st = sllm_shim_launch(c->f_cscores_w, cu_count(), 1, CSW_THREADS, CSW_LDS_PAD, sargs);
+            } else {
+                /* eight tokens per workgroup, four for small chunks (measured:
+                 * the grid of a 64-token chunk is too small at eight) */
+                const int tok = n > CS_SMALL ? CS_TOK : CS_TOK / 2;
+                st = sllm_shim_launch_3d(tok == CS_TOK ? c->f_cscores : c->f_cscores4, (uint32_t) m->n_head_kv, pos_blocks,
+                                         (uint32_t) ((n + tok - 1) / tok), ATT_THREADS, 0, sargs);
+            }
         }
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;

@@ -595,59 +595,82 @@ sllm_k_dec_scores(dec_attn A) { scores_body<false>(A); }
 // serves only the keys.
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
-template <uint32_t CS_TOK>
+template <uint32_t CS_TOK, uint32_t NB = 1>
 __device__ __forceinline__ void chk_scores_body(const dec_attn &A, uint32_t n_tok) {
+    constexpr uint32_t THREADS = ATT_THREADS * NB, LOADS = KT_LOADS / NB;   // NB token blocks per workgroup
     __shared__ __attribute__((aligned(16))) float kt[ATT_POS][KT_STRIDE];
-    const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tb = blockIdx.z * CS_TOK, tid = threadIdx.x;
-    const uint32_t last_tok = min(tb + CS_TOK, n_tok) - 1;
-    const uint32_t npast_max = A.chunk_base + last_tok + 1;
-    if (s0 >= npast_max) return;
+    const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tb0 = blockIdx.z * CS_TOK * NB, tid = threadIdx.x;
+    const uint32_t npast_wg = A.chunk_base + min(tb0 + CS_TOK * NB, n_tok);   // of the workgroup's last token
+    if (s0 >= npast_wg) return;
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, hd4 = hd / 4;
     const float *kc = A.k_cache + (size_t) kvh * A.n_ctx * hd;
 
     // the block's keys (rows past the last token's position re-read a valid row)
-    const uint32_t n_f4 = ATT_POS * hd4, last_cached = npast_max - 1;
-    f32x4 kv[KT_LOADS];
+    const uint32_t n_f4 = ATT_POS * hd4, last_cached = npast_wg - 1;
+    f32x4 kv[LOADS];
 #pragma unroll
-    for (int u = 0; u < KT_LOADS; ++u) {
-        const uint32_t f = min(tid + (uint32_t) u * ATT_THREADS, n_f4 - 1);
+    for (int u = 0; u < (int) LOADS; ++u) {
+        const uint32_t f = min(tid + (uint32_t) u * THREADS, n_f4 - 1);
         const uint32_t r = f / hd4, c4 = f % hd4;
         kv[u] = *G_CAST(const f32x4, kc + (size_t) min(s0 + r, last_cached) * hd + 4 * c4);
     }
 #pragma unroll
-    for (int u = 0; u < KT_LOADS; ++u) {
-        const uint32_t f = tid + (uint32_t) u * ATT_THREADS;
+    for (int u = 0; u < (int) LOADS; ++u) {
+        const uint32_t f = tid + (uint32_t) u * THREADS;
         const uint32_t r = f / hd4, c4 = f % hd4;
-        if (f < n_f4 && s0 + r < npast_max) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
+        if (f < n_f4 && s0 + r < npast_wg) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
     }
     __syncthreads();
 
-    const uint32_t r = tid % ATT_POS, hh = __builtin_amdgcn_readfirstlane(tid / ATT_POS);
-    if (hh >= grp) return;                           // uniform
-    const float *qrow[CS_TOK];
+    // wave w: query head w % 4 of the KV head, token block w / 4 of the workgroup's NB
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / ATT_POS), r = tid % ATT_POS, hh = wave % 4u;
+    const uint32_t tb = tb0 + (wave / 4u) * CS_TOK;
+    if (hh >= grp || tb >= n_tok) return;            // uniform; no barriers past this point
+    const uint32_t last_tok = min(tb + CS_TOK, n_tok) - 1;
+    const uint32_t npast_max = A.chunk_base + last_tok + 1;
+    if (s0 >= npast_max) return;                     // no position of this block at or before its tokens
+    // the queries are not written during the launch: constant address
+    // space, so that their wave-uniform reads are scalar loads
+    typedef __attribute__((address_space(4))) const float cfloat;
+    typedef __attribute__((address_space(4))) const f32x4 cf32x4;
+    cfloat *qrow[CS_TOK];
 #pragma unroll
     for (int tk = 0; tk < (int) CS_TOK; ++tk)
-        qrow[tk] = A.q + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + hh) * hd;
+        qrow[tk] = (cfloat *) (A.q + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + hh) * hd);
     float acc[CS_TOK];
 #pragma unroll
     for (int tk = 0; tk < (int) CS_TOK; ++tk) acc[tk] = 0.0f;
-    for (uint32_t d0 = 0; d0 < hd; d0 += 8) {       // hd % 8 == 0
-        f32x4 k4[2];
+    // four dimensions per step. The queries of the next step load while
+    // this one computes: scalar loads return out of order, so a wait covers
+    // all of them, and the next step's loads go out only after this step's
+    // first product has waited for its own (two buffers of CS_TOK x 4 words)
+    auto qload = [&](uint32_t d0, f32x4 (&q)[CS_TOK]) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) k4[j] = *reinterpret_cast<const f32x4 *>(&kt[r][d0 + 4 * j]);
+        for (int tk = 0; tk < (int) CS_TOK; ++tk) q[tk] = *(cf32x4 *) (qrow[tk] + min(d0, hd - 4));
+    };
+    auto step4 = [&](uint32_t d0, const f32x4 (&qc)[CS_TOK], f32x4 (&qn)[CS_TOK]) {
+        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&kt[r][d0]);
+        float a0 = acc[0] + qc[0][0] * k4[0];
+        __builtin_amdgcn_sched_barrier(0);
+        qload(d0 + 4, qn);
+        __builtin_amdgcn_sched_barrier(0);
+        a0 = a0 + qc[0][1] * k4[1];
+        a0 = a0 + qc[0][2] * k4[2];
+        acc[0] = a0 + qc[0][3] * k4[3];
 #pragma unroll
-        for (int tk = 0; tk < (int) CS_TOK; ++tk) {
-            const f32x8 q = *reinterpret_cast<const f32x8 *>(qrow[tk] + d0);
+        for (int tk = 1; tk < (int) CS_TOK; ++tk) {
             float a = acc[tk];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                a = a + q[4 * j] * k4[j][0];
-                a = a + q[4 * j + 1] * k4[j][1];
-                a = a + q[4 * j + 2] * k4[j][2];
-                a = a + q[4 * j + 3] * k4[j][3];
-            }
-            acc[tk] = a;
+            a = a + qc[tk][0] * k4[0];
+            a = a + qc[tk][1] * k4[1];
+            a = a + qc[tk][2] * k4[2];
+            acc[tk] = a + qc[tk][3] * k4[3];
         }
+    };
+    f32x4 qa[CS_TOK], qb[CS_TOK];
+    qload(0, qa);
+    for (uint32_t d0 = 0; d0 < hd; d0 += 8) {       // hd % 8 == 0
+        step4(d0, qa, qb);
+        step4(d0 + 4, qb, qa);
     }
     if (s0 + r < npast_max) {
 #pragma unroll
@@ -665,6 +688,123 @@ extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_chk_scores(dec_attn A, uint32_t n_tok) { chk_scores_body<8>(A, n_tok); }
 extern "C" __global__ void __launch_bounds__(ATT_THREADS)
 sllm_k_chk_scores4(dec_attn A, uint32_t n_tok) { chk_scores_body<4>(A, n_tok); }
+
+// The chunk's scores as units of one wave: (KV head, query head, 8 tokens,
+// 64 positions), lane r = position s0 + r, the same dot chains as above.
+// The lane streams its key row from the cache (L2) in chunks of 32
+// dimensions (one 128-byte line), the next chunk in flight while this one
+// is used, so the wave needs no LDS and no barrier; the queries come
+// through the scalar unit as above, the next step's in flight. A
+// workgroup of sixteen waves runs on each CU (the host pads its LDS so that
+// no second one fits) and takes units cu, cu + G, cu + 2G, ... of the
+// launch's G workgroups, so that every CU has the same number of units to
+// within one, at most one more than the others on each SIMD.
+constexpr int CSW_THREADS = 1024;
+constexpr uint32_t CSW_TOK = 8;
+
+__device__ __forceinline__ void chk_scores_unit(const dec_attn &A, uint32_t n_tok, uint32_t kvh, uint32_t hh,
+                                                uint32_t tb, uint32_t s0, uint32_t lane) {
+    const uint32_t grp = A.n_head / A.n_kv, hd = A.hd;
+    const uint32_t last_tok = min(tb + CSW_TOK, n_tok) - 1;
+    const uint32_t npast_max = A.chunk_base + last_tok + 1;
+    // the lane's key row (rows past the last token's position re-read a valid row)
+    const GLOBAL f32x4 *krow = G_CAST(const f32x4, A.k_cache + ((size_t) kvh * A.n_ctx + min(s0 + lane, npast_max - 1)) * hd);
+    typedef __attribute__((address_space(4))) const float cfloat;
+    typedef __attribute__((address_space(4))) const f32x4 cf32x4;
+    cfloat *qrow[CSW_TOK];
+#pragma unroll
+    for (int tk = 0; tk < (int) CSW_TOK; ++tk)
+        qrow[tk] = (cfloat *) (A.q + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + hh) * hd);
+    float acc[CSW_TOK];
+#pragma unroll
+    for (int tk = 0; tk < (int) CSW_TOK; ++tk) acc[tk] = 0.0f;
+    auto qload = [&](uint32_t d0, f32x4 (&q)[CSW_TOK]) {
+#pragma unroll
+        for (int tk = 0; tk < (int) CSW_TOK; ++tk) q[tk] = *(cf32x4 *) (qrow[tk] + min(d0, hd - 4));
+    };
+    // four dimensions: the first product waits for this step's queries, then
+    // the next step's go out
+    auto step4 = [&](uint32_t d0, const f32x4 &k4, const f32x4 (&qc)[CSW_TOK], f32x4 (&qn)[CSW_TOK]) {
+        float a0 = acc[0] + qc[0][0] * k4[0];
+        __builtin_amdgcn_sched_barrier(0);
+        qload(d0 + 4, qn);
+        __builtin_amdgcn_sched_barrier(0);
+        a0 = a0 + qc[0][1] * k4[1];
+        a0 = a0 + qc[0][2] * k4[2];
+        acc[0] = a0 + qc[0][3] * k4[3];
+#pragma unroll
+        for (int tk = 1; tk < (int) CSW_TOK; ++tk) {
+            float a = acc[tk];
+            a = a + qc[tk][0] * k4[0];
+            a = a + qc[tk][1] * k4[1];
+            a = a + qc[tk][2] * k4[2];
+            acc[tk] = a + qc[tk][3] * k4[3];
+        }
+    };
+    const uint32_t n_ch = hd / 32u;                    // hd % 32 == 0
+    auto kload = [&](uint32_t ch, f32x4 (&k)[8]) {
+        const uint32_t c = min(ch, n_ch - 1u) * 8u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) k[i] = krow[c + (uint32_t) i];
+    };
+    // 32 dimensions; queries of its first step in qa on entry, of the next chunk's first step on exit
+    f32x4 qa[CSW_TOK], qb[CSW_TOK];
+    auto chunk = [&](uint32_t ch, const f32x4 (&k)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            step4(32u * ch + 4u * (uint32_t) i, k[i], qa, qb);
+            step4(32u * ch + 4u * (uint32_t) i + 4u, k[i + 1], qb, qa);
+        }
+    };
+    f32x4 ka[8], kb[8];
+    kload(0, ka);
+    qload(0, qa);
+    kload(1, kb);
+    uint32_t ch = 0;
+    for (; ch + 2 <= n_ch; ch += 2) {
+        chunk(ch, ka);
+        kload(ch + 2, ka);
+        chunk(ch + 1, kb);
+        kload(ch + 3, kb);
+    }
+    if (ch < n_ch) chunk(ch, ka);                      // an odd chunk count
+    if (s0 + lane < npast_max) {
+#pragma unroll
+        for (int tk = 0; tk < (int) CSW_TOK; ++tk) {
+            const uint32_t t = tb + (uint32_t) tk;
+            if (t < n_tok && s0 + lane <= A.chunk_base + t) {
+                A.scores[(size_t) t * A.n_head * A.sc_stride + (size_t) (kvh * grp + hh) * A.sc_stride + s0 + lane] =
+                    acc[tk] * A.attn_scale;
+            }
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(CSW_THREADS)
+sllm_k_chk_scores_w(dec_attn A, uint32_t n_tok) {
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t G = gridDim.x, cu = blockIdx.x, nkh = A.n_head;
+    const uint32_t grp = A.n_head / A.n_kv;
+    // lane j: token block j's position blocks (a chunk has at most 512
+    // tokens: 64 blocks), then their inclusive prefix sum over the lanes
+    const uint32_t n_tb = (n_tok + CSW_TOK - 1) / CSW_TOK;
+    uint32_t inc = lane < n_tb ? (A.chunk_base + min(CSW_TOK * (lane + 1u), n_tok) + ATT_POS - 1) / ATT_POS : 0u;
+#pragma unroll
+    for (int o = 1; o < 64; o *= 2) {
+        const uint32_t up = (uint32_t) __shfl_up((int) inc, (unsigned) o);
+        inc += lane >= (uint32_t) o ? up : 0u;
+    }
+    const uint32_t n_pairs = __builtin_amdgcn_readlane(inc, 63);
+    const uint32_t n_units = n_pairs * nkh;
+    for (uint32_t k = wave; k * G + cu < n_units; k += CSW_THREADS / 64) {
+        const uint32_t u = k * G + cu;                 // uniform
+        const uint32_t p = u / nkh, kh = u % nkh;
+        // p's token block: the lanes whose inclusive sum is at most p
+        const uint32_t tb8 = (uint32_t) __builtin_popcountll(__ballot(inc <= p));
+        const uint32_t before = tb8 > 0 ? __builtin_amdgcn_readlane(inc, tb8 - 1u) : 0u;
+        chk_scores_unit(A, n_tok, kh / grp, kh % grp, tb8 * CSW_TOK, (p - before) * ATT_POS, lane);
+    }
+}
 
 // Softmax and p . V: workgroup (two query heads of a KV head, 8 head
 // dimensions), eight waves.
