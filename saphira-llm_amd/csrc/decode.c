@@ -131,7 +131,7 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define CSW_THREADS  1024 /* the one-wave-unit scores kernel: sixteen waves per CU */
 #define CSW_LDS_PAD  98304u   /* its (unused) LDS: more than half a CU's, one workgroup per CU */
 #define CP_TOK       4    /* tokens per chunk p.V workgroup */
-#define CP_THREADS   512  /* threads per chunk p.V workgroup: two waves per query head */
+#define CP_THREADS   1024 /* threads per chunk p.V workgroup: sixteen waves, one workgroup per CU */
 #define CSM_ROWS     4    /* softmax rows (one wave each) per chunk softmax workgroup */
 /* sllm_k_chk_kv_store stages a token's query row (n_head * hd = n_embd floats) in 7168 floats of LDS */
 _Static_assert(SLLM_GFX950_DEC_MAX_WIDTH <= 7168, "query row of the chunk KV store");
@@ -991,8 +991,8 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;
             void *pargs[] = { &A, &n_tok };
-            st = sllm_shim_launch_3d(c->f_cpv, (uint32_t) m->n_head_kv, 1, (uint32_t) ((n + CP_TOK - 1) / CP_TOK),
-                                     CP_THREADS, 0, pargs);
+            /* one workgroup per CU, the units dealt over its SIMDs */
+            st = sllm_shim_launch(c->f_cpv, cu_count(), 1, CP_THREADS, CSW_LDS_PAD, pargs);
         }
         /* attn_sub_norm, O */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_PLAIN, B->attn, NULL, NULL, L->attn_sub_norm, (uint32_t) e, 1, NULL);

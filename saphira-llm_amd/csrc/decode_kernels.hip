@@ -1835,42 +1835,40 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
     }
 }
 
-// The chunk's p . V: workgroup (KV head, 4 tokens) of eight waves; wave w
-// is query head h = w % 4 of the KV head and half w / 4 of the head
-// dimensions, one dimension per lane. Each lane adds p_s * v_s to four
-// chains -- its dimension for the four tokens -- in order of s
-// (src/forward.c:706-726), a token's chain left alone past its own
+// The chunk's p . V in units of one wave: (KV head, query head h, half of
+// the head dimensions, 4 tokens), one dimension per lane. Each lane adds
+// p_s * v_s to four chains -- its dimension for the four tokens -- in order
+// of s (src/forward.c:706-726), a token's chain left alone past its own
 // position. p (written over the scores rows by sllm_k_chk_softmax) is the
 // same for every lane of a wave and comes through the scalar unit, eight
-// positions of a token per load; V rows stream from L2 two blocks of sixteen
-// positions ahead. The two waves of a SIMD hide each other's waits.
+// positions of a token per load; V rows stream from L2 two blocks of
+// sixteen positions ahead.
 constexpr uint32_t CP_TOK = 4;
-constexpr int CP_THREADS = 512;
+constexpr int CP_THREADS = 1024;
 
-extern "C" __global__ void __launch_bounds__(CP_THREADS)
-sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
-    // the last token blocks (the longest rows) first
-    const uint32_t kvh = blockIdx.x, tb = (gridDim.z - 1 - blockIdx.z) * CP_TOK, tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t h = wave & 3u, half_id = wave >> 2;
+__device__ __forceinline__ void chk_pv_unit(const dec_attn &A, uint32_t n_tok, uint32_t kvh, uint32_t tb,
+                                            uint32_t lane, uint32_t h, uint32_t half_id) {
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride;
-    if (h >= grp || 64u * half_id >= hd) return;   // uniform; no barriers in this kernel
     const uint32_t last_tok = min(tb + CP_TOK, n_tok) - 1;
     const uint32_t npast_max = A.chunk_base + last_tok + 1, npast_min = A.chunk_base + tb + 1;
     const uint32_t d = min(64u * half_id + lane, hd - 1);
     // dimension d of position s: slice d / 8, element d % 8
     const float *vc = A.v_cache + ((size_t) kvh * (hd / PV_SLICE) + d / PV_SLICE) * A.n_ctx * PV_SLICE + d % PV_SLICE;
-    const float *prow[CP_TOK];                     // token rows past n_tok read the last one's
+    // p is not written during the launch: constant address space, so that
+    // its wave-uniform reads are scalar loads
+    typedef __attribute__((address_space(4))) const f32x8 cf32x8;
+    typedef __attribute__((address_space(4))) const float cfloat;
+    cfloat *prow[CP_TOK];                          // token rows past n_tok read the last one's
     float acc[CP_TOK];
     uint32_t npast_t[CP_TOK];                      // each token's own (past n_tok: never written out)
 #pragma unroll
     for (int tk = 0; tk < (int) CP_TOK; ++tk) {
-        prow[tk] = A.scores + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + h) * ss;
+        prow[tk] = (cfloat *) (A.scores + ((size_t) min(tb + (uint32_t) tk, last_tok) * A.n_head + kvh * grp + h) * ss);
         acc[tk] = 0.0f;
         npast_t[tk] = A.chunk_base + tb + (uint32_t) tk + 1;
     }
     // p of positions s..s+7 of token tk (within the row: sc_stride >= n_ctx, a multiple of 8)
-    auto p8 = [&](int tk, uint32_t s) { return *reinterpret_cast<const f32x8 *>(prow[tk] + min(s, ss - 8)); };
+    auto p8 = [&](int tk, uint32_t s) { return *(cf32x8 *) (prow[tk] + min(s, ss - 8)); };
     float va[16], vb[16];
     auto load16 = [&](uint32_t s, float (&v)[16]) {
 #pragma unroll
@@ -1887,10 +1885,17 @@ sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
 #pragma unroll
         for (int tk = 0; tk < (int) CP_TOK; ++tk) pn[tk] = p8(tk, s + 8);
         __builtin_amdgcn_sched_barrier(0);
+        // per position the four products, then the four sums: no sum right
+        // behind the product it waits for (a wave alone on its SIMD)
 #pragma unroll
         for (int q = 1; q < 8; ++q) {
+            float x[CP_TOK];
 #pragma unroll
-            for (int tk = 0; tk < (int) CP_TOK; ++tk) acc[tk] = acc[tk] + pc[tk][q] * v[q];
+            for (int tk = 0; tk < (int) CP_TOK; ++tk) x[tk] = pc[tk][q] * v[q];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int tk = 0; tk < (int) CP_TOK; ++tk) acc[tk] = acc[tk] + x[tk];
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     f32x8 pa[CP_TOK], pb[CP_TOK];
@@ -1951,6 +1956,40 @@ sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
         for (int tk = 0; tk < (int) CP_TOK; ++tk) {
             const uint32_t t = tb + (uint32_t) tk;
             if (t < n_tok) A.out[(size_t) t * A.n_head * hd + (size_t) (kvh * grp + h) * hd + 64u * half_id + lane] = acc[tk];
+        }
+    }
+}
+
+// One workgroup of sixteen waves per CU (the host pads its LDS so that no
+// second one fits). Units are numbered longest first (the last token blocks
+// first) and dealt over the launch's SIMDs back and forth -- SIMD j of S
+// takes units j, 2S - 1 - j, 2S + j, ... -- so that the SIMDs' sums of
+// lengths agree to within a few percent. A wave reads which SIMD it runs on
+// and takes that SIMD's units in order through a counter in LDS; once they
+// are gone it helps with the other SIMDs' of its CU, so every unit is done
+// whatever the placement of the waves.
+extern "C" __global__ void __launch_bounds__(CP_THREADS)
+sllm_k_chk_pv(dec_attn A, uint32_t n_tok) {
+    __shared__ uint32_t s_next[4];
+    const uint32_t lane = threadIdx.x & 63u;
+    if (threadIdx.x < 4) s_next[threadIdx.x] = 0;
+    __syncthreads();
+    // HW_ID bits 5:4: the SIMD this wave runs on
+    const uint32_t simd = __builtin_amdgcn_readfirstlane((__builtin_amdgcn_s_getreg(63492) >> 4) & 3u);
+    const uint32_t n_simd = 4u * gridDim.x;
+    const uint32_t grp = A.n_head / A.n_kv, halves = (A.hd + 63u) / 64u;
+    const uint32_t per_tb = A.n_kv * grp * halves;                  // units per token block
+    const uint32_t n_tb = (n_tok + CP_TOK - 1) / CP_TOK, n_units = per_tb * n_tb;
+    for (uint32_t j = 0; j < 4u; ++j) {
+        const uint32_t sm = (simd + j) & 3u, sig = 4u * blockIdx.x + sm;
+        for (;;) {
+            uint32_t r = 0;
+            if (lane == 0) r = atomicAdd(&s_next[sm], 1u);
+            r = __builtin_amdgcn_readfirstlane(r);
+            const uint32_t k = r * n_simd + ((r & 1u) ? n_simd - 1u - sig : sig);
+            if (k >= n_units) break;                                // uniform; later rounds are further out
+            const uint32_t rem = k % per_tb, kh = rem / halves;
+            chk_pv_unit(A, n_tok, kh / grp, (n_tb - 1u - k / per_tb) * CP_TOK, lane, kh % grp, rem % halves);
         }
     }
 }
