@@ -123,7 +123,7 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define LM_ROWS     32
 #define LM_MAX_E    8192
 #define LM_WG_PER_CU 2    /* output workgroups per CU (LDS: 32 KiB each); 2 ran 4 us per token faster than 4 */
-#define CHK_THREADS  256
+#define CHK_THREADS  512
 #define CLM_THREADS  256
 #define CLM_TOK      4    /* tokens per chunk output-head workgroup */
 #define CS_TOK       8    /* tokens per chunk scores workgroup (half that up to CS_SMALL tokens) */

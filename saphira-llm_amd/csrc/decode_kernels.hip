@@ -1427,7 +1427,7 @@ struct chk_prep {
 };
 static_assert(sizeof(chk_prep) == 80, "chk_prep must match decode.c");
 
-constexpr int CHK_THREADS = 256;
+constexpr int CHK_THREADS = 512;        // eight waves per token (measured: four leave the SIMDs half idle)
 constexpr uint32_t CHK_MAX_K = 7168;
 
 // The output head over a chunk: logits[t][r] = row r . xn[t] for every
@@ -1453,7 +1453,7 @@ constexpr int CLM_TOK = 4;              // tokens per workgroup
 // input load is unconditional (addresses clamped inside the row) and goes
 // out before the first is used, so the loads overlap instead of each waiting
 // behind the last one's stores.
-template <uint32_t MODE, int CU>
+template <uint32_t MODE, int CU, int TH>
 __device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, double *red_d, double *lane_d,
                                               float *red_f, int *red_i) {
     const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = P.k;
@@ -1463,7 +1463,7 @@ __device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, doub
     u32x2 ha[CU];
 #pragma unroll
     for (int u = 0; u < CU; ++u) {
-        const uint32_t i = min(4 * tid + 4 * CHK_THREADS * (uint32_t) u, k - 4);
+        const uint32_t i = min(4 * tid + 4 * TH * (uint32_t) u, k - 4);
         if (MODE == IN_EMBED) {
             ha[u] = *G_CAST(const u32x2, (const uint16_t *) P.a + (size_t) token * k + i);
         } else {
@@ -1476,7 +1476,7 @@ __device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, doub
     double part = 0.0;
 #pragma unroll
     for (int u = 0; u < CU; ++u) {
-        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        const uint32_t i = 4 * tid + 4 * TH * (uint32_t) u;
         if (i < k) {
             f32x4 v;
             if (MODE == IN_EMBED) {
@@ -1501,7 +1501,7 @@ __device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, doub
     float m = 0.0f;
 #pragma unroll
     for (int u = 0; u < CU; ++u) {
-        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        const uint32_t i = 4 * tid + 4 * TH * (uint32_t) u;
         if (i < k) {
             f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
 #pragma unroll
@@ -1519,12 +1519,12 @@ __device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, doub
     __syncthreads();
     m = red_f[0];
 #pragma unroll
-    for (int w = 1; w < CHK_THREADS / 64; ++w) m = fmaxf(m, red_f[w]);
+    for (int w = 1; w < TH / 64; ++w) m = fmaxf(m, red_f[w]);
     const float qs = m > 0.0f ? 127.0f / m : 0.0f;
     int ls = 0;
 #pragma unroll
     for (int u = 0; u < CU; ++u) {
-        const uint32_t i = 4 * tid + 4 * CHK_THREADS * (uint32_t) u;
+        const uint32_t i = 4 * tid + 4 * TH * (uint32_t) u;
         if (i < k) {
             const f32x4 v = *reinterpret_cast<const f32x4 *>(xs + i);
             const int a = quant_one(v[0] * qs), b = quant_one(v[1] * qs);
@@ -1541,32 +1541,36 @@ __device__ __forceinline__ void chk_prep_body(const chk_prep &P, float *xs, doub
     if (tid == 0) {
         int32_t asum = 0;
 #pragma unroll
-        for (int w = 0; w < CHK_THREADS / 64; ++w) asum += red_i[w];
+        for (int w = 0; w < TH / 64; ++w) asum += red_i[w];
         G_CAST(float, P.act_out + t)[0] = qs;
         G_CAST(int32_t, P.act_out + t)[1] = asum;
     }
 }
 
-template <int CU>
+template <int CU, int TH>
 __device__ __forceinline__ void chk_prep_width(const chk_prep &P, float *xs, double *red_d, double *lane_d,
                                                float *red_f, int *red_i) {
     switch (P.mode) {
-    case IN_EMBED: chk_prep_body<IN_EMBED, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
-    case IN_RESID: chk_prep_body<IN_RESID, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
-    case IN_SILU:  chk_prep_body<IN_SILU, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
-    default:       chk_prep_body<IN_PLAIN, CU>(P, xs, red_d, lane_d, red_f, red_i); break;
+    case IN_EMBED: chk_prep_body<IN_EMBED, CU, TH>(P, xs, red_d, lane_d, red_f, red_i); break;
+    case IN_RESID: chk_prep_body<IN_RESID, CU, TH>(P, xs, red_d, lane_d, red_f, red_i); break;
+    case IN_SILU:  chk_prep_body<IN_SILU, CU, TH>(P, xs, red_d, lane_d, red_f, red_i); break;
+    default:       chk_prep_body<IN_PLAIN, CU, TH>(P, xs, red_d, lane_d, red_f, red_i); break;
     }
 }
 
-extern "C" __global__ void __launch_bounds__(CHK_THREADS)
-sllm_k_chk_prep(chk_prep P) {
+template <int TH>
+__device__ __forceinline__ void chk_prep_entry(const chk_prep &P) {
     __shared__ __attribute__((aligned(16))) float xs[CHK_MAX_K];
-    __shared__ double red_d[CHK_THREADS / 64], lane_d[4];
-    __shared__ float red_f[CHK_THREADS / 64];
-    __shared__ int red_i[CHK_THREADS / 64];
-    if (P.k <= 4 * CHK_THREADS * 3) chk_prep_width<3>(P, xs, red_d, lane_d, red_f, red_i);
-    else chk_prep_width<(int) (CHK_MAX_K / 4 / CHK_THREADS)>(P, xs, red_d, lane_d, red_f, red_i);
+    __shared__ double red_d[TH / 64], lane_d[4];
+    __shared__ float red_f[TH / 64];
+    __shared__ int red_i[TH / 64];
+    constexpr int CU_S = (3072 + 4 * TH - 1) / (4 * TH);    // widths up to 3072 (n_embd), then up to CHK_MAX_K
+    if (P.k <= 4u * TH * CU_S) chk_prep_width<CU_S, TH>(P, xs, red_d, lane_d, red_f, red_i);
+    else chk_prep_width<(int) ((CHK_MAX_K + 4 * TH - 1) / (4 * TH)), TH>(P, xs, red_d, lane_d, red_f, red_i);
 }
+
+extern "C" __global__ void __launch_bounds__(CHK_THREADS)
+sllm_k_chk_prep(chk_prep P) { chk_prep_entry<CHK_THREADS>(P); }
 
 // Workgroup t: token t's key roped at its position (NeoX, src/ops.c:467-549)
 // and stored with its value into the caches (src/forward.c:668-690), so that
