@@ -936,7 +936,7 @@ static int prep(sllm_gfx950_ctx *c, int32_t n, uint32_t mode, const void *a, con
  * head for every token into chk.logits (and the last row into c->logits);
  * otherwise for the last token only, straight into c->logits. Either way the
  * last row's argmax lands in the step record. Q, K and V are one launch,
- * gate and up another (sllm_gfx950_gemm_multi). */
+ * gate and up another. */
 static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_logits) {
     const struct sllm_gfx950_model *m = c->m;
     const chunk_bufs *B = &c->chk;
@@ -999,12 +999,21 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_O], e, e, B->q8, B->act, (size_t) n, B->proj, NULL);
         /* ffn_inp = attn_out + inpSA; ffn_norm; gate, up */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_RESID, B->proj, B->x, B->fi, L->ffn_norm, (uint32_t) e, 1, NULL);
+        int glu = 1;
         if (st == SLLM_GFX950_OK) {
-            const sllm_gfx950_gemm_job gu[2] = { { L->w[P_GATE], f, B->g, NULL }, { L->w[P_UP], f, B->u, NULL } };
-            st = sllm_gfx950_gemm_multi(gu, 2, e, B->q8, B->act, (size_t) n);
+            /* where the token count's tile has a gate + up form, its
+             * epilogue makes h = silu(gate) * up (into g) */
+            st = sllm_shim_gemm_glu(L->w[P_GATE], L->w[P_UP], f, e, B->q8, B->act, (size_t) n, B->g);
+            if (st == SLLM_SHIM_NOT_FUSED) {
+                const sllm_gfx950_gemm_job gu[2] = { { L->w[P_GATE], f, B->g, NULL }, { L->w[P_UP], f, B->u, NULL } };
+                glu = 0;
+                st = sllm_gfx950_gemm_multi(gu, 2, e, B->q8, B->act, (size_t) n);
+            }
         }
-        /* silu(gate) * up, ffn_sub_norm, down */
-        if (st == SLLM_GFX950_OK) st = prep(c, n, IN_SILU, B->g, B->u, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL);
+        /* silu(gate) * up (unless done), ffn_sub_norm, down */
+        if (st == SLLM_GFX950_OK)
+            st = glu ? prep(c, n, IN_PLAIN, B->g, NULL, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL)
+                     : prep(c, n, IN_SILU, B->g, B->u, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL);
         if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_DOWN], e, f, B->q8, B->act, (size_t) n, B->proj, NULL);
     }
     if (st != SLLM_GFX950_OK) return st;

@@ -126,6 +126,7 @@ static struct {
     hipFunction_t  k_gemm[15];
     hipFunction_t  k_gemm_t[5];
     hipFunction_t  k_gemm_rope[2];       /* dk2x2, dk4x4 with the chunk's cache store */
+    hipFunction_t  k_gemm_glu[2];        /* dk2x2, dk4x4 gate + up with silu(gate) * up */
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -248,6 +249,8 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm[14], g.mod, "sllm_k_gemm_dq2x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_rope[0], g.mod, "sllm_k_gemm_dk2x2_rope"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_rope[1], g.mod, "sllm_k_gemm_dk4x4_rope"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_glu[0], g.mod, "sllm_k_gemm_dk2x2_glu"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_glu[1], g.mod, "sllm_k_gemm_dk4x4_glu"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[0], g.mod, "sllm_k_gemm_tdl1x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[1], g.mod, "sllm_k_gemm_tdl2x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[2], g.mod, "sllm_k_gemm_tdk2x2"));
@@ -1213,6 +1216,29 @@ int sllm_shim_gemm_qkv_rope(const sllm_gfx950_gemm_job jobs[3], size_t n, const 
     k_gemm_rope rr = *r;
     void *args[] = { &a, &rr };
     HIP_TRY(hipModuleLaunchKernel(g.k_gemm_rope[which], (uint32_t) gx, (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
+                                  g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
+int sllm_shim_gemm_glu(const uint8_t *w_gate, const uint8_t *w_up, size_t n_rows, size_t n, const int8_t *q,
+                       const sllm_gfx950_act *act, size_t m, float *out) {
+    NEED_OPEN();
+    if (out == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_glu: no output");
+    const sllm_gfx950_gemm_job jobs[2] = { { w_gate, n_rows, out, NULL }, { w_up, n_rows, out, NULL } };
+    k_gemm_args a;
+    int tile = 0;
+    uint64_t gx, gy;
+    const int st = gemm_prepare(jobs, 2, n, q, act, m, &a, &tile, &gx, &gy);
+    if (st != SLLM_GFX950_OK || gx == 0) return st;
+    const int which = tile == 12 ? 0 : (tile == 9 ? 1 : -1);
+    if (which < 0) return SLLM_SHIM_NOT_FUSED;
+    /* one tile per BN / 2 rows of each tensor: the same grid as the pair */
+    const uint32_t half_rows = k_gemm_rows[tile] / 2;
+    a.tiles[0] = (uint32_t) ((n_rows + half_rows - 1) / half_rows);
+    a.tiles[1] = a.tiles[2] = 0;
+    a.n_jobs = 1;
+    void *args[] = { &a };
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm_glu[which], a.tiles[0], (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
                                   g.stream, args, NULL));
     return SLLM_GFX950_OK;
 }

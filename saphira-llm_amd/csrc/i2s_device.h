@@ -35,6 +35,37 @@ struct act_t {          // layout of sllm_i2s_act (include/saphira_llm/i2s_gemm.
     int32_t sum;        // sum of the quantised values
 };
 
+// ggml_v_expf, one lane (src/ops.c:342-379): the lane's value does not depend
+// on its neighbours, and the vector code's all-in-range shortcut returns what
+// the blend gives such a lane. NONPOS: x is never above zero (a softmax's
+// x - max; NaN allowed), so n <= 0 always holds where it matters and the
+// select of g folds to a constant -- the same bits for every x with the sign
+// bit set and for NaN (tests/test_expf_nonpos.py compares the two forms).
+template <bool NONPOS = false>
+__device__ __forceinline__ float ggml_v_expf(float x) {
+    const float r = 0x1.8p23f;
+    const float z = fmaf(x, 0x1.715476p+0f, r);
+    const float n = z - r;
+    const float b = fmaf(-n, 0x1.7f7d1cp-20f, fmaf(-n, 0x1.62e4p-1f, x));
+    const uint32_t e = __float_as_uint(z) << 23;
+    const float k = __uint_as_float(e + __float_as_uint(1.0f));
+    const float u = b * b;
+    const float j = fmaf(fmaf(fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u,
+                              fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
+                         u, 0x1.ffffecp-1f * b);
+    // the three results, then a select: no branch per element
+    const uint32_t g = (NONPOS || n <= 0.0f) ? 0x82000000u : 0u;
+    const float s1 = __uint_as_float(g + 0x7f000000u);
+    const float s2 = __uint_as_float(e - g);
+    const float in_range = fmaf(j, k, k), scaled = fmaf(s2, j, s2) * s1, extreme = s1 * s1;
+    return !(fabsf(n) > 126.0f) ? in_range : (fabsf(n) > 192.0f ? extreme : scaled);
+}
+
+// SiLU as src/ops.c:428-440 computes it in its eight-wide body
+__device__ __forceinline__ float silu(float v) {
+    return v / (1.0f + ggml_v_expf(0.0f - v));
+}
+
 // ---------------------------------------------------------------------------
 // wave / block reductions
 // ---------------------------------------------------------------------------

@@ -350,6 +350,7 @@ struct gemm_view {
     const int8_t  *q;
     const act_t   *act;
     uint32_t       job;
+    const uint8_t *w2;          // a gate + up tile: the up tensor (w is gate's)
 };
 
 // A chunk's Q + K + V launch (jobs 0, 1, 2 of gemm_args) that also does the
@@ -721,10 +722,10 @@ __device__ __forceinline__ void gemm_place(uint32_t &bx, uint32_t &by) {
 // rows of the output: a lane's accumulators hold rows 16 apart, the store
 // wants four consecutive ones per lane. The caller has drained its copies
 // into S.
-template <int TM, int TN, int KG, bool ROPE = false>
+template <int TM, int TN, int KG, bool ROPE = false, bool GLU = false>
 __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &V, uint32_t m, uint32_t t0,
                                                    uint32_t n0, uint32_t wr, uint32_t kgrp, uint32_t wave_all,
-                                                   float ep_ws, act_t ep_at, i32x4v (&c)[TM][TN],
+                                                   float ep_ws, float ep_ws2, act_t ep_at, i32x4v (&c)[TM][TN],
                                                    const gemm_rope *R) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
     constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u;
@@ -734,6 +735,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
     uint32_t *mine = reinterpret_cast<uint32_t *>(S + kgrp * E_TILE);
     float *post_s = reinterpret_cast<float *>(S + KG * E_TILE);
     int32_t *sum_s = reinterpret_cast<int32_t *>(S + KG * E_TILE + BM * 4u);
+    float *post2_s = reinterpret_cast<float *>(S + KG * E_TILE + BM * 8u);   // GLU: the up tensor's
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -745,8 +747,49 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
     if (tid < BM) {
         post_s[tid] = ep_ws / ep_at.scale;
         sum_s[tid] = ep_at.sum;
+        if (GLU) post2_s[tid] = ep_ws2 / ep_at.scale;
     }
     __syncthreads();
+    const bool vec_f = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out & 15u) == 0;
+    // streaming stores: written through as the tiles finish rather than left
+    // dirty in L2 for the end-of-kernel writeback
+    auto put = [&](bool vec, GLOBAL uint32_t *o, uint32_t n, u32x4 v) {
+        if (vec) {
+            __builtin_nontemporal_store(v, reinterpret_cast<GLOBAL u32x4 *>(o));
+        } else {
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) if (n + e < V.n_rows) __builtin_nontemporal_store(v[e], o + e);
+        }
+    };
+    if constexpr (GLU) {
+        // columns [0, BN / 2) of the tile are gate rows n0 .., columns
+        // [BN / 2, BN) the same rows of up: h = silu(gate) * up
+        // (src/forward.c:776-778), each factor as the plain epilogue makes it
+        constexpr uint32_t HB = BN / 2u, GLPT = HB / 4u, GRPS = 64u / GLPT;
+        const uint32_t grow = lane / GLPT, gcol = 4u * (lane % GLPT);
+        for (uint32_t row0 = wave_all * GRPS; row0 < BM; row0 += 4u * KG * GRPS) {
+            const uint32_t row = row0 + grow, t = t0 + row, n = n0 + gcol;
+            if (t < m && n < V.n_rows) {
+                i32x4v dg = *reinterpret_cast<const i32x4v *>(S + (row * EP + gcol) * 4u);
+                i32x4v du = *reinterpret_cast<const i32x4v *>(S + (row * EP + HB + gcol) * 4u);
+#pragma unroll
+                for (uint32_t k2 = 1; k2 < (uint32_t) KG; ++k2) {
+                    dg += *reinterpret_cast<const i32x4v *>(S + k2 * E_TILE + (row * EP + gcol) * 4u);
+                    du += *reinterpret_cast<const i32x4v *>(S + k2 * E_TILE + (row * EP + HB + gcol) * 4u);
+                }
+                const float pg = post_s[row], pu = post2_s[row];
+                const int32_t sum = sum_s[row];
+                u32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float gf = (float) (dg[e] - sum) * pg, uf = (float) (du[e] - sum) * pu;
+                    v[e] = __float_as_uint(silu(gf) * uf);
+                }
+                put(vec_f, G_CAST(uint32_t, V.out) + (size_t) t * V.n_rows + n, n, v);
+            }
+        }
+        return;
+    }
     constexpr uint32_t LPT = BN / 4u;               // lanes per tile row in the stores
     constexpr uint32_t RPS = 64u / LPT;             // tile rows per store instruction
     const uint32_t srow = lane / LPT, scol = 4u * (lane % LPT);
@@ -814,17 +857,6 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
         return;
     }
     const bool vec_i = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out_i & 15u) == 0;
-    const bool vec_f = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out & 15u) == 0;
-    // streaming stores: written through as the tiles finish rather than left
-    // dirty in L2 for the end-of-kernel writeback
-    auto put = [&](bool vec, GLOBAL uint32_t *o, uint32_t n, u32x4 v) {
-        if (vec) {
-            __builtin_nontemporal_store(v, reinterpret_cast<GLOBAL u32x4 *>(o));
-        } else {
-#pragma unroll
-            for (uint32_t e = 0; e < 4u; ++e) if (n + e < V.n_rows) __builtin_nontemporal_store(v[e], o + e);
-        }
-    };
     for (uint32_t row0 = wave_all * RPS; row0 < BM; row0 += 4u * KG * RPS) {
         const uint32_t row = row0 + srow, t = t0 + row, n = n0 + scol;
         if (t < m && n < V.n_rows) {
@@ -851,7 +883,10 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
 // waves on every SIMD, one of each group, so that one's waits are covered by
 // the other's MFMAs), and the groups' int32 sums meet in LDS at the end
 // (exact in any order).
-template <int TM, int TN, int STAGES, int KG = 1, bool ROPE = false>
+// GLU: a gate + up tile (V.w gate, V.w2 up, n_rows each): BN / 2 rows of
+// each tensor, gate's in K group 0's half of the weight slot and up's in
+// group 1's, so that the epilogue finds both factors of every output.
+template <int TM, int TN, int STAGES, int KG = 1, bool ROPE = false, bool GLU = false>
 __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by,
                                              const gemm_rope *R = nullptr) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
@@ -871,18 +906,19 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
     constexpr uint32_t PB = 64u * KG, CR = 4u * KG, A_REGION = STAGES * A_BYTES, WSLOT = BN * PB;
     // the epilogue reuses the ring: KG tiles of BM rows of EP (BN + 4) words,
     // then post and sum of the BM tokens
-    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = KG * E_TILE + BM * 8u;
+    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_BYTES = KG * E_TILE + BM * (GLU ? 12u : 8u);
     constexpr uint32_t S_BYTES = STAGES * STAGE > E_BYTES ? STAGES * STAGE : E_BYTES;
     __shared__ __attribute__((aligned(1024))) uint8_t S[S_BYTES];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wave = wave_all & 3u, kgrp = wave_all >> 2;   // place in the tile, K group
     const uint32_t g = lane >> 4, li = lane & 15u;
-    const uint32_t t0 = by * BM, n0 = V.tile * BN;
+    static_assert(!GLU || KG == 2, "a gate + up tile is two K groups, one per tensor");
+    const uint32_t t0 = by * BM, n0 = V.tile * (GLU ? BN / 2u : BN);
     const uint32_t nsup = k / 256u, kb = k >> 2;
     // the epilogue's operands, loaded now so that their latency hides behind
     // the main loop: w_scale, and token t0 + tid's act for the first BM threads
-    float ep_ws = 0.0f;
+    float ep_ws = 0.0f, ep_ws2 = 0.0f;
     act_t ep_at = { 1.0f, 0 };
     if (tid < BM) {
         // the sixteen-wave tiles (a few tokens, one token tile): a vector
@@ -892,6 +928,7 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
         const GLOBAL float *wsp = G_CAST(const float, V.w + (size_t) V.n_rows * kb);
         if (KG == 4) ep_ws = wsp[vzero()];
         else ep_ws = *wsp;
+        if (GLU) ep_ws2 = *G_CAST(const float, V.w2 + (size_t) V.n_rows * kb);
         if (V.act != nullptr) ep_at = V.act[min(t0 + tid, m - 1)];
     }
     // copy sources: instruction j of this wave fills LDS granules
@@ -911,7 +948,8 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
         if (WL) {                                   // K group kgrp copies rows [kgrp BN/KG, (kgrp + 1) BN/KG)
             const uint32_t r = kgrp * (BN / KG) + p / CR;
             bch[j] = (p % CR) ^ (r & 7u);
-            bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb;
+            if (GLU) bsrc[j] = (kgrp == 0 ? V.w : V.w2) + (size_t) min(n0 + r - kgrp * (BN / 2u), V.n_rows - 1) * kb;
+            else bsrc[j] = V.w + (size_t) min(n0 + r, V.n_rows - 1) * kb;
         } else {
             const uint32_t r = p >> 2, ch = (p & 3u) ^ ((r >> 2) & 3u);
             bch[j] = 0;
@@ -1024,7 +1062,7 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
         }
     }
     wait_vmem<0>();                                 // no copy may land after the workgroup leaves
-    gemm_tile_epilogue<TM, TN, KG, ROPE>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_at, c, R);
+    gemm_tile_epilogue<TM, TN, KG, ROPE, GLU>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_ws2, ep_at, c, R);
 }
 
 // the tile of a three-job launch (gemm_args) or of a plan (gemm_table)
@@ -1033,6 +1071,16 @@ __device__ __forceinline__ void gemm_dl_block(const gemm_args &G, const gemm_rop
     uint32_t bx, by;
     gemm_place(bx, by);
     gemm_dl_tile<TM, TN, STAGES, KG, ROPE>(gemm_pick(G, bx), G.k, G.m, by, R);
+}
+
+// a gate + up launch: job 0 of gemm_args is gate, job 1 up (the same
+// n_rows); tiles[0] counts the row tiles of BN / 2 rows of each
+template <int TM, int TN, int STAGES>
+__device__ __forceinline__ void gemm_dl_glu(const gemm_args &G) {
+    uint32_t bx, by;
+    gemm_place(bx, by);
+    const gemm_view V = { G.w[0], G.out[0], nullptr, G.n_rows[0], bx, G.q, G.act, 0u, G.w[1] };
+    gemm_dl_tile<TM, TN, STAGES, 2, false, true>(V, G.k, G.m, by);
 }
 
 template <int TM, int TN, int STAGES, int KG = 1>
@@ -1259,6 +1307,11 @@ extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_dk2x2_rope(gemm_args G, gemm_rope R) { gemm_dl_block<2, 2, 4, 2, true>(G, &R); }
 extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_dk4x4_rope(gemm_args G, gemm_rope R) { gemm_dl_block<4, 4, 4, 2, true>(G, &R); }
+// gate + up with silu(gate) * up in the epilogue (gemm_dl_glu)
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk2x2_glu(gemm_args G) { gemm_dl_glu<2, 2, 4>(G); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk4x4_glu(gemm_args G) { gemm_dl_glu<4, 4, 4>(G); }
 // sixteen waves in four K groups over a 16 x 64 / 32 x 64 tile: for grids
 // of fewer workgroups than CUs (a lone tensor against a few tokens), each
 // group walks a quarter of the super-steps

@@ -84,6 +84,14 @@ _Static_assert(sizeof(k_gemm_rope) == 40, "k_gemm_rope must match gemm_rope in i
 SLLM_HIDDEN int         sllm_shim_gemm_qkv_rope(const sllm_gfx950_gemm_job jobs[3], size_t n, const int8_t *q,
                                                 const sllm_gfx950_act *act, size_t m, const k_gemm_rope *r);
 
+/* A chunk's gate + up GEMM (two tensors of n_rows x n) whose epilogue writes
+ * h = silu(gate) * up into out ([m][n_rows] f32) in place of the two
+ * products. SLLM_SHIM_NOT_FUSED (nothing launched) where the token count
+ * picks a tile without a gate + up form: the caller then runs the plain
+ * GEMM and its own SiLU. */
+SLLM_HIDDEN int         sllm_shim_gemm_glu(const uint8_t *w_gate, const uint8_t *w_up, size_t n_rows, size_t n,
+                                           const int8_t *q, const sllm_gfx950_act *act, size_t m, float *out);
+
 /* noalloc.hip: the address on `device` (current) of the static array behind
  * sllm_gfx950_gemv_batch_noalloc; 0 or the HIP error */
 SLLM_HIDDEN int         sllm_noalloc_resolve(int device, void **out);

@@ -1,4 +1,4 @@
-// ggml_v_expf as decode_kernels.hip computes it (src/ops.c:342-379), the
+// ggml_v_expf as i2s_device.h computes it (src/ops.c:342-379), the
 // general form against the NONPOS one the softmax uses: same bits for every x
 // with the sign bit set (a stride through them; argv[1]: the stride) and for
 // a sample of the NaNs.

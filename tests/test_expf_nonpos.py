@@ -1,5 +1,5 @@
 """The softmax's ggml_v_expf with the x <= 0 specialisation gives the general
-function's bits (decode_kernels.hip: NONPOS). Host C, both forms as the
+function's bits (i2s_device.h: NONPOS). Host C, both forms as the
 device computes them; a stride through every float with the sign bit set,
 plus the exponent boundaries of the range selects, plus sampled NaNs. (The
 whole 2^31 run matches too; it takes minutes.)"""
