@@ -558,10 +558,11 @@ int sllm_gfx950_ctx_reset(sllm_gfx950_ctx *c) {
     const hipStream_t s = sllm_shim_stream();
     hipError_t he = hipSuccess;
     if (c->n_past > 0) {
-        /* the live prefix of every (layer, KV head): n_past key rows each, and
-         * n_past positions of every 8-dimension value slice */
+        /* the live prefix of every (layer, KV head): n_past positions of
+         * every 8-dimension key and value slice */
         const size_t hd = (size_t) c->m->hd, rows = (size_t) c->m->n_layer * (size_t) c->m->n_head_kv;
-        he = hipMemset2DAsync(c->k_cache, (size_t) c->n_ctx * hd * 4, 0, (size_t) c->n_past * hd * 4, rows, s);
+        he = hipMemset2DAsync(c->k_cache, (size_t) c->n_ctx * PV_SLICE * 4, 0, (size_t) c->n_past * PV_SLICE * 4,
+                              rows * (hd / PV_SLICE), s);
         if (he == hipSuccess) {
             he = hipMemset2DAsync(c->v_cache, (size_t) c->n_ctx * PV_SLICE * 4, 0, (size_t) c->n_past * PV_SLICE * 4,
                                   rows * (hd / PV_SLICE), s);
@@ -789,44 +790,45 @@ int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, 
     }
     const struct sllm_gfx950_model *m = c->m;
     const size_t hd = (size_t) m->hd, rows = (size_t) m->n_layer * (size_t) m->n_head_kv;
-    const size_t n_sl = hd / PV_SLICE, np = (size_t) n_pos, nc = (size_t) c->n_ctx;
-    const size_t dpitch = nc * hd * 4, vpitch = nc * PV_SLICE * 4;
+    const size_t n_sl = hd / PV_SLICE, np = (size_t) n_pos;
+    const size_t pitch = (size_t) c->n_ctx * PV_SLICE * 4;
     const hipStream_t s = sllm_shim_stream();
-    /* the values go in slice-major, [layer][KV head][dimension / 8][position][8]:
-     * rearranged on the host first */
-    float *vs = NULL;
+    /* both caches are slice-major, [layer][KV head][dimension / 8][position][8]:
+     * the [layer][KV head][position][hd] rows are rearranged on the host first */
+    float *ks = NULL, *vs = NULL;
     if (n_pos > 0) {
-        vs = malloc(rows * np * hd * sizeof *vs);
-        if (vs == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_kv_load: host staging");
+        ks = malloc(2 * rows * np * hd * sizeof *ks);
+        if (ks == NULL) return sllm_shim_fail(SLLM_GFX950_ERR_NOMEM, "ctx_kv_load: host staging");
+        vs = ks + rows * np * hd;
         for (size_t r = 0; r < rows; ++r) {
             for (size_t sl = 0; sl < n_sl; ++sl) {
-                float *dst = vs + (r * n_sl + sl) * np * PV_SLICE;
-                for (size_t p = 0; p < np; ++p) memcpy(dst + p * PV_SLICE, v + (r * np + p) * hd + sl * PV_SLICE, PV_SLICE * 4);
+                float *kd = ks + (r * n_sl + sl) * np * PV_SLICE, *vd = vs + (r * n_sl + sl) * np * PV_SLICE;
+                for (size_t p = 0; p < np; ++p) {
+                    memcpy(kd + p * PV_SLICE, k + (r * np + p) * hd + sl * PV_SLICE, PV_SLICE * 4);
+                    memcpy(vd + p * PV_SLICE, v + (r * np + p) * hd + sl * PV_SLICE, PV_SLICE * 4);
+                }
             }
         }
     }
     hipError_t he = hipSuccess;
     if (n_pos > 0) {
-        const size_t w = np * hd * 4, wv = np * PV_SLICE * 4;
-        he = hipMemcpy2DAsync(c->k_cache, dpitch, k, w, w, rows, hipMemcpyHostToDevice, s);
-        if (he == hipSuccess) he = hipMemcpy2DAsync(c->v_cache, vpitch, vs, wv, wv, rows * n_sl, hipMemcpyHostToDevice, s);
+        const size_t w = np * PV_SLICE * 4;
+        he = hipMemcpy2DAsync(c->k_cache, pitch, ks, w, w, rows * n_sl, hipMemcpyHostToDevice, s);
+        if (he == hipSuccess) he = hipMemcpy2DAsync(c->v_cache, pitch, vs, w, w, rows * n_sl, hipMemcpyHostToDevice, s);
     }
     /* positions past the restored prefix read as absent (zero) in every
      * (layer, KV head), as src/forward.c:1098-1118 clears them */
     if (he == hipSuccess && n_pos < c->n_ctx) {
-        const size_t from = np * hd * 4, w = dpitch - from;
-        he = hipMemset2DAsync((uint8_t *) c->k_cache + from, dpitch, 0, w, rows, s);
-        if (he == hipSuccess) {
-            const size_t vfrom = np * PV_SLICE * 4;
-            he = hipMemset2DAsync((uint8_t *) c->v_cache + vfrom, vpitch, 0, vpitch - vfrom, rows * n_sl, s);
-        }
+        const size_t from = np * PV_SLICE * 4;
+        he = hipMemset2DAsync((uint8_t *) c->k_cache + from, pitch, 0, pitch - from, rows * n_sl, s);
+        if (he == hipSuccess) he = hipMemset2DAsync((uint8_t *) c->v_cache + from, pitch, 0, pitch - from, rows * n_sl, s);
     }
     if (he == hipSuccess && logits != NULL) {
         he = hipMemcpyAsync(c->logits, logits, (size_t) m->n_vocab * 4, hipMemcpyHostToDevice, s);
     }
     if (he != hipSuccess) {
         hipStreamSynchronize(s);               /* the staging buffer may still be read */
-        free(vs);
+        free(ks);
         return sllm_shim_hip_fail(he, "ctx_kv_load");
     }
     int st = SLLM_GFX950_OK;
@@ -847,7 +849,7 @@ int sllm_gfx950_ctx_kv_load(sllm_gfx950_ctx *c, const float *k, const float *v, 
         if (st == SLLM_GFX950_OK) st = sllm_shim_launch(c->f_argmax, 1, 1, 256, 0, aargs);
     }
     he = hipStreamSynchronize(s);
-    free(vs);
+    free(ks);
     if (st != SLLM_GFX950_OK) return st;
     if (he != hipSuccess) return sllm_shim_hip_fail(he, "ctx_kv_load");
     c->n_past = n_pos;

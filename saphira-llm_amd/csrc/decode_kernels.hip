@@ -377,7 +377,7 @@ __device__ __forceinline__ void dec_variant(const dec_stage &st, const gemv_job 
 
 struct dec_attn {
     const float    *q, *k, *v;          // projections: q [n_head*hd], k / v [n_kv*hd]
-    float          *k_cache;            // this layer's keys [n_kv][n_ctx][hd]
+    float          *k_cache;            // this layer's keys [n_kv][hd / 8][n_ctx][8]
     float          *v_cache;            // this layer's values [n_kv][hd / 8][n_ctx][8]: a slice of
                                         // eight dimensions of every position is contiguous
     const float    *rope;               // [n_ctx][half] (cos, sin)
@@ -474,6 +474,17 @@ sllm_k_dec_gemv(dec_gemv_args A) {
 // roped. CHUNK: grid z is the chunk's token t at position chunk_base + t,
 // whose keys (its own included) are already in the cache; q, scores and out
 // advance by one token's worth per t.
+// The block of ATT_POS key rows from s0 as float4 f = 0 .. ATT_POS hd / 4 - 1
+// of a workgroup's loads: f / 2 walks the rows of one eight-dimension slice
+// of the cache, then the next slice, so that consecutive threads read
+// consecutive 16 bytes; rows past `last` re-read row `last`. kt_src: the
+// float offset in the KV head's cache; kt_col: the column in an LDS row.
+__device__ __forceinline__ size_t kt_src(uint32_t f, uint32_t s0, uint32_t last, uint32_t n_ctx) {
+    const uint32_t h2 = f & 1u, r = (f >> 1) % ATT_POS, sl = (f >> 1) / ATT_POS;
+    return ((size_t) sl * n_ctx + min(s0 + r, last)) * PV_SLICE + 4u * h2;
+}
+__device__ __forceinline__ uint32_t kt_col(uint32_t f) { return ((f >> 1) / ATT_POS) * PV_SLICE + 4u * (f & 1u); }
+
 template <bool CHUNK>
 __device__ __forceinline__ void scores_body(const dec_attn &A) {
     __shared__ __attribute__((aligned(16))) float qr[ATT_MAX_GRP][ATT_MAX_HD];
@@ -498,8 +509,7 @@ __device__ __forceinline__ void scores_body(const dec_attn &A) {
 #pragma unroll
     for (int u = 0; u < KT_LOADS; ++u) {
         const uint32_t f = min(tid + (uint32_t) u * ATT_THREADS, n_f4 - 1);
-        const uint32_t r = f / hd4, c4 = f % hd4;
-        kv[u] = *G_CAST(const f32x4, kc + (size_t) min(s0 + r, last_cached) * hd + 4 * c4);
+        kv[u] = *G_CAST(const f32x4, kc + kt_src(f, s0, last_cached, A.n_ctx));
     }
     rope_in qi[QR_PER_THREAD];
 #pragma unroll
@@ -522,15 +532,15 @@ __device__ __forceinline__ void scores_body(const dec_attn &A) {
     }
     if (!CHUNK && pos - s0 < ATT_POS && tid < hd) {
         const float val = rope_apply(ki, tid, half);
+        const size_t at = ((size_t) (tid / PV_SLICE) * A.n_ctx + pos) * PV_SLICE + tid % PV_SLICE;
         kt[pos - s0][tid] = val;
-        kc[(size_t) pos * hd + tid] = val;
-        vc[((size_t) (tid / PV_SLICE) * A.n_ctx + pos) * PV_SLICE + tid % PV_SLICE] = vnew;
+        kc[at] = val;
+        vc[at] = vnew;
     }
 #pragma unroll
     for (int u = 0; u < KT_LOADS; ++u) {
-        const uint32_t f = tid + (uint32_t) u * ATT_THREADS;
-        const uint32_t r = f / hd4, c4 = f % hd4;
-        if (f < n_f4 && s0 + r < n_cached) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
+        const uint32_t f = tid + (uint32_t) u * ATT_THREADS, r = (f >> 1) % ATT_POS;
+        if (f < n_f4 && s0 + r < n_cached) *reinterpret_cast<f32x4 *>(&kt[r][kt_col(f)]) = kv[u];
     }
     __syncthreads();
     // (3) thread (h, r): the dot in order of d
@@ -580,14 +590,12 @@ __device__ __forceinline__ void chk_scores_body(const dec_attn &A, uint32_t n_to
 #pragma unroll
     for (int u = 0; u < (int) LOADS; ++u) {
         const uint32_t f = min(tid + (uint32_t) u * THREADS, n_f4 - 1);
-        const uint32_t r = f / hd4, c4 = f % hd4;
-        kv[u] = *G_CAST(const f32x4, kc + (size_t) min(s0 + r, last_cached) * hd + 4 * c4);
+        kv[u] = *G_CAST(const f32x4, kc + kt_src(f, s0, last_cached, A.n_ctx));
     }
 #pragma unroll
     for (int u = 0; u < (int) LOADS; ++u) {
-        const uint32_t f = tid + (uint32_t) u * THREADS;
-        const uint32_t r = f / hd4, c4 = f % hd4;
-        if (f < n_f4 && s0 + r < npast_wg) *reinterpret_cast<f32x4 *>(&kt[r][4 * c4]) = kv[u];
+        const uint32_t f = tid + (uint32_t) u * THREADS, r = (f >> 1) % ATT_POS;
+        if (f < n_f4 && s0 + r < npast_wg) *reinterpret_cast<f32x4 *>(&kt[r][kt_col(f)]) = kv[u];
     }
     __syncthreads();
 
@@ -660,9 +668,11 @@ sllm_k_chk_scores4(dec_attn A, uint32_t n_tok) { chk_scores_body<4>(A, n_tok); }
 
 // The chunk's scores as units of one wave: (KV head, query head, 8 tokens,
 // 64 positions), lane r = position s0 + r, the same dot chains as above.
-// The lane streams its key row from the cache (L2) in chunks of 32
-// dimensions (one 128-byte line), the next chunk in flight while this one
-// is used, so the wave needs no LDS and no barrier; the queries come
+// The lane streams its key from the cache (L2) in chunks of 32 dimensions
+// (four slices of eight: each load instruction reads 16 bytes of 64
+// consecutive positions, 32 bytes apart, rather than 64 separate rows), the
+// next chunk in flight while this one is used, so the wave needs no LDS and
+// no barrier; the queries come
 // through the scalar unit as above, the next step's in flight. A
 // workgroup of sixteen waves runs on each CU (the host pads its LDS so that
 // no second one fits) and takes units cu, cu + G, cu + 2G, ... of the
@@ -676,8 +686,11 @@ __device__ __forceinline__ void chk_scores_unit(const dec_attn &A, uint32_t n_to
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd;
     const uint32_t last_tok = min(tb + CSW_TOK, n_tok) - 1;
     const uint32_t npast_max = A.chunk_base + last_tok + 1;
-    // the lane's key row (rows past the last token's position re-read a valid row)
-    const GLOBAL f32x4 *krow = G_CAST(const f32x4, A.k_cache + ((size_t) kvh * A.n_ctx + min(s0 + lane, npast_max - 1)) * hd);
+    // the lane's key (rows past the last token's position re-read a valid
+    // row): eight dimensions at krow, the next eight n_ctx * 8 floats on
+    const GLOBAL float *krow = G_CAST(const float, A.k_cache + ((size_t) kvh * A.n_ctx * hd +
+                                                                (size_t) min(s0 + lane, npast_max - 1) * PV_SLICE));
+    const size_t kslice = (size_t) A.n_ctx * PV_SLICE;
     typedef __attribute__((address_space(4))) const float cfloat;
     typedef __attribute__((address_space(4))) const f32x4 cf32x4;
     cfloat *qrow[CSW_TOK];
@@ -712,9 +725,10 @@ __device__ __forceinline__ void chk_scores_unit(const dec_attn &A, uint32_t n_to
     };
     const uint32_t n_ch = hd / 32u;                    // hd % 32 == 0
     auto kload = [&](uint32_t ch, f32x4 (&k)[8]) {
-        const uint32_t c = min(ch, n_ch - 1u) * 8u;
+        const uint32_t sl = min(ch, n_ch - 1u) * 4u;     // four slices of eight dimensions
 #pragma unroll
-        for (int i = 0; i < 8; ++i) k[i] = krow[c + (uint32_t) i];
+        for (int i = 0; i < 8; ++i)
+            k[i] = *reinterpret_cast<const GLOBAL f32x4 *>(krow + (sl + (uint32_t) i / 2u) * kslice + 4u * ((uint32_t) i & 1u));
     };
     // 32 dimensions; queries of its first step in qa on entry, of the next chunk's first step on exit
     f32x4 qa[CSW_TOK], qb[CSW_TOK];
@@ -1569,7 +1583,8 @@ sllm_k_chk_kv_store(dec_attn A) {
     for (uint32_t i = threadIdx.x; i < gqa; i += ATT_THREADS) {
         const uint32_t kvh = i / hd, d = i % hd;
         const rope_in r = rope_load(ks + (size_t) kvh * hd, d, half, cst);
-        A.k_cache[((size_t) kvh * A.n_ctx + pos) * hd + d] = rope_apply(r, d, half);
+        A.k_cache[(((size_t) kvh * (hd / PV_SLICE) + d / PV_SLICE) * A.n_ctx + pos) * PV_SLICE + d % PV_SLICE] =
+            rope_apply(r, d, half);
     }
     for (uint32_t i = threadIdx.x; i < nq; i += ATT_THREADS) {
         const uint32_t hh = i / hd, d = i % hd;

@@ -361,7 +361,7 @@ struct gemm_view {
 // where a row tile holds whole heads (BN % hd == 0) and half % 4 == 0.
 struct gemm_rope {
     const float *rope;          // [n_ctx][half] (cos, sin)
-    float       *k_cache;       // [n_kv][n_ctx][hd]
+    float       *k_cache;       // [n_kv][hd / 8][n_ctx][8]
     float       *v_cache;       // [n_kv][hd / 8][n_ctx][8]
     uint32_t     n_ctx, hd, half, pos0;
 };
@@ -820,7 +820,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
 #pragma unroll
             for (int e = 0; e < 4; ++e) fr[p][e] = (float) (d[e] - sum) * post;
             if (V.job == 2 && t < m && n < V.n_rows) {
-                // slice-major: [KV head][dimension / 8][position][dimension % 8]
+                // slice-major (both caches): [KV head][dimension / 8][position][dimension % 8]
                 GLOBAL float *o = G_CAST(float, R->v_cache) +
                                   (((size_t) (n / hd) * (hd / 8u) + dd / 8u) * R->n_ctx + R->pos0 + t) * 8u + dd % 8u;
                 *reinterpret_cast<GLOBAL f32x4 *>(o) = (f32x4) { fr[p][0], fr[p][1], fr[p][2], fr[p][3] };
@@ -850,7 +850,8 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
                 }
                 GLOBAL float *dst = V.job == 0
                     ? G_CAST(float, V.out) + (size_t) t * V.n_rows + n
-                    : G_CAST(float, R->k_cache) + ((size_t) (n / hd) * R->n_ctx + R->pos0 + t) * hd + dd;
+                    : G_CAST(float, R->k_cache) +
+                          (((size_t) (n / hd) * (hd / 8u) + dd / 8u) * R->n_ctx + R->pos0 + t) * 8u + dd % 8u;
                 *reinterpret_cast<GLOBAL f32x4 *>(dst) = o;
             }
         }

@@ -70,7 +70,7 @@ SLLM_HIDDEN int         sllm_shim_launch_3d(hipFunction_t f, uint32_t gx, uint32
 /* A chunk's Q + K + V GEMM (jobs 0, 1, 2, each with an f32 output) with the
  * attention's cache store in its epilogue (mirror of gemm_rope in
  * i2s_kernels.hip): queries roped in place in jobs[0].out, keys roped into
- * k_cache, values into the slice-major v_cache, token t at position
+ * k_cache and values into v_cache (both slice-major), token t at position
  * pos0 + t; jobs[1].out and jobs[2].out are not written.
  * SLLM_SHIM_NOT_FUSED (nothing launched) where the chosen tile does not
  * hold whole heads: the caller then runs the plain GEMM and its own store. */
