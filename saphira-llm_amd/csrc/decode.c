@@ -945,11 +945,13 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
     const size_t e = (size_t) m->n_embd, f = (size_t) m->n_ff, g = (size_t) m->gqa;
     const uint32_t pos_blocks = (uint32_t) ((base + n + ATT_POS - 1) / ATT_POS);
     int st = SLLM_GFX950_OK;
+    int l_out_in_x = 0;                 /* the layer below's down GEMM left l_out in x */
     for (int32_t il = 0; il < m->n_layer && st == SLLM_GFX950_OK; ++il) {
         const dev_layer *L = &m->layers[il];
         /* l_out of the layer below (cproj + cffn_inp), or the embedding; attn_norm */
-        st = il == 0 ? prep(c, n, IN_EMBED, m->tok_embd, NULL, B->x, L->attn_norm, (uint32_t) e, 1, NULL)
-                     : prep(c, n, IN_RESID, B->proj, B->fi, B->x, L->attn_norm, (uint32_t) e, 1, NULL);
+        if (il == 0) st = prep(c, n, IN_EMBED, m->tok_embd, NULL, B->x, L->attn_norm, (uint32_t) e, 1, NULL);
+        else if (l_out_in_x) st = prep(c, n, IN_PLAIN, B->x, NULL, NULL, L->attn_norm, (uint32_t) e, 1, NULL);
+        else st = prep(c, n, IN_RESID, B->proj, B->fi, B->x, L->attn_norm, (uint32_t) e, 1, NULL);
         k_dec_attn A = c->attn_args[il];
         A.q = B->q; A.k = B->k; A.v = B->v; A.scores = B->scores; A.out = B->attn;
         A.chunk_base = (uint32_t) base;
@@ -996,11 +998,19 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
             /* one workgroup per CU, the units dealt over its SIMDs */
             st = sllm_shim_launch(c->f_cpv, cu_count(), 1, CP_THREADS, CSW_LDS_PAD, pargs);
         }
-        /* attn_sub_norm, O */
+        /* attn_sub_norm, O; where the tile has the form, its epilogue also
+         * forms ffn_inp = attn_out + inpSA (into fi) */
         if (st == SLLM_GFX950_OK) st = prep(c, n, IN_PLAIN, B->attn, NULL, NULL, L->attn_sub_norm, (uint32_t) e, 1, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_O], e, e, B->q8, B->act, (size_t) n, B->proj, NULL);
-        /* ffn_inp = attn_out + inpSA; ffn_norm; gate, up */
-        if (st == SLLM_GFX950_OK) st = prep(c, n, IN_RESID, B->proj, B->x, B->fi, L->ffn_norm, (uint32_t) e, 1, NULL);
+        int fi_done = 0;
+        if (st == SLLM_GFX950_OK) {
+            st = sllm_shim_gemm_res(L->w[P_O], e, e, B->q8, B->act, (size_t) n, B->fi, B->x);
+            if (st == SLLM_GFX950_OK) fi_done = 1;
+            else if (st == SLLM_SHIM_NOT_FUSED) st = sllm_gfx950_gemm(L->w[P_O], e, e, B->q8, B->act, (size_t) n, B->proj, NULL);
+        }
+        /* ffn_inp (unless done); ffn_norm; gate, up */
+        if (st == SLLM_GFX950_OK)
+            st = fi_done ? prep(c, n, IN_PLAIN, B->fi, NULL, NULL, L->ffn_norm, (uint32_t) e, 1, NULL)
+                         : prep(c, n, IN_RESID, B->proj, B->x, B->fi, L->ffn_norm, (uint32_t) e, 1, NULL);
         int glu = 1;
         if (st == SLLM_GFX950_OK) {
             /* where the token count's tile has a gate + up form, its
@@ -1016,7 +1026,18 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK)
             st = glu ? prep(c, n, IN_PLAIN, B->g, NULL, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL)
                      : prep(c, n, IN_SILU, B->g, B->u, NULL, L->ffn_sub_norm, (uint32_t) f, 1, NULL);
-        if (st == SLLM_GFX950_OK) st = sllm_gfx950_gemm(L->w[P_DOWN], e, f, B->q8, B->act, (size_t) n, B->proj, NULL);
+        /* down; below the last layer, where the tile has the form, its
+         * epilogue also forms l_out = ffn_out + ffn_inp (into x: its inpSA
+         * is consumed by now; the last layer's parts stay apart for the
+         * output head's residual sum) */
+        l_out_in_x = 0;
+        if (st == SLLM_GFX950_OK && il + 1 < m->n_layer) {
+            st = sllm_shim_gemm_res(L->w[P_DOWN], e, f, B->q8, B->act, (size_t) n, B->x, B->fi);
+            if (st == SLLM_GFX950_OK) l_out_in_x = 1;
+            else if (st == SLLM_SHIM_NOT_FUSED) st = SLLM_GFX950_OK;
+        }
+        if (st == SLLM_GFX950_OK && !l_out_in_x)
+            st = sllm_gfx950_gemm(L->w[P_DOWN], e, f, B->q8, B->act, (size_t) n, B->proj, NULL);
     }
     if (st != SLLM_GFX950_OK) return st;
     const hipStream_t s = sllm_shim_stream();

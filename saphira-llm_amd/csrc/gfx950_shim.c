@@ -127,6 +127,7 @@ static struct {
     hipFunction_t  k_gemm_t[5];
     hipFunction_t  k_gemm_rope[2];       /* dk2x2, dk4x4 with the chunk's cache store */
     hipFunction_t  k_gemm_glu[2];        /* dk2x2, dk4x4 gate + up with silu(gate) * up */
+    hipFunction_t  k_gemm_res[4];        /* dk2x2, dk4x4, dq1x1, dq2x1 with a residual added */
     int            force_gemm_tile;
     hipFunction_t  k_checksum;
     hipStream_t    stream;
@@ -251,6 +252,10 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_rope[1], g.mod, "sllm_k_gemm_dk4x4_rope"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_glu[0], g.mod, "sllm_k_gemm_dk2x2_glu"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_glu[1], g.mod, "sllm_k_gemm_dk4x4_glu"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_res[0], g.mod, "sllm_k_gemm_dk2x2_res"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_res[1], g.mod, "sllm_k_gemm_dk4x4_res"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_res[2], g.mod, "sllm_k_gemm_dq1x1_res"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_res[3], g.mod, "sllm_k_gemm_dq2x1_res"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[0], g.mod, "sllm_k_gemm_tdl1x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[1], g.mod, "sllm_k_gemm_tdl2x1"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[2], g.mod, "sllm_k_gemm_tdk2x2"));
@@ -1239,6 +1244,24 @@ int sllm_shim_gemm_glu(const uint8_t *w_gate, const uint8_t *w_up, size_t n_rows
     a.n_jobs = 1;
     void *args[] = { &a };
     HIP_TRY(hipModuleLaunchKernel(g.k_gemm_glu[which], a.tiles[0], (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
+                                  g.stream, args, NULL));
+    return SLLM_GFX950_OK;
+}
+
+int sllm_shim_gemm_res(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q, const sllm_gfx950_act *act,
+                       size_t m, float *out, const float *res) {
+    NEED_OPEN();
+    if (out == NULL || res == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_res: output and residual must be given");
+    const sllm_gfx950_gemm_job job = { w, n_rows, out, NULL };
+    k_gemm_args a;
+    int tile = 0;
+    uint64_t gx, gy;
+    const int st = gemm_prepare(&job, 1, n, q, act, m, &a, &tile, &gx, &gy);
+    if (st != SLLM_GFX950_OK || gx == 0) return st;
+    const int which = tile == 12 ? 0 : (tile == 9 ? 1 : (tile == 13 ? 2 : (tile == 14 ? 3 : -1)));
+    if (which < 0) return SLLM_SHIM_NOT_FUSED;
+    void *args[] = { &a, (void *) &res };
+    HIP_TRY(hipModuleLaunchKernel(g.k_gemm_res[which], (uint32_t) gx, (uint32_t) gy, 1, k_gemm_threads[tile], 1, 1, 0,
                                   g.stream, args, NULL));
     return SLLM_GFX950_OK;
 }

@@ -351,6 +351,7 @@ struct gemm_view {
     const act_t   *act;
     uint32_t       job;
     const uint8_t *w2;          // a gate + up tile: the up tensor (w is gate's)
+    const float   *res;         // a residual tile: [m][n_rows] added to the output
 };
 
 // A chunk's Q + K + V launch (jobs 0, 1, 2 of gemm_args) that also does the
@@ -722,7 +723,7 @@ __device__ __forceinline__ void gemm_place(uint32_t &bx, uint32_t &by) {
 // rows of the output: a lane's accumulators hold rows 16 apart, the store
 // wants four consecutive ones per lane. The caller has drained its copies
 // into S.
-template <int TM, int TN, int KG, bool ROPE = false, bool GLU = false>
+template <int TM, int TN, int KG, bool ROPE = false, bool GLU = false, bool RES = false>
 __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &V, uint32_t m, uint32_t t0,
                                                    uint32_t n0, uint32_t wr, uint32_t kgrp, uint32_t wave_all,
                                                    float ep_ws, float ep_ws2, act_t ep_at, i32x4v (&c)[TM][TN],
@@ -858,6 +859,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
         return;
     }
     const bool vec_i = (V.n_rows & 3u) == 0 && ((uintptr_t) V.out_i & 15u) == 0;
+    const bool vec_r = vec_f && ((uintptr_t) V.res & 15u) == 0;
     for (uint32_t row0 = wave_all * RPS; row0 < BM; row0 += 4u * KG * RPS) {
         const uint32_t row = row0 + srow, t = t0 + row, n = n0 + scol;
         if (t < m && n < V.n_rows) {
@@ -873,6 +875,18 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
                 u32x4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = __float_as_uint((float) (d[e] - sum) * post);
+                if (RES) {
+                    // the residual sums (src/forward.c:744-750, :795-800): out + res
+                    if (vec_r) {
+                        const f32x4 r = *reinterpret_cast<const GLOBAL f32x4 *>(G_CAST(const float, V.res) + at);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(__uint_as_float(v[e]) + r[e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + (uint32_t) e < V.n_rows) v[e] = __float_as_uint(__uint_as_float(v[e]) + V.res[at + e]);
+                    }
+                }
                 put(vec_f, G_CAST(uint32_t, V.out) + at, n, v);
             }
         }
@@ -887,7 +901,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(uint8_t *S, const gemm_view &
 // GLU: a gate + up tile (V.w gate, V.w2 up, n_rows each): BN / 2 rows of
 // each tensor, gate's in K group 0's half of the weight slot and up's in
 // group 1's, so that the epilogue finds both factors of every output.
-template <int TM, int TN, int STAGES, int KG = 1, bool ROPE = false, bool GLU = false>
+template <int TM, int TN, int STAGES, int KG = 1, bool ROPE = false, bool GLU = false, bool RES = false>
 __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uint32_t m, uint32_t by,
                                              const gemm_rope *R = nullptr) {
     constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
@@ -1063,7 +1077,7 @@ __device__ __forceinline__ void gemm_dl_tile(const gemm_view &V, uint32_t k, uin
         }
     }
     wait_vmem<0>();                                 // no copy may land after the workgroup leaves
-    gemm_tile_epilogue<TM, TN, KG, ROPE, GLU>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_ws2, ep_at, c, R);
+    gemm_tile_epilogue<TM, TN, KG, ROPE, GLU, RES>(S, V, m, t0, n0, wr, kgrp, wave_all, ep_ws, ep_ws2, ep_at, c, R);
 }
 
 // the tile of a three-job launch (gemm_args) or of a plan (gemm_table)
@@ -1082,6 +1096,17 @@ __device__ __forceinline__ void gemm_dl_glu(const gemm_args &G) {
     gemm_place(bx, by);
     const gemm_view V = { G.w[0], G.out[0], nullptr, G.n_rows[0], bx, G.q, G.act, 0u, G.w[1] };
     gemm_dl_tile<TM, TN, STAGES, 2, false, true>(V, G.k, G.m, by);
+}
+
+// one tensor (job 0 of gemm_args) whose f32 output gets a residual added:
+// out = (dot - sum) * post + res, res of the output's shape
+template <int TM, int TN, int STAGES, int KG>
+__device__ __forceinline__ void gemm_dl_res(const gemm_args &G, const float *res) {
+    uint32_t bx, by;
+    gemm_place(bx, by);
+    gemm_view V = gemm_pick(G, bx);
+    V.res = res;
+    gemm_dl_tile<TM, TN, STAGES, KG, false, false, true>(V, G.k, G.m, by);
 }
 
 template <int TM, int TN, int STAGES, int KG = 1>
@@ -1313,6 +1338,16 @@ extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_dk2x2_glu(gemm_args G) { gemm_dl_glu<2, 2, 4>(G); }
 extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_dk4x4_glu(gemm_args G) { gemm_dl_glu<4, 4, 4>(G); }
+// one tensor with a residual added in the epilogue (gemm_dl_res), in the
+// shapes of dk2x2, dk4x4, dq1x1 and dq2x1
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk2x2_res(gemm_args G, const float *res) { gemm_dl_res<2, 2, 4, 2>(G, res); }
+extern "C" __global__ void __launch_bounds__(512)
+sllm_k_gemm_dk4x4_res(gemm_args G, const float *res) { gemm_dl_res<4, 4, 4, 2>(G, res); }
+extern "C" __global__ void __launch_bounds__(1024)
+sllm_k_gemm_dq1x1_res(gemm_args G, const float *res) { gemm_dl_res<1, 1, 16, 4>(G, res); }
+extern "C" __global__ void __launch_bounds__(1024)
+sllm_k_gemm_dq2x1_res(gemm_args G, const float *res) { gemm_dl_res<2, 1, 12, 4>(G, res); }
 // sixteen waves in four K groups over a 16 x 64 / 32 x 64 tile: for grids
 // of fewer workgroups than CUs (a lone tensor against a few tokens), each
 // group walks a quarter of the super-steps

@@ -89,6 +89,11 @@ SLLM_HIDDEN int         sllm_shim_gemm_qkv_rope(const sllm_gfx950_gemm_job jobs[
  * products. SLLM_SHIM_NOT_FUSED (nothing launched) where the token count
  * picks a tile without a gate + up form: the caller then runs the plain
  * GEMM and its own SiLU. */
+/* A chunk's single-tensor GEMM whose epilogue adds a residual of the
+ * output's shape: out = w . q (the f32 epilogue) + res. SLLM_SHIM_NOT_FUSED
+ * (nothing launched) where the token count picks a tile without that form. */
+SLLM_HIDDEN int         sllm_shim_gemm_res(const uint8_t *w, size_t n_rows, size_t n, const int8_t *q,
+                                           const sllm_gfx950_act *act, size_t m, float *out, const float *res);
 SLLM_HIDDEN int         sllm_shim_gemm_glu(const uint8_t *w_gate, const uint8_t *w_up, size_t n_rows, size_t n,
                                            const int8_t *q, const sllm_gfx950_act *act, size_t m, float *out);
 
