@@ -10,8 +10,9 @@ to 64 over a 70-token sequence (later chunks attend to keys earlier ones
 wrote), chunks over a restored 1024-position cache at tiny and BitNet-2B
 widths, chunks of 200 and 150 tokens (the scores' eight-token workgroups),
 the full 30-block 2B model in one 100-token chunk, 512-token chunks at 2B
-widths, the cache store folded into the Q + K + V GEMM (forced tiles), and
-decode / greedy generation carrying on after a chunk.
+widths, the cache store folded into the Q + K + V GEMM (forced tiles),
+widths where no GEMM epilogue is fused (384 / 640), and decode / greedy
+generation carrying on after a chunk.
 """
 import numpy as np
 import pytest
@@ -139,6 +140,27 @@ def test_chunks_above_128_tokens(amd, orc, dev):
     finally:
         g.close()
     assert np.array_equal(bits(got), bits(want)), _first_diff(got, want)
+
+
+def test_chunks_where_no_gemm_epilogue_is_fused(amd, orc, dev):
+    """Widths that are multiples of 128 but not of 256 (n_embd 384, n_ff
+    640): every projection takes the split-K tiles, which have no fused
+    epilogue, so the chunk runs its own cache store, SiLU and residual sums
+    (the 256-multiple widths of the other tests take the fused forms);
+    prefill in chunks of 7 and 100 tokens (the tiles on either side of 64),
+    every position's logits against the oracle."""
+    cfg = dict(TINY, n_layer=3, n_embd=384, n_ff=640, n_head=6, n_head_kv=2, n_rot=64, n_vocab=555)
+    model = amd.synth_model(cfg, 86)
+    toks = _tokens(140, cfg["n_vocab"], 87)
+    want = _oracle_logits(orc, model, 160, toks)
+    print("[chunk] widths 384 / 640: no fused GEMM epilogue", flush=True)
+    for chunk in (7, 100):
+        g = amd.DeviceDecoder(dev, model, 160)
+        try:
+            got = g.prefill_chunked(toks, chunk)
+        finally:
+            g.close()
+        assert np.array_equal(bits(got), bits(want)), f"chunk {chunk}: " + _first_diff(got, want)
 
 
 def _prefix_case(amd, orc, dev, widths):
