@@ -132,7 +132,8 @@ enum { IN_PLAIN = 0, IN_RESID = 1, IN_EMBED = 2, IN_SILU = 3 };
 #define CSW_LDS_PAD  98304u   /* its (unused) LDS: more than half a CU's, one workgroup per CU */
 #define CP_TOK       4    /* tokens per chunk p.V workgroup */
 #define CP_THREADS   1024 /* threads per chunk p.V workgroup: sixteen waves, one workgroup per CU */
-#define CSM_ROWS     4    /* softmax rows (one wave each) per chunk softmax workgroup */
+#define CSM_WAVES    4    /* waves per chunk softmax workgroup */
+#define CSM_HALF     256  /* rows of at most this many positions take half a wave */
 /* sllm_k_chk_kv_store stages a token's query row (n_head * hd = n_embd floats) in 7168 floats of LDS */
 _Static_assert(SLLM_GFX950_DEC_MAX_WIDTH <= 7168, "query row of the chunk KV store");
 
@@ -989,7 +990,12 @@ static int launch_chunk(sllm_gfx950_ctx *c, int32_t n, int32_t base, int all_log
         if (st == SLLM_GFX950_OK) {
             uint32_t n_tok = (uint32_t) n;
             void *margs[] = { &A, &n_tok };
-            st = sllm_shim_launch(c->f_csoft, (uint32_t) ((n * m->n_head + CSM_ROWS - 1) / CSM_ROWS), 1, CSM_ROWS * 64, 0,
+            /* the rows of at most CSM_HALF positions two to a wave,
+             * the others one (decode_kernels.hip: csm_short_rows) */
+            const uint32_t n_short = (uint32_t) (base >= CSM_HALF ? 0 : (n < CSM_HALF - base ? n : CSM_HALF - base)) *
+                                     (uint32_t) m->n_head;
+            const uint32_t waves = (n_short + 1) / 2 + (uint32_t) n * (uint32_t) m->n_head - n_short;
+            st = sllm_shim_launch(c->f_csoft, (waves + CSM_WAVES - 1) / CSM_WAVES, 1, CSM_WAVES * 64, 0,
                                   margs);
         }
         if (st == SLLM_GFX950_OK) {

@@ -1668,24 +1668,20 @@ sllm_k_chk_lm_head(chk_lm L) {
     }
 }
 
-// The chunk's softmax rows: one wave per (token, query head) row, the
-// decode step's operations (src/ops.c:386-422) -- the max; ggml_v_expf over
+// The chunk's softmax rows: one wave per (token, query head) row, or half
+// a wave for rows of at most 256 positions; the decode step's operations
+// (src/ops.c:386-422) -- the max; ggml_v_expf over
 // whole groups of eight, the C library's expf over the rest; the double sum
 // of the groups (((e0+e4) + (e1+e5)) + (e2+e6)) + (e3+e7) and of the tail
 // terms in any order, checked, in the reference's order when the check
 // cannot decide; inv = 1/sum -- then p_s = e_s * inv written back over the
 // row for s < npast (e recomputed for rows past 512 positions: the same
 // bits).
-constexpr int CSM_THREADS = 256;        // four rows per workgroup
+constexpr int CSM_THREADS = 256;        // four waves per workgroup
 
-extern "C" __global__ void __launch_bounds__(CSM_THREADS)
-sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
-    __shared__ uint64_t tab[32];
-    if (threadIdx.x < 32) tab[threadIdx.x] = c_expf_tab[threadIdx.x];
-    __syncthreads();
-    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t row_i = blockIdx.x * (CSM_THREADS / 64) + wave;
-    if (row_i >= n_tok * A.n_head) return;          // uniform
+// One row of at most 512 positions or more, a whole wave (lane l holds
+// positions 8l .. 8l + 7 of each block of 512)
+__device__ __forceinline__ void csm_full_row(const dec_attn &A, uint32_t row_i, uint32_t lane, const uint64_t *tab) {
     const uint32_t t = row_i / A.n_head, hh = row_i % A.n_head, ss = A.sc_stride;
     const uint32_t npast = A.chunk_base + t + 1, nb = npast / 8, nt = nb * 8;
     float *sc = A.scores + (size_t) t * A.n_head * ss + (size_t) hh * ss;
@@ -1821,6 +1817,143 @@ sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
             }
         }
     }
+}
+// The max and the double sum over the 32 lanes of each half of the wave
+// (every lane gets its half's), as wave_max / wave_sum_d
+__device__ __forceinline__ float half_max(float v) {
+    v = fmaxf(v, dpp_mov_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_mov_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_mov_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_mov_f<DPP_MIRROR>(v));
+    const float lo = fmaxf(lane_f(v, 0), lane_f(v, 16)), hi = fmaxf(lane_f(v, 32), lane_f(v, 48));
+    return (threadIdx.x & 32u) ? hi : lo;
+}
+
+__device__ __forceinline__ double half_sum_d(double v) {
+    v += dpp_mov_d<DPP_XOR1>(v);
+    v += dpp_mov_d<DPP_XOR2>(v);
+    v += dpp_mov_d<DPP_HALF_MIRROR>(v);
+    v += dpp_mov_d<DPP_MIRROR>(v);
+    const double lo = read_lane_d(v, 0) + read_lane_d(v, 16), hi = read_lane_d(v, 32) + read_lane_d(v, 48);
+    return (threadIdx.x & 32u) ? hi : lo;
+}
+
+// Rows of at most 256 positions, two to a wave: lanes 0..31 take row ra,
+// lanes 32..63 row rb (lane 32h + j holds positions 8j .. 8j + 7), each half
+// with the operations of csm_full_row over its own lanes. two = false: rb
+// repeats ra and its half stores nothing.
+constexpr uint32_t CSM_HALF = 256;
+
+__device__ __forceinline__ void csm_pair_rows(const dec_attn &A, uint32_t ra, uint32_t rb, bool two, uint32_t lane,
+                                              const uint64_t *tab) {
+    const uint32_t hw = lane >> 5, lh = lane & 31u, ss = A.sc_stride;
+    const uint32_t r = hw ? rb : ra;
+    const uint32_t t = r / A.n_head, hh = r % A.n_head;
+    const uint32_t npast = A.chunk_base + t + 1, nb = npast / 8, nt = nb * 8;
+    float *sc = A.scores + (size_t) t * A.n_head * ss + (size_t) hh * ss;
+    // each row's tail group (its lane within the half), for wave-uniform lane reads
+    const uint32_t lta = min((A.chunk_base + ra / A.n_head + 1) / 8u, 31u);
+    const uint32_t ltb = min((A.chunk_base + rb / A.n_head + 1) / 8u, 31u);
+
+    auto group_sum = [](const float (&e)[8]) {
+        const double t0 = (double) e[0] + (double) e[4], t1 = (double) e[1] + (double) e[5];
+        const double t2 = (double) e[2] + (double) e[6], t3 = (double) e[3] + (double) e[7];
+        return ((t0 + t1) + t2) + t3;
+    };
+    auto load8 = [&](uint32_t s, float (&v)[8]) {
+        const uint32_t at = min(s, ss - 8);
+        const f32x4 a = *G_CAST(const f32x4, sc + at), b = *G_CAST(const f32x4, sc + at + 4);
+        v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+        v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+    };
+
+    const uint32_t s = 8 * lh;
+    float v[8];
+    load8(s, v);
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, s + (uint32_t) i < npast ? v[i] : -INFINITY);
+    m = half_max(m);
+    // the tail group (npast - nt <= 7 terms, the C library's expf): term i of
+    // each half's tail evaluated by lane i of that half
+    {
+        const uint32_t cnt = npast - nt, lt = nt / 8u;
+        float xt = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float xa = lane_f(v[i], (int) lta), xb = lane_f(v[i], 32 + (int) ltb);
+            xt = lh == (uint32_t) i ? (hw ? xb : xa) : xt;
+        }
+        float et = 0.0f;
+        if (lh < cnt) et = sllm_libm_expf(xt - m, tab);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float ea = lane_f(et, i), eb = lane_f(et, 32 + i);
+            if (lh == lt && (uint32_t) i < cnt) v[i] = hw ? eb : ea;
+        }
+    }
+    double part = 0.0;
+    if (s < nt) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ggml_v_expf<true>(v[i] - m);
+        part = group_sum(v);
+    } else if (s < npast) {                        // the tail, term by term
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (s + (uint32_t) i < npast) part += (double) v[i];
+        }
+    }
+    // inv = 1/sum: checked, else the reference's order by the half's first lane
+    const double sum = half_sum_d(part);
+    const double bound = sum * ((double) (nb + (npast - nt) + 8) * 0x1p-52);
+    float inv = (float) (1.0 / (sum - bound));
+    if (inv != (float) (1.0 / (sum + bound))) {     // uniform over the half
+        if (lh == 0) {
+            double seq = 0.0;
+            for (uint32_t q = 0; q < nt; q += 8) {
+                float e[8];
+                load8(q, e);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) e[i] = ggml_v_expf<true>(e[i] - m);
+                seq += group_sum(e);
+            }
+            for (uint32_t q = nt; q < npast; ++q) seq += (double) sllm_libm_expf(sc[q] - m, tab);
+            inv = (float) (1.0 / seq);
+        }
+    }
+    {
+        const float ia = lane_f(inv, 0), ib = lane_f(inv, 32);
+        inv = hw ? ib : ia;
+    }
+    if (s < npast && (two || hw == 0)) {
+        *G_CAST(f32x4, sc + s) = (f32x4) { v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv };
+        *G_CAST(f32x4, sc + s + 4) = (f32x4) { v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv };
+    }
+}
+
+// The rows of tokens whose npast is at most CSM_HALF come first, two to a
+// wave, then one row per wave; the host sizes the grid with the same count
+// (csm_waves).
+__device__ __forceinline__ uint32_t csm_short_rows(const dec_attn &A, uint32_t n_tok) {
+    return (A.chunk_base >= CSM_HALF ? 0u : min(CSM_HALF - A.chunk_base, n_tok)) * A.n_head;
+}
+
+extern "C" __global__ void __launch_bounds__(CSM_THREADS)
+sllm_k_chk_softmax(dec_attn A, uint32_t n_tok) {
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = c_expf_tab[threadIdx.x];
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t w = blockIdx.x * (CSM_THREADS / 64) + wave;
+    const uint32_t n_short = csm_short_rows(A, n_tok), w_short = (n_short + 1) / 2;
+    if (w < w_short) {                              // uniform
+        const bool two = 2 * w + 1 < n_short;
+        csm_pair_rows(A, 2 * w, two ? 2 * w + 1 : 2 * w, two, lane, tab);
+        return;
+    }
+    const uint32_t row_i = n_short + (w - w_short);
+    if (row_i >= n_tok * A.n_head) return;          // uniform
+    csm_full_row(A, row_i, lane, tab);
 }
 
 // The chunk's p . V in units of one wave: (KV head, query head h, half of
