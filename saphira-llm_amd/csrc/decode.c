@@ -60,6 +60,8 @@ typedef struct k_dec_attn {
     float             attn_scale;
     uint32_t          n_head, n_kv, hd, half, n_ctx, sc_stride;
     uint32_t          chunk_base;
+    const uint8_t    *ahead;
+    uint64_t          ahead_bytes;
 } k_dec_attn;
 
 typedef struct k_dec_lm {
@@ -106,7 +108,7 @@ typedef struct k_dec_gemv_args {
 _Static_assert(sizeof(k_dec_step) == 64, "k_dec_step must match dec_step");
 _Static_assert(sizeof(k_dec_gemv_args) == 296, "k_dec_gemv_args must match dec_gemv_args");
 _Static_assert(sizeof(k_dec_stage) == 72, "k_dec_stage must match dec_stage");
-_Static_assert(sizeof(k_dec_attn) == 104, "k_dec_attn must match dec_attn");
+_Static_assert(sizeof(k_dec_attn) == 120, "k_dec_attn must match dec_attn");
 _Static_assert(sizeof(k_dec_lm) == 72, "k_dec_lm must match dec_lm");
 _Static_assert(sizeof(k_chk_prep) == 80, "k_chk_prep must match chk_prep");
 _Static_assert(sizeof(k_chk_lm) == 40, "k_chk_lm must match chk_lm");
@@ -505,7 +507,18 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
                 c->k_cache + (size_t) il * c->kv_per_layer, c->v_cache + (size_t) il * c->kv_per_layer,
                 c->rope, c->scores, c->attn, c->step, attn_scale,
                 (uint32_t) m->n_head, (uint32_t) m->n_head_kv, (uint32_t) m->hd, (uint32_t) half,
-                (uint32_t) n_ctx, sc_stride, 0 };
+                (uint32_t) n_ctx, sc_stride, 0, NULL, 0 };
+            /* what the chunk's scores kernel reads ahead: this layer's O,
+             * gate, up and down weights and the next layer's Q, K and V (one
+             * run of the model allocation, in that order) */
+            const dev_layer *D = &m->layers[il];
+            const int more = il + 1 < m->n_layer;
+            size_t rows, k;
+            proj_shape(m, more ? P_V : P_DOWN, &rows, &k);
+            const uint8_t *from = (const uint8_t *) D->w[P_O];
+            const uint8_t *to = (const uint8_t *) (more ? m->layers[il + 1].w[P_V] : D->w[P_DOWN]) + i2s_bytes(rows, k);
+            c->attn_args[il].ahead = from;
+            c->attn_args[il].ahead_bytes = (uint64_t) (to - from) & ~(uint64_t) 15;
         }
         c->lm_args = (k_dec_lm) { c->down, c->ffn_inp, m->output_norm, m->tok_embd, c->logits, c->lm_partial,
                                   c->step, m->eps, (uint32_t) m->n_embd, (uint32_t) m->n_vocab, 0 };

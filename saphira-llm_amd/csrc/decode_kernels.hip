@@ -388,8 +388,10 @@ struct dec_attn {
     uint32_t        n_head, n_kv, hd, half, n_ctx;
     uint32_t        sc_stride;          // scores row stride: n_ctx rounded up to 8
     uint32_t        chunk_base;         // chunk kernels: the position of the chunk's first token
+    const uint8_t  *ahead;              // chunk scores: bytes read ahead (this layer's O weights ..
+    uint64_t        ahead_bytes;        // the next layer's V weights), a multiple of 16
 };
-static_assert(sizeof(dec_attn) == 104, "dec_attn must match decode.c");
+static_assert(sizeof(dec_attn) == 120, "dec_attn must match decode.c");
 
 constexpr int ATT_THREADS = 256;
 constexpr uint32_t ATT_POS = 64;        // positions per scores workgroup
@@ -765,6 +767,21 @@ __device__ __forceinline__ void chk_scores_unit(const dec_attn &A, uint32_t n_to
 
 extern "C" __global__ void __launch_bounds__(CSW_THREADS)
 sllm_k_chk_scores_w(dec_attn A, uint32_t n_tok) {
+    // the GEMMs that follow read their weights from HBM with few loads in
+    // flight; this VALU-bound kernel leaves the bandwidth idle, so it reads
+    // them first (five 16-byte loads per thread over the whole grid, used
+    // only at the end): they then come from the Infinity Cache
+    constexpr int AHEAD = 5;
+    u32x4 ahead[AHEAD];
+    {
+        const size_t n16 = A.ahead_bytes / 16, stride = (size_t) gridDim.x * CSW_THREADS;
+        const GLOBAL u32x4 *src = G_CAST(const u32x4, A.ahead);
+#pragma unroll
+        for (int j = 0; j < AHEAD; ++j) {
+            const size_t at = (size_t) blockIdx.x * CSW_THREADS + threadIdx.x + (size_t) j * stride;
+            ahead[j] = at < n16 ? src[at] : (u32x4) { 0u, 0u, 0u, 0u };
+        }
+    }
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t G = gridDim.x, cu = blockIdx.x, nkh = A.n_head;
     const uint32_t grp = A.n_head / A.n_kv;
@@ -787,6 +804,12 @@ sllm_k_chk_scores_w(dec_attn A, uint32_t n_tok) {
         const uint32_t before = tb8 > 0 ? __builtin_amdgcn_readlane(inc, tb8 - 1u) : 0u;
         chk_scores_unit(A, n_tok, kh / grp, kh % grp, tb8 * CSW_TOK, (p - before) * ATT_POS, lane);
     }
+    // keep the read-ahead loads: their value goes nowhere (blockIdx.x never
+    // equals gridDim.x)
+    u32x4 x = ahead[0];
+#pragma unroll
+    for (int k = 1; k < AHEAD; ++k) x ^= ahead[k];
+    if (blockIdx.x == gridDim.x) A.scores[0] = (float) (x[0] ^ x[1] ^ x[2] ^ x[3]);
 }
 
 // Softmax and p . V: workgroup (two query heads of a KV head, 8 head
