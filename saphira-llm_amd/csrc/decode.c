@@ -608,9 +608,14 @@ static int launch_token(sllm_gfx950_ctx *c) {
             st = sllm_shim_launch(c->f_gemv, A->n_wg, 1, SLLM_SLAB_THREADS, 0, args);
             if (s == S_QKV && st == SLLM_GFX950_OK) {
                 void *aargs[] = { &c->attn_args[il] };
-                st = sllm_shim_launch(c->f_scores, (uint32_t) m->n_head_kv, kv_chunks, ATT_THREADS, 0, aargs);
+                /* at most eight KV heads: eight columns of workgroups, KV head h
+                 * in column h (XCD h) for both kernels (decode_kernels.hip) */
+                const int cols = m->n_head_kv <= 8;
+                if (cols) st = sllm_shim_launch(c->f_scores, 8u * kv_chunks, 1, ATT_THREADS, 0, aargs);
+                else st = sllm_shim_launch(c->f_scores, (uint32_t) m->n_head_kv, kv_chunks, ATT_THREADS, 0, aargs);
                 if (st == SLLM_GFX950_OK) {
-                    st = sllm_shim_launch(c->f_pv, (uint32_t) m->n_head_kv * slices * pv_wpk, 1, PV_THREADS, 0, aargs);
+                    const uint32_t n_pv = (cols ? 8u : (uint32_t) m->n_head_kv) * slices * pv_wpk;
+                    st = sllm_shim_launch(c->f_pv, n_pv, 1, PV_THREADS, 0, aargs);
                 }
             }
         }

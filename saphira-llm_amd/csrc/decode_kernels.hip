@@ -491,7 +491,14 @@ template <bool CHUNK>
 __device__ __forceinline__ void scores_body(const dec_attn &A) {
     __shared__ __attribute__((aligned(16))) float qr[ATT_MAX_GRP][ATT_MAX_HD];
     __shared__ __attribute__((aligned(16))) float kt[ATT_POS][KT_STRIDE];
-    const uint32_t kvh = blockIdx.x, s0 = blockIdx.y * ATT_POS, tid = threadIdx.x;
+    // decode step, at most eight KV heads: a one-dimensional grid of eight
+    // columns, KV head h in column h (workgroups go to the eight XCDs in
+    // turn), so that the scores land in the L2 of the XCD whose p.V
+    // workgroups read them; the other columns return at once
+    const bool xcd = !CHUNK && A.n_kv <= 8;
+    const uint32_t kvh = xcd ? blockIdx.x % 8u : blockIdx.x;
+    const uint32_t s0 = (xcd ? blockIdx.x / 8u : blockIdx.y) * ATT_POS, tid = threadIdx.x;
+    if (kvh >= A.n_kv) return;
     const uint32_t t = CHUNK ? blockIdx.z : 0u;
     const uint32_t pos = CHUNK ? A.chunk_base + t : (uint32_t) A.step->pos, npast = pos + 1;
     if (s0 >= npast) return;
@@ -849,14 +856,21 @@ __device__ __forceinline__ void pv_body(const dec_attn &A) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t grp = A.n_head / A.n_kv, hd = A.hd, ss = A.sc_stride, slices = hd / PV_SLICE;
     const uint32_t wpk = (grp + PV_HPW - 1) / PV_HPW;      // workgroups per (KV head, slice)
-    // workgroup -> (KV head, slice, its first query head): the workgroups of
-    // one (KV head, slice) on one XCD (workgroups go to the eight XCDs in
-    // turn) when the grid allows
+    // workgroup -> (KV head, slice, its first query head). At most eight KV
+    // heads: KV head h's workgroups all in column h of eight (XCD h, where
+    // sllm_k_dec_scores left its scores and where its slices of V are read
+    // twice), the other columns returning at once. Else the workgroups of
+    // one (KV head, slice) on one XCD when the grid allows.
     uint32_t kvh, slice, j;
     {
         const uint32_t total = A.n_kv * slices * wpk, L = blockIdx.x;
         uint32_t p;
-        if (total % (8 * wpk) == 0) {
+        if (A.n_kv <= 8) {
+            if (L % 8u >= A.n_kv) return;
+            const uint32_t r = L / 8u;
+            p = (L % 8u) * slices + r / wpk;
+            j = r % wpk;
+        } else if (total % (8 * wpk) == 0) {
             const uint32_t per = total / 8, x = L % 8, r = L / 8;
             p = x * (per / wpk) + r / wpk;
             j = r % wpk;
