@@ -125,6 +125,7 @@ static struct {
     hipFunction_t  k_copy;
     hipFunction_t  k_gemm[15];
     hipFunction_t  k_gemm_t[5];
+    hipFunction_t  k_gemm_s;             /* plans of a few tokens as one stream per workgroup */
     hipFunction_t  k_gemm_rope[2];       /* dk2x2, dk4x4 with the chunk's cache store */
     hipFunction_t  k_gemm_glu[2];        /* dk2x2, dk4x4 gate + up with silu(gate) * up */
     hipFunction_t  k_gemm_res[4];        /* dk2x2, dk4x4, dq1x1, dq2x1 with a residual added */
@@ -261,6 +262,7 @@ static int load_functions(void) {
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[2], g.mod, "sllm_k_gemm_tdk2x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[3], g.mod, "sllm_k_gemm_tdk4x2"));
     HIP_TRY(hipModuleGetFunction(&g.k_gemm_t[4], g.mod, "sllm_k_gemm_tdk4x4"));
+    HIP_TRY(hipModuleGetFunction(&g.k_gemm_s, g.mod, "sllm_k_gemm_s1"));
     for (int i = 0; i < N_LPR; ++i) HIP_TRY(hipModuleGetFunction(&g.k_stream[i], g.mod, k_stream_names[i]));
     g.force_variant = -1;
     return SLLM_GFX950_OK;
@@ -1291,12 +1293,146 @@ _Static_assert(sizeof(k_gemm_table) == 24, "k_gemm_table must match gemm_table i
 /* the plan kernels: the tile shapes 6, 7, 13, 11 and 10 over a table */
 static const int k_gemm_t_shape[5] = { 5, 6, 12, 10, 9 };
 
+/* a streamed plan (i2s_kernels.hip: gemm_srec, gemm_stream) */
+typedef struct k_gemm_srec {
+    const uint8_t         *w;
+    const int8_t          *q;
+    float                 *out;
+    int32_t               *out_i;
+    const sllm_gfx950_act *act;
+    const float           *ws;
+    uint32_t               k, rows, n_rows, vec;
+} k_gemm_srec;
+
+typedef struct k_gemm_stream {
+    const k_gemm_srec *recs;
+    const uint32_t    *range;
+    const void        *pad0;
+    uint32_t           m, gy, n_ranges, pad;
+} k_gemm_stream;
+
+_Static_assert(sizeof(k_gemm_srec) == 64, "k_gemm_srec must match gemm_srec in i2s_kernels.hip");
+_Static_assert(sizeof(k_gemm_stream) == 40, "k_gemm_stream must match gemm_stream in i2s_kernels.hip");
+
+#define GS_ROWS 128u          /* rows per streamed tile */
+#define GS_STEPS 2u           /* 256-k super-steps per iteration */
+#define GS_TOKENS 4           /* plans of at most this many tokens stream (measured on the 96 FFN */
+                              /* tensors: 4 tokens 90.7 against 93.1 us, 16 tokens 105.7 against 102.6) */
+#define GS_RMAX 64u           /* tiles per run, as the kernel's LDS holds them */
+
 struct sllm_gfx950_gemm_plan {
-    uint8_t      *tables_dev;     /* jobs, then the row tile -> job map */
+    uint8_t      *tables_dev;     /* jobs, then the row tile -> job map; or the stream's tables */
     k_gemm_table  table;
+    k_gemm_stream stream;
     uint32_t      gx, gy;
-    int           kind;           /* index into k_gemm_t */
+    int           kind;           /* index into k_gemm_t, or 5: the stream */
 };
+
+/* The stream's tables: every tile of rows_per rows of the jobs in order,
+ * cut into runs of about equal iteration counts (ss 256-k super-steps
+ * each), at most GS_RMAX tiles per run and at least one run per CU where
+ * there are tiles enough. Host memory: recs, then range[n_runs + 1]. */
+static int gemm_stream_tables(const sllm_gfx950_gemm_plan_job *jobs, size_t n_jobs, uint32_t rows_per, uint32_t ss,
+                              uint8_t **host_out, size_t *bytes_out, uint32_t *n_tiles_out, uint32_t *n_runs_out) {
+    uint64_t n_tiles = 0, total = 0;
+    for (size_t j = 0; j < n_jobs; ++j) {
+        const uint64_t t = (jobs[j].n_rows + rows_per - 1) / rows_per;
+        n_tiles += t;
+        total += t * ((jobs[j].n / 256 + ss - 1) / ss);
+    }
+    if (n_tiles == 0 || n_tiles > UINT32_MAX / 2) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm_plan: tiles");
+    uint32_t n_runs = (uint32_t) ((n_tiles + 47) / 48);
+    if (n_runs < (uint32_t) g.cu) n_runs = (uint32_t) g.cu;
+    if (n_runs > n_tiles) n_runs = (uint32_t) n_tiles;
+    uint32_t *it = malloc(n_tiles * sizeof *it);
+    if (it == NULL) return fail(SLLM_GFX950_ERR_NOMEM, "gemm_plan: host tables");
+    uint8_t *host = NULL;
+    for (;;) {
+        const size_t bytes = n_tiles * sizeof(k_gemm_srec) + ((size_t) n_runs + 1) * sizeof(uint32_t);
+        free(host);
+        host = malloc(bytes);
+        if (host == NULL) {
+            free(it);
+            return fail(SLLM_GFX950_ERR_NOMEM, "gemm_plan: host tables");
+        }
+        k_gemm_srec *rec = (k_gemm_srec *) host;
+        uint32_t *range = (uint32_t *) (host + n_tiles * sizeof(k_gemm_srec));
+        uint32_t t = 0;
+        for (size_t j = 0; j < n_jobs; ++j) {
+            const sllm_gfx950_gemm_plan_job *J = &jobs[j];
+            const size_t kb = J->n / 4;
+            const int vec = J->n_rows % 4 == 0 && ((uintptr_t) J->out & 15u) == 0 && ((uintptr_t) J->rows_out & 15u) == 0;
+            for (size_t n0 = 0; n0 < J->n_rows; n0 += rows_per, ++t) {
+                const size_t rows = J->n_rows - n0 < rows_per ? J->n_rows - n0 : rows_per;
+                rec[t] = (k_gemm_srec) { J->w + n0 * kb, J->q, J->out ? J->out + n0 : NULL,
+                                         J->rows_out ? J->rows_out + n0 : NULL, J->act,
+                                         (const float *) (J->w + J->n_rows * kb), (uint32_t) J->n, (uint32_t) rows,
+                                         (uint32_t) J->n_rows, (uint32_t) vec };
+                it[t] = (uint32_t) ((J->n / 256 + ss - 1) / ss);
+            }
+        }
+        /* run r ends at the tile boundary nearest to (r + 1) total / n_runs */
+        uint64_t done = 0;
+        t = 0;
+        for (uint32_t r = 0; r < n_runs; ++r) {
+            range[r] = t;
+            const uint64_t target = total * (r + 1) / n_runs;
+            uint32_t cnt = 0;
+            uint64_t acc = 0;
+            while (t < n_tiles && cnt < GS_RMAX &&
+                   (cnt == 0 || r + 1 == n_runs || 2 * (done + acc) + it[t] <= 2 * target)) {
+                acc += it[t];
+                ++t;
+                ++cnt;
+            }
+            done += acc;
+        }
+        range[n_runs] = t;
+        if (t == n_tiles) {
+            *host_out = host;
+            *bytes_out = bytes;
+            *n_tiles_out = (uint32_t) n_tiles;
+            *n_runs_out = n_runs;
+            free(it);
+            return SLLM_GFX950_OK;
+        }
+        n_runs += 8;                            /* a run hit GS_RMAX: cut finer */
+    }
+}
+
+static int gemm_plan_stream(const sllm_gfx950_gemm_plan_job *jobs, size_t n_jobs, size_t m,
+                            sllm_gfx950_gemm_plan **plan) {
+    uint8_t *host = NULL;
+    size_t bytes = 0;
+    uint32_t n_tiles = 0, n_runs = 0;
+    int st = gemm_stream_tables(jobs, n_jobs, GS_ROWS, GS_STEPS, &host, &bytes, &n_tiles, &n_runs);
+    if (st != SLLM_GFX950_OK) return st;
+    sllm_gfx950_gemm_plan *p = calloc(1, sizeof *p);
+    if (p == NULL) {
+        free(host);
+        return fail(SLLM_GFX950_ERR_NOMEM, "gemm_plan: host tables");
+    }
+    hipError_t e = hipMalloc((void **) &p->tables_dev, bytes);
+    if (e != hipSuccess) {
+        p->tables_dev = NULL;
+    } else {
+        e = hipMemcpy(p->tables_dev, host, bytes, hipMemcpyHostToDevice);
+    }
+    free(host);
+    if (e != hipSuccess) {
+        if (p->tables_dev) hipFree(p->tables_dev);
+        free(p);
+        return hip_fail(e, "gemm_plan: tables");
+    }
+    const uint32_t gy = (uint32_t) ((m + 15) / 16);    /* 16 tokens per token tile */
+    const uint32_t *range = (const uint32_t *) (p->tables_dev + (size_t) n_tiles * sizeof(k_gemm_srec));
+    p->stream = (k_gemm_stream) { (const k_gemm_srec *) p->tables_dev, range, NULL, (uint32_t) m, gy, n_runs, 0 };
+    p->gx = 8u * gy * ((n_runs + 7u) / 8u);
+    p->gy = 1;
+    p->kind = 5;
+    *plan = p;
+    return SLLM_GFX950_OK;
+}
 
 int sllm_gfx950_gemm_plan_create(const sllm_gfx950_gemm_plan_job *jobs, size_t n_jobs, size_t m,
                                  sllm_gfx950_gemm_plan **plan) {
@@ -1316,9 +1452,16 @@ int sllm_gfx950_gemm_plan_create(const sllm_gfx950_gemm_plan_job *jobs, size_t n
         if ((uint64_t) m * J->n_rows > (uint64_t) 1 << 40) return fail(SLLM_GFX950_ERR_TOO_LARGE, "gemm_plan: m x rows too large");
     }
     /* the tile: forced, or by token count (measured on the FFN tensors of
-     * 32 weight sets: 32 x 128 up to 32 tokens, 64 x 256 above) */
+     * 32 weight sets: the stream up to GS_TOKENS, 32 x 128 up to 32 tokens,
+     * 64 x 256 above) */
     int kind = -1;
     for (int i = 0; i < 5; ++i) if (g.force_gemm_tile - 1 == k_gemm_t_shape[i]) kind = i;
+    if (kind < 0 && g.force_gemm_tile == 0 && m <= GS_TOKENS) {
+        /* the stream, where every job's outputs are within its buffers' 32-bit offsets */
+        int ok = 1;
+        for (size_t j = 0; j < n_jobs; ++j) if ((uint64_t) m * jobs[j].n_rows * 4 > 0x7FFFFFFFu) ok = 0;
+        if (ok) return gemm_plan_stream(jobs, n_jobs, m, plan);
+    }
     if (kind < 0) kind = m <= 32 ? 2 : 4;
     const int shape = k_gemm_t_shape[kind];
     const uint32_t rows_per = k_gemm_rows[shape], tok_per = k_gemm_tokens[shape];
@@ -1369,6 +1512,12 @@ int sllm_gfx950_gemm_plan_create(const sllm_gfx950_gemm_plan_job *jobs, size_t n
 int sllm_gfx950_gemm_plan_run(const sllm_gfx950_gemm_plan *p) {
     NEED_OPEN();
     if (p == NULL) return fail(SLLM_GFX950_ERR_ARG, "gemm_plan_run: NULL plan");
+    if (p->kind >= 5) {
+        k_gemm_stream sa = p->stream;
+        void *sargs[] = { &sa };
+        HIP_TRY(hipModuleLaunchKernel(g.k_gemm_s, p->gx, 1, 1, 512, 1, 1, 0, g.stream, sargs, NULL));
+        return SLLM_GFX950_OK;
+    }
     k_gemm_table t = p->table;
     void *args[] = { &t };
     HIP_TRY(hipModuleLaunchKernel(g.k_gemm_t[p->kind], p->gx, p->gy, 1, k_gemm_threads[k_gemm_t_shape[p->kind]],

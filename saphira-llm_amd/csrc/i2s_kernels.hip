@@ -1118,6 +1118,359 @@ __device__ __forceinline__ void gemm_dl_table(const gemm_table &T) {
     gemm_dl_tile<TM, TN, STAGES, KG>(V, J.k, T.m, by);
 }
 
+// ---------------------------------------------------------------------------
+// GEMM plans of a few tokens as one stream per workgroup
+// ---------------------------------------------------------------------------
+//
+// A plan's row tiles (128 rows of one tensor each) are cut into contiguous
+// runs of about equal weight bytes, one run per workgroup (with several
+// token tiles, one workgroup per run and token tile). The workgroup streams
+// its run through one ring of LDS stages, as the direct-load tiles do, but
+// the ring does not stop at a tile's end: the copies run D - 1 iterations
+// ahead across tile boundaries, so a tile's start never waits for memory
+// and its epilogue runs while the next tile's copies are in flight. Each
+// tile's sums go to one of two LDS tiles at its last iteration and are
+// stored at the next one. The stores are buffer stores, always issued
+// (lanes with nothing to store aim past the buffer), so that every wave
+// knows how many vector memory instructions it has issued, and each wait
+// for an iteration's copies names exactly the instructions issued after
+// them (loads and stores complete in order).
+
+// One row tile of a streamed plan (mirrored in gfx950_shim.c).
+struct gemm_srec {
+    const uint8_t *w;          // the tile's first weight row; rows past `rows` clamp to its last
+    const int8_t  *q;          // the job's int8 token rows [m][k]
+    float         *out;        // the job's [m][n_rows] epilogue from the tile's first column, or null
+    int32_t       *out_i;      // raw dots from the tile's first column, or null
+    const act_t   *act;        // [m], or null without an epilogue
+    const float   *ws;         // the tensor's w_scale
+    uint32_t       k, rows, n_rows, vec;   // vec: float4 stores (n_rows % 4 == 0, outputs 16-byte aligned)
+};
+static_assert(sizeof(gemm_srec) == 64, "gemm_srec must match gfx950_shim.c");
+
+struct gemm_stream {
+    const gemm_srec *recs;     // every tile of the plan, in stream order
+    const uint32_t  *range;    // [n_ranges + 1]: run r is recs[range[r] .. range[r + 1])
+    const void      *pad0;
+    uint32_t         m, gy, n_ranges, pad;
+};
+static_assert(sizeof(gemm_stream) == 40, "gemm_stream must match gfx950_shim.c");
+
+constexpr uint32_t GS_RMAX = 64;       // tiles per run (the host cuts longer runs)
+constexpr int GS_THREADS = 512;        // two K groups of four waves
+
+// s_waitcnt vmcnt(n) for a uniform n (clamped to 63): a binary search over
+// the immediates
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vmem_rt(uint32_t n) {
+    if constexpr (LO == HI) {
+        wait_vmem<LO>();
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n <= (uint32_t) MID) wait_vmem_rt<LO, MID>(n);
+        else wait_vmem_rt<MID + 1, HI>(n);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    const uint64_t v = (uint64_t) (uintptr_t) p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t) v), hi = __builtin_amdgcn_readfirstlane((uint32_t) (v >> 32));
+    return (T *) (uintptr_t) (((uint64_t) hi << 32) | lo);
+}
+
+// 16 tokens x 128 rows per tile; an iteration is two super-steps, one per
+// K group (128 bytes of each weight row); D iterations in the ring.
+// (Measured slower on the 96 FFN tensors: 64-row tiles reading 256 bytes of
+// each row per iteration, and 32 x 128 tiles with a shallower ring.)
+template <int D>
+__device__ __forceinline__ void gemm_stream_body(const gemm_stream &P) {
+    constexpr int TM = 1, TN = 2, SPG = 1;
+    constexpr int KG = 2, SS = KG * SPG;           // super-steps per iteration
+    constexpr uint32_t BM = 16u * TM, BN = 64u * TN;
+    constexpr uint32_t A_BYTES = BM * 256u, PB = 64u * SS, CR = 4u * SS, WSLOT = BN * PB;
+    constexpr int VM = (TM + TN) * SPG;            // copies per wave per iteration (and one more at a tile's first)
+    static_assert(D >= 2 && D * (VM + 1) + 8 * TM < 64, "ring");
+    constexpr uint32_t A_REGION = (uint32_t) (SS * D) * A_BYTES, W_REGION = D * WSLOT;
+    constexpr uint32_t EP = BN + 4u, E_TILE = BM * EP * 4u, E_SET = KG * E_TILE;
+    constexpr uint32_t EPS = 8u, EP_SLOT = 512u;   // a tile's act dwords, then w_scale at dword 127
+    static_assert(2u * BM < 127u && EPS > (uint32_t) D, "tile constants");
+    constexpr uint32_t OFF_E = A_REGION + W_REGION, OFF_EPS = OFF_E + 2u * E_SET, OFF_REC = OFF_EPS + EPS * EP_SLOT;
+    constexpr uint32_t S_BYTES = OFF_REC + GS_RMAX * (uint32_t) sizeof(gemm_srec);
+    static_assert(S_BYTES <= 160u * 1024u, "LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t S[S_BYTES];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wave = wave_all & 3u, kgrp = wave_all >> 2;
+    const uint32_t g = lane >> 4, li = lane & 15u;
+
+    // workgroup -> (token tile, run): the token tiles of one run on one XCD
+    const uint32_t xcd = blockIdx.x & 7u, a8 = blockIdx.x >> 3;
+    const uint32_t by = a8 % P.gy, run = (a8 / P.gy) * 8u + xcd;
+    if (run >= P.n_ranges) return;                 // uniform
+    const uint32_t r0 = P.range[run], nt = min(P.range[run + 1] - r0, GS_RMAX);
+    if (nt == 0) return;
+    gemm_srec *R = reinterpret_cast<gemm_srec *>(S + OFF_REC);
+    for (uint32_t i = tid; i < nt * 4u; i += (uint32_t) GS_THREADS)
+        reinterpret_cast<u32x4 *>(R)[i] = G_CAST(const u32x4, P.recs + r0)[i];
+    __syncthreads();
+    // the run's iterations, from its tiles' K: lane i takes tile i (nt <= 64)
+    const uint32_t total = (uint32_t) wave_sum(lane < nt ? (int) ((R[lane].k / 256u + SS - 1) / SS) : 0);
+
+    const uint32_t m = P.m, t0 = by * BM;
+    // copy lanes: token row and (swizzled) granule of copy j; weight row and chunk
+    constexpr int NB = TN * SPG;                   // weight copies per wave per iteration
+    uint32_t a_t[TM], a_g[TM], b_r[NB], bch[NB];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
+        a_t[j] = p >> 4;
+        a_g[j] = (p & 15u) ^ (a_t[j] & 15u);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const uint32_t p = ((uint32_t) j * 4u + wave) * 64u + lane;
+        b_r[j] = kgrp * (BN / KG) + p / CR;
+        bch[j] = (p % CR) ^ (b_r[j] & 7u);
+    }
+
+    // the producer: tile pt, its iteration pit
+    const int8_t *asrc[TM];
+    const uint8_t *bsrc[NB];
+    const uint32_t *epsrc = nullptr;
+    uint32_t pt = 0, pit = 0, p_iters = 1, p_nsup = 1, gp = 0, ops = 0;
+    auto p_enter = [&](uint32_t t) {
+        const gemm_srec &rc = R[t];
+        const uint32_t k = __builtin_amdgcn_readfirstlane(rc.k), kb = k >> 2;
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(rc.rows);
+        const int8_t *q = uniform_ptr(rc.q);
+        const uint8_t *w = uniform_ptr(rc.w);
+        const act_t *act = uniform_ptr(rc.act);
+        const float *ws = uniform_ptr(rc.ws);
+        p_nsup = k / 256u;
+        p_iters = (p_nsup + SS - 1) / SS;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) asrc[j] = q + (size_t) min(t0 + a_t[j], m - 1) * k + a_g[j] * 16u;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bsrc[j] = w + (size_t) min(b_r[j], rows - 1) * kb;
+        const uint32_t d = 64u * (wave & 1u) + lane;
+        epsrc = act != nullptr && d < 2u * BM
+            ? reinterpret_cast<const uint32_t *>(act + min(t0 + d / 2u, m - 1)) + (d & 1u)
+            : reinterpret_cast<const uint32_t *>(ws);
+    };
+    // the producer's next iteration: each K group its super-step's tokens and
+    // its half of the iteration's weight rows (whole lines: 8 rows x 128
+    // bytes per instruction); at a tile's first iteration also the tile's
+    // act and w_scale, one dword per lane
+    auto issue = [&]() {
+        const uint32_t slot = gp % (uint32_t) D;
+#pragma unroll
+        for (int u = 0; u < SPG; ++u) {
+            const uint32_t l = SPG * kgrp + (uint32_t) u, s = min(SS * pit + l, p_nsup - 1);
+            uint8_t *abase = S + (SS * slot + l) * A_BYTES;
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                // four token rows per copy; none past the last token (their
+                // sums are never stored, whatever the slot holds)
+                if (((uint32_t) j * 4u + wave) * 4u < m - t0) {        // uniform per wave
+                    __builtin_amdgcn_global_load_lds((const void *) (asrc[j] + s * 256u),
+                                                     LDS_PTR(abase + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+                    ops += 1u;
+                }
+            }
+        }
+        uint8_t *wbase = S + A_REGION + slot * WSLOT + kgrp * (BN / KG) * PB;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t ch = SS * pit + bch[j] / 4u < p_nsup ? bch[j] : (bch[j] & 3u);
+            __builtin_amdgcn_global_load_lds((const void *) (bsrc[j] + pit * PB + ch * 16u),
+                                             LDS_PTR(wbase + ((uint32_t) j * 4u + wave) * 1024u), 16, 0, 0);
+        }
+        ops += (uint32_t) NB;
+        if (pit == 0) {                            // uniform
+            __builtin_amdgcn_global_load_lds((const void *) epsrc,
+                                             LDS_PTR(S + OFF_EPS + (pt % EPS) * EP_SLOT + (wave & 1u) * 256u), 4, 0, 0);
+            ops += 1u;
+        }
+        ++gp;
+        if (++pit == p_iters) {
+            pit = 0;
+            if (++pt < nt) p_enter(pt);
+        }
+    };
+
+    // the stores of tile u, whose sums are in E set u % 2 (rows of 32 lanes x
+    // four columns, two rows per instruction): (float)(dot - sum) * (w_scale /
+    // act_scale), src/i2s_gemm.c:271-290
+    auto store_tile = [&](uint32_t u) {
+        const gemm_srec &rc = R[u];
+        float *out = uniform_ptr(rc.out);
+        int32_t *out_i = uniform_ptr(rc.out_i);
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(rc.rows), n_rows = __builtin_amdgcn_readfirstlane(rc.n_rows);
+        const bool vec = __builtin_amdgcn_readfirstlane(rc.vec) != 0u;
+        const uint32_t *cst = reinterpret_cast<const uint32_t *>(S + OFF_EPS + (u % EPS) * EP_SLOT);
+        const float ws = __uint_as_float(cst[127]);
+        const uint8_t *E0 = S + OFF_E + (u & 1u) * E_SET;
+        const uint32_t limit = ((m - 1u) * n_rows + rows) * 4u;     // bytes from the tile's first column
+        constexpr uint32_t LPT = BN / 4u, RPS = 64u / LPT;
+        const uint32_t srow = lane / LPT, scol = 4u * (lane % LPT);
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, (short) 0, (int) limit, 0x00020000);
+        const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc(out_i, (short) 0, (int) limit, 0x00020000);
+        for (uint32_t row0 = wave_all * RPS; row0 < BM; row0 += 8u * RPS) {    // uniform per wave
+            const uint32_t row = row0 + srow, t = t0 + row;
+            i32x4v d = *reinterpret_cast<const i32x4v *>(E0 + (row * EP + scol) * 4u);
+            d += *reinterpret_cast<const i32x4v *>(E0 + E_TILE + (row * EP + scol) * 4u);
+            const bool ok = t < m && scol < rows;
+            const uint32_t at = ok ? (t * n_rows + scol) * 4u : 0xFFFFFFF0u;
+            if (out_i != nullptr) {                // uniform
+                if (vec) {
+                    __builtin_amdgcn_raw_buffer_store_b128((u32x4) d, ri, (int) at, 0, CPOL_NT);
+                    ops += 1u;
+                } else {
+#pragma unroll
+                    for (uint32_t e = 0; e < 4u; ++e) {
+                        const uint32_t ae = ok && scol + e < rows ? at + 4u * e : 0xFFFFFFF0u;
+                        __builtin_amdgcn_raw_buffer_store_b32((uint32_t) d[e], ri, (int) ae, 0, CPOL_NT);
+                    }
+                    ops += 4u;
+                }
+            }
+            if (out != nullptr) {                  // uniform
+                const float sc = __uint_as_float(cst[2u * row]);
+                const int32_t sum = (int32_t) cst[2u * row + 1u];
+                const float post = ws / sc;
+                u32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = __float_as_uint((float) (d[e] - sum) * post);
+                if (vec) {
+                    __builtin_amdgcn_raw_buffer_store_b128(v, ro, (int) at, 0, CPOL_NT);
+                    ops += 1u;
+                } else {
+#pragma unroll
+                    for (uint32_t e = 0; e < 4u; ++e) {
+                        const uint32_t ae = ok && scol + e < rows ? at + 4u * e : 0xFFFFFFF0u;
+                        __builtin_amdgcn_raw_buffer_store_b32(v[e], ro, (int) ae, 0, CPOL_NT);
+                    }
+                    ops += 4u;
+                }
+            }
+        }
+    };
+
+    uint32_t aoff[4];                              // token 16 tm + li (tm * 4096 added), granule of step f
+#pragma unroll
+    for (int f = 0; f < 4; ++f) aoff[f] = li * 256u + (((8u * (g >> 1) + 2u * (uint32_t) f + (g & 1u)) ^ li) * 16u);
+    const uint32_t wr = wave * (16u * TN);         // this wave's first row in the tile
+    constexpr uint32_t BROW16 = 16u * PB;
+    i32x4v c[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
+
+    p_enter(0);
+    uint32_t mk[D - 1];                            // ops issued up to iteration G + i's copies
+#pragma unroll
+    for (int i = 0; i < D - 1; ++i) {
+        if (gp < total) issue();
+        mk[i] = ops;
+    }
+    uint32_t ct = 0, cit = 0;
+    uint32_t c_nsup = __builtin_amdgcn_readfirstlane(R[0].k) / 256u, c_iters = (c_nsup + SS - 1) / SS;
+    bool pend = false;                             // tile ct - 1's sums wait in E
+    for (uint32_t G = 0; G < total; ++G) {
+        wait_vmem_rt<0, 63>(min(ops - mk[0], 63u));   // this iteration's copies done
+        __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's LDS reads and writes done
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (gp < total) issue();
+#pragma unroll
+        for (int i = 0; i < D - 2; ++i) mk[i] = mk[i + 1];
+        mk[D - 2] = ops;
+        __builtin_amdgcn_sched_barrier(0);
+        if (pend) {                                // uniform
+            store_tile(ct - 1);
+            pend = false;
+        }
+#pragma unroll
+        for (int u = 0; u < SPG; ++u) {
+        const uint32_t l = SPG * kgrp + (uint32_t) u;
+        if (SS * cit + l < c_nsup) {               // past the tile's last super-step: nothing
+            const uint32_t slot = G % (uint32_t) D;
+            const uint8_t *st = S + (SS * slot + l) * A_BYTES;
+            const uint8_t *sw = S + slot * WSLOT;
+            const uint32_t boff = A_REGION + (wr + li) * PB + (((4u * l + g) ^ (li & 7u)) * 16u);
+            u32x4 raw[TN];
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) raw[tn] = *reinterpret_cast<const u32x4 *>(sw + boff + (uint32_t) tn * BROW16);
+            i32x4v av[2][TM], bv[2][TN];
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) av[0][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[0] + (uint32_t) tm * 4096u);
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) bv[0][tn][dd] = (int32_t) ((raw[tn][dd] >> 6u) & 0x03030303u);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                const int cu = f & 1, nx = cu ^ 1;
+                if (f < 3) {
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+                        av[nx][tm] = *reinterpret_cast<const i32x4v *>(st + aoff[f + 1] + (uint32_t) tm * 4096u);
+#pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                        for (int dd = 0; dd < 4; ++dd)
+                            bv[nx][tn][dd] = (int32_t) ((raw[tn][dd] >> (4u - 2u * (uint32_t) f)) & 0x03030303u);
+                    }
+                }
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+                        c[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[cu][tm], bv[cu][tn], c[tm][tn], 0, 0, 0);
+                }
+                if (f < 3) {
+                    constexpr int VPM = (8 * TN + TM * TN - 1) / (TM * TN);
+#pragma unroll
+                    for (int i = 0; i < TM * TN; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        if (i < TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        }
+        if (++cit == c_iters) {                    // tile ct done: its sums into E set ct % 2
+            uint32_t *mine = reinterpret_cast<uint32_t *>(S + OFF_E + (ct & 1u) * E_SET + kgrp * E_TILE);
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        mine[(16u * (uint32_t) tm + 4u * g + (uint32_t) rr) * EP + wr + 16u * (uint32_t) tn + li] =
+                            (uint32_t) c[tm][tn][rr];
+                    c[tm][tn] = (i32x4v) { 0, 0, 0, 0 };
+                }
+            pend = true;
+            cit = 0;
+            if (++ct < nt) {
+                c_nsup = __builtin_amdgcn_readfirstlane(R[ct].k) / 256u;
+                c_iters = (c_nsup + SS - 1) / SS;
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __syncthreads();
+    if (pend) store_tile(ct - 1);
+    wait_vmem<0>();                                // no copy may land after the workgroup leaves
+}
+
 } // namespace
 
 // ---------------------------------------------------------------------------
@@ -1367,6 +1720,10 @@ extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_tdk4x2(gemm_table T) { gemm_dl_table<4, 2, 4, 2>(T); }
 extern "C" __global__ void __launch_bounds__(512)
 sllm_k_gemm_tdk4x4(gemm_table T) { gemm_dl_table<4, 4, 4, 2>(T); }
+
+// a plan of a few tokens as one stream per workgroup (16 x 128 tiles)
+extern "C" __global__ void __launch_bounds__(GS_THREADS)
+sllm_k_gemm_s1(gemm_stream P) { gemm_stream_body<4>(P); }
 
 // ---------------------------------------------------------------------------
 // calibration kernels: a plain copy and a read-only checksum of known size,

@@ -166,13 +166,15 @@ def test_gemm_refuses_bad_arguments(amd, dev):
 
 
 @pytest.mark.parametrize("tile", [0, 6, 7, 10, 11, 13])
-@pytest.mark.parametrize("m", [1, 4, 16, 17, 64, 100])
+@pytest.mark.parametrize("m", [1, 3, 4, 16, 17, 64, 100])
 def test_gemm_plan_over_many_tensors(amd, orc, dev, tile, m):
-    """A GEMM plan of six tensors with their own K (2560 and 6912), token
+    """A GEMM plan of seven tensors with their own K (2560 and 6912), token
     rows and outputs, one launch: each job's dots and outputs are the single
     sllm_gfx950_gemm's for it, and the oracle's on the first and last token;
-    the automatic tile (0) and every plan tile forced, from one token up."""
-    shapes = [(640, 2560), (2560, 6912), (384, 2560), (128, 6912), (2560, 2560), (64, 2560)]
+    the automatic tile (0: the stream up to four tokens) and every plan tile
+    forced, from one token up. Rows 90 (not a multiple of four) take the
+    element-wise stores."""
+    shapes = [(640, 2560), (2560, 6912), (384, 2560), (128, 6912), (2560, 2560), (64, 2560), (90, 2560)]
     ws = [amd.synth_i2s(amd.synth_seed(8, j, r, k), r, k) for j, (r, k) in enumerate(shapes)]
     xs = [np.concatenate([amd.synth_normal(amd.synth_seed(8, j, t, 3000), k) for t in range(m)]).astype(np.float32)
           for j, (r, k) in enumerate(shapes)]
