@@ -32,7 +32,7 @@
 typedef struct k_dec_step {
     int32_t        token, pos, next, advance;
     uint64_t       reserved0;
-    uint32_t       lm_next, err;
+    uint32_t       reserved1, err;
     const int32_t *feed;
     int32_t       *gen;
     int32_t        n_feed, i_feed, n_gen, cap_gen;
@@ -454,7 +454,9 @@ int sllm_gfx950_ctx_new(const sllm_gfx950_model *m, int32_t n_ctx, sllm_gfx950_c
     c->sc_stride = sc_stride;
     const uint32_t n_pass = (uint32_t) ((m->n_vocab + LM_ROWS - 1) / LM_ROWS);
     const uint32_t lm_cap = (uint32_t) (sllm_shim_cu() > 0 ? sllm_shim_cu() : 256) * LM_WG_PER_CU;
-    const uint32_t lm_wg = n_pass < lm_cap ? n_pass : lm_cap;
+    /* passes dealt round-robin: as many workgroups as give every one the
+     * same number of passes (but the last few, one fewer) */
+    const uint32_t lm_per = (n_pass + lm_cap - 1) / lm_cap, lm_wg = (n_pass + lm_per - 1) / lm_per;
     const size_t sizes[] = {
         c->kv_per_layer * (size_t) m->n_layer * 4,          /* k cache */
         c->kv_per_layer * (size_t) m->n_layer * 4,          /* v cache */

@@ -40,7 +40,7 @@ struct dec_step {
     int32_t        next;        // argmax of the last logits
     int32_t        advance;     // nonzero: the step moves on by itself (greedy loop)
     uint64_t       reserved0;
-    uint32_t       lm_next;     // output passes handed out past the grid's first ones (reset per token)
+    uint32_t       reserved1;
     uint32_t       err;
     const int32_t *feed;        // prompt tokens still to consume: feed[i_feed .. n_feed)
     int32_t       *gen;         // generated tokens
@@ -1207,7 +1207,7 @@ struct dec_lm {
     const uint16_t *embd;        // [n_vocab][n_embd] f16, the tied output projection
     float          *logits;
     uint64_t       *partial;     // one argmax key per workgroup
-    dec_step       *step;        // its lm_next: the pass counter
+    dec_step       *step;
     float           eps;
     uint32_t        n_embd, n_vocab, pad;
 };
@@ -1238,15 +1238,15 @@ __device__ __forceinline__ uint64_t argmax_key(float s, uint32_t row) {
 // elements from its own load and step 2i' + 1's from lane j + 4 (a DPP
 // row shift), so each accumulator still sees its steps in order; lanes 4..7
 // only load.
-// Passes of 32 rows: workgroup w takes pass w first, then passes handed out
-// in order by an atomic counter (the step record's lm_next, which the argmax
-// kernel and the host reset for every token), so that workgroups that stream
-// faster take more passes. Each lane streams its rows in batches of eight
-// 16-byte loads with the next batch always in flight -- across a pass
-// boundary too: the next pass's number is taken a whole pass ahead. The
-// final residual and the norm weight are loaded before the first batch, so
-// that the norm does not wait behind the weight stream (loads complete in
-// order).
+// Passes of 32 rows: workgroup w takes passes w, w + grid, w + 2 grid, ...;
+// the host sizes the grid so that every workgroup has the same number of
+// passes but the last few, which have one fewer (4008 passes over 501
+// workgroups at 2B: eight each). Passes handed out by an atomic counter
+// measured 1 % slower per token: the counter's atomics queue up. Each lane
+// streams its rows in batches of eight 16-byte loads with the next batch
+// always in flight, across a pass boundary too. The final residual and the
+// norm weight are loaded before the first batch, so that the norm does not
+// wait behind the weight stream (loads complete in order).
 constexpr int LM_XV = (int) (LM_MAX_E / 4 / LM_THREADS);   // float4 of the residual per thread
 
 extern "C" __global__ void __launch_bounds__(LM_THREADS)
@@ -1254,11 +1254,9 @@ sllm_k_dec_lm_head(dec_lm L) {
     __shared__ __attribute__((aligned(16))) float xn[LM_MAX_E];
     __shared__ double red_d[LM_THREADS / 64], lane_d[4];
     __shared__ uint64_t red_k[LM_THREADS / 64];
-    __shared__ uint32_t s_next;
     const uint32_t e = L.n_embd, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t j = lane % 8, steps = e / 32, pairs = (steps + 1) / 2, nb = (pairs + LM_UNROLL - 1) / LM_UNROLL;
     const uint32_t n_pass = (L.n_vocab + LM_ROWS - 1) / LM_ROWS;
-    uint32_t *next_ctr = &L.step->lm_next;
 
     // (1) the final residual and the norm weight, then the first batch
     f32x4 av[LM_XV], bv[LM_XV], wv[LM_XV];
@@ -1283,8 +1281,6 @@ sllm_k_dec_lm_head(dec_lm L) {
     u32x4 ha[LM_UNROLL], hb[LM_UNROLL];
     uint32_t p = blockIdx.x;
     if (p < n_pass) load(p, 0, ha);
-    uint32_t grabbed = 0;                                    // thread 0: the counter's value, used a pass later
-    if (tid == 0 && p < n_pass) grabbed = atomicAdd(next_ctr, 1u);
 
     // (2) RMSNorm of a + b into LDS
     double part = 0.0;
@@ -1310,11 +1306,8 @@ sllm_k_dec_lm_head(dec_lm L) {
             *reinterpret_cast<f32x4 *>(xn + i) = x;
         }
     }
-    if (tid == 0) s_next = gridDim.x + grabbed;
-    __syncthreads();
-    uint32_t pn = s_next;                                   // the pass after p
-    __syncthreads();
-    if (tid == 0 && pn < n_pass) grabbed = atomicAdd(next_ctr, 1u);
+    __syncthreads();                                        // xn complete
+    uint32_t pn = p + gridDim.x;                            // the pass after p
 
     uint64_t best = 0;
     float acc[8];
@@ -1369,13 +1362,7 @@ sllm_k_dec_lm_head(dec_lm L) {
         ++it;
         p = p2;
         b = b2;
-        if (b == 0 && p < n_pass) {                       // entered pass p: learn the one after it
-            if (tid == 0) s_next = gridDim.x + grabbed;
-            __syncthreads();
-            pn = s_next;
-            __syncthreads();
-            if (tid == 0 && pn < n_pass) grabbed = atomicAdd(next_ctr, 1u);
-        }
+        if (b == 0) pn = p + gridDim.x;                   // entered pass p
     }
 
     best = wave_max_u64(best);
@@ -1407,7 +1394,6 @@ sllm_k_dec_argmax(const uint64_t *__restrict__ partial, uint32_t n, const float 
     int32_t next = best == 0 ? 0 : (int32_t) (0xffffffffu - (uint32_t) best);
     if (__builtin_isnan(logits[0])) next = 0;
     st->next = next;
-    st->lm_next = 0;                                      // the next output pass counter starts over
     if (st->advance) {
         if (st->i_feed < st->n_feed) {
             st->token = st->feed[st->i_feed];
