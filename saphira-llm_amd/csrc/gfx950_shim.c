@@ -1307,12 +1307,11 @@ typedef struct k_gemm_srec {
 typedef struct k_gemm_stream {
     const k_gemm_srec *recs;
     const uint32_t    *range;
-    const void        *pad0;
     uint32_t           m, gy, n_ranges, pad;
 } k_gemm_stream;
 
 _Static_assert(sizeof(k_gemm_srec) == 64, "k_gemm_srec must match gemm_srec in i2s_kernels.hip");
-_Static_assert(sizeof(k_gemm_stream) == 40, "k_gemm_stream must match gemm_stream in i2s_kernels.hip");
+_Static_assert(sizeof(k_gemm_stream) == 32, "k_gemm_stream must match gemm_stream in i2s_kernels.hip");
 
 #define GS_ROWS 128u          /* rows per streamed tile */
 #define GS_STEPS 2u           /* 256-k super-steps per iteration */
@@ -1426,7 +1425,7 @@ static int gemm_plan_stream(const sllm_gfx950_gemm_plan_job *jobs, size_t n_jobs
     }
     const uint32_t gy = (uint32_t) ((m + 15) / 16);    /* 16 tokens per token tile */
     const uint32_t *range = (const uint32_t *) (p->tables_dev + (size_t) n_tiles * sizeof(k_gemm_srec));
-    p->stream = (k_gemm_stream) { (const k_gemm_srec *) p->tables_dev, range, NULL, (uint32_t) m, gy, n_runs, 0 };
+    p->stream = (k_gemm_stream) { (const k_gemm_srec *) p->tables_dev, range, (uint32_t) m, gy, n_runs, 0 };
     p->gx = 8u * gy * ((n_runs + 7u) / 8u);
     p->gy = 1;
     p->kind = 5;

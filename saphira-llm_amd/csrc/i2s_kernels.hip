@@ -1151,10 +1151,9 @@ static_assert(sizeof(gemm_srec) == 64, "gemm_srec must match gfx950_shim.c");
 struct gemm_stream {
     const gemm_srec *recs;     // every tile of the plan, in stream order
     const uint32_t  *range;    // [n_ranges + 1]: run r is recs[range[r] .. range[r + 1])
-    const void      *pad0;
     uint32_t         m, gy, n_ranges, pad;
 };
-static_assert(sizeof(gemm_stream) == 40, "gemm_stream must match gfx950_shim.c");
+static_assert(sizeof(gemm_stream) == 32, "gemm_stream must match gfx950_shim.c");
 
 constexpr uint32_t GS_RMAX = 64;       // tiles per run (the host cuts longer runs)
 constexpr int GS_THREADS = 512;        // two K groups of four waves
