@@ -361,6 +361,31 @@ def test_every_failed_hip_call_returns_hip_error(env):
         assert _sweep(env.L, name, *s, "*", HIP_INVALID_VALUE, HIP) > 0, name
 
 
+def test_streamed_plan_tables_for_many_uneven_tensors(amd, env):
+    """A plan of at most four tokens streams (i2s_kernels.hip: gemm_stream_body):
+    the host cuts its 128-row tiles into runs of about equal iterations, at
+    most 64 tiles a run. 20,000 one-iteration tiles beside 200 tiles of 128
+    iterations make runs that want more than 64 tiles, so the cut is redone
+    with more runs until every run fits; the tables must come out whole (the
+    sanitizer build runs this too) and the plan must run and free cleanly."""
+    L = env.L
+    w_small = env.put(amd.synth_i2s(amd.synth_seed(9, 1, 64, 256), 64, 256))
+    w_big = env.put(amd.synth_i2s(amd.synth_seed(9, 2, 256, 65536), 256, 65536))
+    q, act = env.alloc(4 * 65536), env.alloc(64)
+    out_small, out_big = env.alloc(4 * 4 * 64), env.alloc(4 * 4 * 256)
+    # the big tensors first: the runs after them, cut for about 108
+    # iterations, stop at 64 one-iteration tiles (37 re-cuts, 717 runs)
+    jobs = [amd.GemmPlanJob(w_big, 256, 65536, q, act, out_big, None) for _ in range(100)]
+    jobs += [amd.GemmPlanJob(w_small, 64, 256, q, act, out_small, None) for _ in range(20000)]
+    arr = (amd.GemmPlanJob * len(jobs))(*jobs)
+    p = c_void_p()
+    assert L.sllm_gfx950_gemm_plan_create(arr, len(jobs), 4, byref(p)) == 0, _err(L)
+    try:
+        assert L.sllm_gfx950_gemm_plan_run(p) == 0, _err(L)
+    finally:
+        L.sllm_gfx950_gemm_plan_destroy(p)
+
+
 def test_open_failures_leave_the_library_closed(amd, fake, env):
     """A failed open -- at each of its HIP calls -- returns -61 (or -60 when
     the runtime reports no device), leaves nothing behind and the library
