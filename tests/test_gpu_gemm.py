@@ -218,6 +218,67 @@ def test_gemm_plan_over_many_tensors(amd, orc, dev, tile, m):
             b.free()
 
 
+@pytest.mark.parametrize("m", [1, 3, 4])
+def test_streamed_plan_runs_of_many_tiles(amd, orc, dev, m):
+    """Up to four tokens a plan streams: its 128-row tiles are cut into runs,
+    one per workgroup, and each run keeps one ring of copies going across
+    its tiles' boundaries, storing a tile's outputs during the next tile's
+    first iteration (i2s_kernels.hip: gemm_stream_body). 100 jobs over five
+    shapes -- K = 256, 768, 2560, 6912; rows 130 and 90 not multiples of
+    128, 90 not of 4 -- make 620 tiles on 256 runs, so runs go from one K to
+    another and end on partial tiles. Every job's dots and outputs are the
+    single sllm_gfx950_gemm's for its tensor and tokens, and those the
+    oracle's on the first and last token."""
+    shapes = [(640, 2560), (384, 768), (130, 256), (2560, 6912), (90, 2560)]
+    ws = [amd.synth_i2s(amd.synth_seed(11, j, r, k), r, k) for j, (r, k) in enumerate(shapes)]
+    xs = [np.concatenate([amd.synth_normal(amd.synth_seed(11, j, t, 5000), k) for t in range(m)]).astype(np.float32)
+          for j, (r, k) in enumerate(shapes)]
+    bw = [dev.put(w) for w in ws]
+    bx = [dev.put(x) for x in xs]
+    bq = [dev.alloc(m * k) for r, k in shapes]
+    ba = [dev.alloc(8 * m) for _ in shapes]
+    refs = [(dev.alloc(4 * m * r), dev.alloc(4 * m * r)) for r, k in shapes]
+    n_jobs = 100
+    outs = [(dev.alloc(4 * m * shapes[i % 5][0]), dev.alloc(4 * m * shapes[i % 5][0])) for i in range(n_jobs)]
+    print(f"[streamed plan] m={m}", flush=True)
+    plan = None
+    try:
+        for j, (r, k) in enumerate(shapes):
+            dev.quant_act(bx[j].vp, k, m, bq[j].vp, ba[j].vp)
+            dev.gemm(bw[j].vp, r, k, bq[j].vp, ba[j].vp, m, refs[j][0].vp, refs[j][1].vp)
+        # a third of the jobs write only raw dots, a third only the epilogue
+        jobs = []
+        for i in range(n_jobs):
+            j = i % 5
+            r, k = shapes[j]
+            jobs.append((bw[j].vp, r, k, bq[j].vp, ba[j].vp, None if i % 3 == 0 else outs[i][0].vp,
+                         None if i % 3 == 1 else outs[i][1].vp))
+        plan = dev.gemm_plan(jobs, m)
+        dev.gemm_plan_run(plan)
+        dev.sync()
+        for j, (r, k) in enumerate(shapes):
+            yr = refs[j][0].download(np.float32, m * r).reshape(m, r)
+            dr = refs[j][1].download(np.int32, m * r).reshape(m, r)
+            for t in (0, m - 1):
+                yo, qo, do, so, su = orc.linear(ws[j], r, k, xs[j][t * k:(t + 1) * k])
+                assert np.array_equal(dr[t], do) and np.array_equal(bits(yr[t]), bits(yo)), f"shape {j} token {t}"
+        for i in range(n_jobs):
+            r, k = shapes[i % 5]
+            yr = refs[i % 5][0].download(np.float32, m * r).reshape(m, r)
+            dr = refs[i % 5][1].download(np.int32, m * r).reshape(m, r)
+            if i % 3 != 0:
+                y = outs[i][0].download(np.float32, m * r).reshape(m, r)
+                assert np.array_equal(bits(y), bits(yr)), f"job {i}"
+            if i % 3 != 1:
+                d = outs[i][1].download(np.int32, m * r).reshape(m, r)
+                assert np.array_equal(d, dr), f"job {i}"
+    finally:
+        if plan is not None:
+            dev.gemm_plan_destroy(plan)
+        for b in bw + bx + bq + ba + [b for p in refs + outs for b in p]:
+            b.free()
+
+
 def test_gemm_plan_refuses_bad_jobs(amd, dev):
     lib = amd.lib()
     w = dev.put(amd.synth_i2s(1, 64, 384))
